@@ -1,0 +1,60 @@
+// Internal helpers shared by the gfx950 int8 kernels and the C-ABI layer.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bh {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// Output element types of the dequant epilogue.
+// OUT_I32 stores the raw accumulator (scales and bias unused): the hook the
+// parity tests use to check the integer sums themselves.
+enum OutDtype : int { OUT_F32 = 0, OUT_BF16 = 1, OUT_I32 = 2 };
+
+// f32 -> bf16 bits, round-to-nearest-even on the discarded 16 bits, NaN kept
+// NaN by forcing the top mantissa bit (same rule as the reference's host
+// converter, crates/model/src/half.rs:49-58).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+    uint32_t bits = __float_as_uint(f);
+    if ((bits & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((bits >> 16) | 0x0040u);
+    uint32_t bias = 0x7fffu + ((bits >> 16) & 1u);
+    return (uint16_t)((bits + bias) >> 16);
+}
+
+// The dequant epilogue of matmul_i8_dyn / matmul_i8_gemv: (f32(acc)*sx)*sw,
+// evaluated left to right with no fused multiply-add (the library is built
+// with -ffp-contract=off), then the optional bias add.
+__device__ __forceinline__ float dequant(int acc, float sxm, float swn) {
+    float v = (float)acc * sxm;
+    return v * swn;
+}
+
+template <int OUT>
+__device__ __forceinline__ void store_out(void* out, int64_t idx, float v) {
+    if constexpr (OUT == OUT_F32) {
+        reinterpret_cast<float*>(out)[idx] = v;
+    } else {
+        reinterpret_cast<uint16_t*>(out)[idx] = f32_to_bf16_rne(v);
+    }
+}
+
+// 16 bytes (16 int8 along K) of row `row` starting at byte `kb`, zero beyond
+// `kbytes`. ALIGNED: the row base and kb are 16-byte aligned and kbytes % 16
+// == 0, so one dwordx4 load either lies fully inside the row or fully past it.
+template <bool ALIGNED>
+__device__ __forceinline__ v4i load_k16(const uint8_t* rowp, int kb, int kbytes) {
+    v4i r = {0, 0, 0, 0};
+    if constexpr (ALIGNED) {
+        if (kb < kbytes) r = *reinterpret_cast<const v4i*>(rowp + kb);
+    } else {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(rowp + kb);
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+            if (kb + 4 * d < kbytes) r[d] = (int)p[d];
+    }
+    return r;
+}
+
+}  // namespace bh

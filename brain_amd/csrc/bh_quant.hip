@@ -1,0 +1,177 @@
+// Per-token activation quantization and per-channel weight quantization on gfx950.
+//
+// Reference semantics restated here (paths under the swedishembedded/brain tree):
+//   max_abs_row  crates/kernels/wgsl/max_abs_row.wgsl:27-34 (== max_abs_rows.wgsl:60-84)
+//       sx[m] = max(max_k |x[m,k]|, 1e-8) / 127
+//   quant_pack   crates/kernels/wgsl/quant_pack.wgsl:29-44
+//       inv = 1/sx[m]; q = clamp(round_ties_even(x*inv), -127, 127); 4 bytes per u32, LE along K
+//   quantize_weight crates/model/src/int8.rs:33-59 (host; rounding ties AWAY from zero)
+//
+// `max` is exact, so any reduction order gives the same scale; 1/sx is an
+// IEEE-correct division (the library is built with correctly rounded fp32
+// divide) and x*inv is a single rounded product, so the packed bytes are
+// bit-identical to a serial host evaluation.
+#include "bh_common.h"
+
+namespace bh {
+
+constexpr int QT = 256;  // threads per row block (4 wave64)
+
+// Row max|x| over `k` floats with a block of QT threads. VEC: float4 loads
+// (row base 16-byte aligned, k % 4 == 0).
+template <bool VEC>
+__device__ __forceinline__ float row_absmax(const float* __restrict__ row, int k) {
+    float a = 0.0f;
+    if constexpr (VEC) {
+        const float4* r4 = reinterpret_cast<const float4*>(row);
+        for (int i = threadIdx.x; i < (k >> 2); i += QT) {
+            float4 v = r4[i];
+            a = fmaxf(a, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+    } else {
+        for (int i = threadIdx.x; i < k; i += QT) a = fmaxf(a, fabsf(row[i]));
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
+    __shared__ float red[QT / 64];
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = a;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int w = 1; w < QT / 64; ++w) m = fmaxf(m, red[w]);
+    return m;
+}
+
+__device__ __forceinline__ uint32_t quant_byte(float v, float inv) {
+    float q = rintf(v * inv);                 // ties to even
+    q = fminf(fmaxf(q, -127.0f), 127.0f);
+    return (uint32_t)((int)q & 0xff);
+}
+
+__device__ __forceinline__ uint32_t quant_word(float4 v, float inv) {
+    return quant_byte(v.x, inv) | (quant_byte(v.y, inv) << 8) | (quant_byte(v.z, inv) << 16) |
+           (quant_byte(v.w, inv) << 24);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(QT) void max_abs_rows_kernel(const float* __restrict__ x, int m, int k,
+                                                          float* __restrict__ sx) {
+    const int row = blockIdx.x;
+    if (row >= m) return;
+    float a = row_absmax<VEC>(x + (int64_t)row * k, k);
+    if (threadIdx.x == 0) sx[row] = fmaxf(a, 1e-8f) / 127.0f;
+}
+
+// One thread per packed output word (M*K/4 words), as quant_pack.wgsl.
+template <bool VEC>
+__global__ __launch_bounds__(QT) void quant_pack_kernel(const float* __restrict__ x,
+                                                        const float* __restrict__ sx, int m, int k,
+                                                        uint32_t* __restrict__ xq) {
+    const int kg = k >> 2;
+    const int64_t total = (int64_t)m * kg;
+    for (int64_t idx = (int64_t)blockIdx.x * QT + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * QT) {
+        const int64_t r = idx / kg;
+        const float inv = 1.0f / sx[r];
+        float4 v;
+        if constexpr (VEC) {
+            v = reinterpret_cast<const float4*>(x)[idx];  // row r, group g: floats 4*idx
+        } else {
+            const float* p = x + idx * 4;
+            v = make_float4(p[0], p[1], p[2], p[3]);
+        }
+        xq[idx] = quant_word(v, inv);
+    }
+}
+
+// max_abs_row and quant_pack fused: one block per row, the row is read twice
+// (the second read hits L2), sx written once. Same arithmetic as the pair.
+template <bool VEC>
+__global__ __launch_bounds__(QT) void quantize_rows_kernel(const float* __restrict__ x, int m, int k,
+                                                           float* __restrict__ sx,
+                                                           uint32_t* __restrict__ xq) {
+    const int row = blockIdx.x;
+    if (row >= m) return;
+    const float* xr = x + (int64_t)row * k;
+    float a = row_absmax<VEC>(xr, k);
+    const float s = fmaxf(a, 1e-8f) / 127.0f;
+    if (threadIdx.x == 0) sx[row] = s;
+    const float inv = 1.0f / s;
+    const int kg = k >> 2;
+    uint32_t* q = xq + (int64_t)row * kg;
+    for (int g = threadIdx.x; g < kg; g += QT) {
+        float4 v;
+        if constexpr (VEC) v = reinterpret_cast<const float4*>(xr)[g];
+        else v = make_float4(xr[4 * g], xr[4 * g + 1], xr[4 * g + 2], xr[4 * g + 3]);
+        q[g] = quant_word(v, inv);
+    }
+}
+
+// Per-output-row weight quantization (crates/model/src/int8.rs:33-59):
+// sw = max(max|w|, 1e-8)/127, q = clamp(round_half_away(w*(1/sw)), +-127),
+// NaN -> 0 (Rust's saturating `as i32`).
+__device__ __forceinline__ uint32_t wquant_byte(float v, float inv) {
+    float q = roundf(v * inv);
+    if (q != q) return 0u;
+    q = fminf(fmaxf(q, -127.0f), 127.0f);
+    return (uint32_t)((int)q & 0xff);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(QT) void quantize_weight_kernel(const float* __restrict__ w, int n, int k,
+                                                             uint32_t* __restrict__ packed,
+                                                             float* __restrict__ sw) {
+    const int row = blockIdx.x;
+    if (row >= n) return;
+    const float* wr = w + (int64_t)row * k;
+    float a = row_absmax<VEC>(wr, k);
+    const float s = fmaxf(a, 1e-8f) / 127.0f;
+    if (threadIdx.x == 0) sw[row] = s;
+    const float inv = 1.0f / s;
+    const int kg = k >> 2;
+    uint32_t* q = packed + (int64_t)row * kg;
+    for (int g = threadIdx.x; g < kg; g += QT) {
+        float4 v;
+        if constexpr (VEC) v = reinterpret_cast<const float4*>(wr)[g];
+        else v = make_float4(wr[4 * g], wr[4 * g + 1], wr[4 * g + 2], wr[4 * g + 3]);
+        q[g] = wquant_byte(v.x, inv) | (wquant_byte(v.y, inv) << 8) | (wquant_byte(v.z, inv) << 16) |
+               (wquant_byte(v.w, inv) << 24);
+    }
+}
+
+static inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+hipError_t launch_max_abs_rows(hipStream_t s, const float* x, int m, int k, float* sx) {
+    if (m <= 0) return hipSuccess;
+    const bool vec = (k % 4 == 0) && al16(x);
+    if (vec) max_abs_rows_kernel<true><<<m, QT, 0, s>>>(x, m, k, sx);
+    else max_abs_rows_kernel<false><<<m, QT, 0, s>>>(x, m, k, sx);
+    return hipGetLastError();
+}
+
+hipError_t launch_quant_pack(hipStream_t s, const float* x, const float* sx, int m, int k, uint32_t* xq) {
+    const int64_t total = (int64_t)m * (k / 4);
+    if (total <= 0) return hipSuccess;
+    int64_t blocks = (total + QT - 1) / QT;
+    if (blocks > 65536) blocks = 65536;
+    if (al16(x)) quant_pack_kernel<true><<<(unsigned)blocks, QT, 0, s>>>(x, sx, m, k, xq);
+    else quant_pack_kernel<false><<<(unsigned)blocks, QT, 0, s>>>(x, sx, m, k, xq);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, float* sx, uint32_t* xq) {
+    if (m <= 0) return hipSuccess;
+    if (al16(x)) quantize_rows_kernel<true><<<m, QT, 0, s>>>(x, m, k, sx, xq);
+    else quantize_rows_kernel<false><<<m, QT, 0, s>>>(x, m, k, sx, xq);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_weight(hipStream_t s, const float* w, int n, int k, uint32_t* packed, float* sw) {
+    if (n <= 0) return hipSuccess;
+    if (al16(w)) quantize_weight_kernel<true><<<n, QT, 0, s>>>(w, n, k, packed, sw);
+    else quantize_weight_kernel<false><<<n, QT, 0, s>>>(w, n, k, packed, sw);
+    return hipGetLastError();
+}
+
+}  // namespace bh

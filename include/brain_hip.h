@@ -1,0 +1,267 @@
+/* brain_hip.h — C ABI of the MI355X (gfx950) int8 W8A8 matmul backend.
+ *
+ * Drop-in boundary for the int8 linear path of swedishembedded/brain. The
+ * reference's plugin seam is the generic kernel-dispatch trait
+ * `backend_api::Backend` (crates/backend-api/src/lib.rs:696-908): kernels are
+ * named, dispatched as `step(kind, bufs, params, threads)` and run in order by
+ * `submit`. This header exports
+ *   (1) that trait as plain C functions over opaque handles (section B), so a
+ *       thin Rust `backend-hip` crate can `impl Backend` by forwarding, and
+ *   (2) the same four kernels as typed, stream-ordered calls on caller-owned
+ *       device pointers (section A) for callers that manage memory themselves.
+ *   (3) the host-side int8 helpers the model layer calls (section C).
+ *
+ * Conventions
+ *  - Every function returns an int status: BH_OK (0) or a negative BH_ERR_*;
+ *    bh_last_error() gives a thread-local message. Nothing throws across the ABI.
+ *  - Packed int8 tensors are `uint32_t` words holding 4 int8 values,
+ *    little-endian along K (byte b of word g = element 4g+b). K must be a
+ *    multiple of 4; `kg` = K/4 is the packed word count, as in the reference's
+ *    `[m, kg, n]` matmul params.
+ *  - `stream` is a hipStream_t (NULL = the legacy default stream). Calls in
+ *    section A only enqueue work; they never synchronise.
+ *  - Arithmetic (bit-exact with the reference on the same inputs):
+ *      sx[m]    = max(max_k |x[m,k]|, 1e-8) / 127
+ *      xq[m,k]  = clamp(round_half_even(x[m,k] * (1/sx[m])), -127, 127)
+ *      acc[m,n] = sum_k xq[m,k] * wq[n,k]                  (exact i32)
+ *      out[m,n] = (f32(acc) * sx[m]) * sw[n] [+ bias[n]]   (no FMA; bf16 = RNE)
+ */
+#ifndef BRAIN_HIP_H
+#define BRAIN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BH_ABI_VERSION 1
+
+enum {
+    BH_OK = 0,
+    BH_ERR_INVALID = -1,     /* bad argument, shape or binding */
+    BH_ERR_HIP = -2,         /* HIP runtime error */
+    BH_ERR_UNSUPPORTED = -3, /* kernel name / feature not provided */
+    BH_ERR_NOMEM = -4,       /* device allocation failed */
+    BH_ERR_TIMEOUT = -5      /* bounded wait expired */
+};
+
+/* Output element type of the dequant epilogue. */
+/* BH_OUT_I32 stores the raw i32 accumulators (sx, sw, bias unused) — the
+ * hook for checking the integer sums bit for bit. */
+enum { BH_OUT_F32 = 0, BH_OUT_BF16 = 1, BH_OUT_I32 = 2 };
+
+/* Thread-local description of the last failing call on this thread. */
+const char* bh_last_error(void);
+int bh_abi_version(void);
+
+/* ======================================================================
+ * A. Typed, stream-ordered kernels on caller-owned device memory.
+ * ====================================================================== */
+
+/* Per-token scale. Replaces the `max_abs_row` / `max_abs_rows` dispatch,
+ * bindings [x, sx], params [m, k] (crates/kernels/wgsl/max_abs_row.wgsl:27-34,
+ * max_abs_rows.wgsl:60-84). x: [m,k] f32, sx: [m] f32. */
+int bh_max_abs_rows(void* stream, const float* x, uint32_t m, uint32_t k, float* sx);
+
+/* Quantize + pack. Replaces the `quant_pack` dispatch, bindings [x, sx, xq],
+ * params [m, k] (crates/kernels/wgsl/quant_pack.wgsl:26-45). k % 4 == 0. */
+int bh_quant_pack(void* stream, const float* x, const float* sx, uint32_t m, uint32_t k, uint32_t* xq);
+
+/* max_abs_rows + quant_pack in one launch; bit-identical to the pair.
+ * Replaces the two steps of `model::int8::quant_rows_steps`
+ * (crates/model/src/int8.rs:221-235). */
+int bh_quantize_rows(void* stream, const float* x, uint32_t m, uint32_t k, float* sx, uint32_t* xq);
+
+/* W8A8 matmul, variant chosen by bh_select_i8 (GEMV for m <= 32, MFMA tile
+ * otherwise). Replaces the `matmul_i8_dyn` / `matmul_i8_gemv` dispatches,
+ * bindings [xq, wq, sx, sw, out], params [m, kg, n]
+ * (crates/kernels/wgsl/matmul_i8_dyn.wgsl:50-280, matmul_i8_gemv.wgsl:39-76)
+ * and the selection in crates/model/src/ops.rs:667-730.
+ * xq [m,kg] u32, wq [n,kg] u32, sx [m] f32, sw [n] f32, bias [n] f32 or NULL
+ * (the reference adds bias with a separate `bias_add` dispatch; fusing it is
+ * bit-identical because the add happens after the same two products),
+ * out [m,n] f32 (BH_OUT_F32) or bf16 bits (BH_OUT_BF16). */
+int bh_matmul_i8(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
+                 const float* bias, void* out, int out_dtype, uint32_t m, uint32_t kg, uint32_t n);
+
+/* Forced decode variant (crates/kernels/wgsl/matmul_i8_gemv.wgsl:39-76); m <= 32. */
+int bh_matmul_i8_gemv(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
+                      const float* bias, void* out, int out_dtype, uint32_t m, uint32_t kg, uint32_t n);
+
+/* Forced tiled variant (crates/kernels/wgsl/matmul_i8_dyn.wgsl:50-280); any m. */
+int bh_matmul_i8_dyn(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
+                     const float* bias, void* out, int out_dtype, uint32_t m, uint32_t kg, uint32_t n);
+
+/* Static per-tensor scales: out = f32(acc) * (sx*sw). Replaces `matmul_i8`,
+ * bindings [x, w, out], params [m, kg, n, sx_bits, sw_bits]
+ * (crates/kernels/wgsl/matmul_i8.wgsl:49-262). */
+int bh_matmul_i8_static(void* stream, const uint32_t* xq, const uint32_t* wq, float sx, float sw, float* out,
+                        uint32_t m, uint32_t kg, uint32_t n);
+
+/* One whole int8 linear: quantize x [m,k] f32 into the caller's scratch
+ * (sx [m], xq [m,k/4]) and run bh_matmul_i8. The sequence
+ * `Ops::act` + `Ops::matmul` (crates/model/src/ops.rs:574-580, 667-730). */
+int bh_linear_i8(void* stream, const float* x, const uint32_t* wq, const float* sw, const float* bias,
+                 float* sx_scratch, uint32_t* xq_scratch, void* out, int out_dtype, uint32_t m, uint32_t k,
+                 uint32_t n);
+
+/* Per-output-channel weight quantization on the device; bit-identical to
+ * bh_quantize_weight (crates/model/src/int8.rs:33-59). w [n,k] f32 ->
+ * packed [n,k/4] u32, sw [n] f32. */
+int bh_quantize_weight_device(void* stream, const float* w, uint32_t n, uint32_t k, uint32_t* packed, float* sw);
+
+/* Int8 matrix-core roof probe: `blocks` workgroups of 256 threads each run
+ * `iters` dependent-free v_mfma_i32_16x16x64_i8 chains; out[blocks*256] i32
+ * receives a data-dependent sum so nothing folds. Ops executed =
+ * blocks*4*iters*8*32768. The MI355X counterpart of the `roof_dp4a` probe
+ * (crates/kernels/wgsl/roof_dp4a.wgsl:28-63, crates/gpu-core/src/roof.rs:99-130). */
+int bh_roof_mfma_i8(void* stream, uint32_t blocks, uint32_t iters, int32_t* out);
+
+/* ======================================================================
+ * B. backend_api::Backend as a C ABI (crates/backend-api/src/lib.rs:696-908).
+ * ====================================================================== */
+
+typedef struct bh_backend bh_backend; /* `Box<dyn Backend>` */
+typedef struct bh_buffer bh_buffer;   /* `DeviceBuffer` (refcounted, clones alias) */
+typedef struct bh_dispatch bh_dispatch; /* `Step` (refcounted recorded dispatch) */
+
+/* Kernel names this backend executes (the reference's kernel catalogue names,
+ * crates/kernels/src/lib.rs:555-713):
+ *   "max_abs_row", "max_abs_rows"  bindings [x, sx]                    params [m, k]
+ *   "quant_pack"                   bindings [x, sx, xq]                params [m, k]
+ *   "matmul_i8_dyn", "matmul_i8_gemv"
+ *                                  bindings [xq, wq, sx, sw, out]      params [m, kg, n]
+ *   "matmul_i8"                    bindings [x, w, out]                params [m, kg, n, f32 sx, f32 sw]
+ *   "bias_add"                     bindings [out, bias]                params [m, n]
+ *   "roof_dp4a"                    bindings [inp, out]                 params [n, iters, a, b]
+ * `threads` is accepted for signature parity and ignored: each kernel derives
+ * its own grid from its params. */
+
+/* Backend factory (`Factory`, crates/backend-api/src/lib.rs:992-1020).
+ * names[i] (and optionally srcs[i], ignored except for being accepted) is the
+ * kernel set; the returned backend's kernel index i is names[i]. With
+ * flags & BH_CREATE_LENIENT, unknown names are accepted and fail with
+ * BH_ERR_UNSUPPORTED only when dispatched; without it creation fails so the
+ * caller can fall back to another backend. device = HIP device ordinal. */
+#define BH_CREATE_LENIENT 1u
+int bh_backend_create(const char* const* names, const char* const* srcs, uint32_t n_kernels, int device,
+                      uint32_t flags, bh_backend** out);
+void bh_backend_destroy(bh_backend* be);
+/* `kind()`: "hip". */
+const char* bh_backend_kind(const bh_backend* be);
+/* Index of `name` in the creation list, or -1 (`Gpu::kernel_index`, crates/gpu-core/src/lib.rs:796). */
+int bh_kernel_index(const bh_backend* be, const char* name);
+/* The backend's HIP stream (hipStream_t) — steps run on it in submit order. */
+void* bh_backend_stream(const bh_backend* be);
+
+/* `DeviceCaps` + `NumericSupport` (crates/backend-api/src/lib.rs:177-213, 471-507). */
+typedef struct {
+    uint32_t compute_units;
+    uint32_t max_workgroup_size;
+    uint32_t workgroup_mem_bytes;
+    uint32_t subgroup_size;
+    uint32_t unified_memory;
+    uint32_t workgroup_reductions; /* 1: cooperative (GEMV) variants are valid */
+    float peak_bandwidth_gbs;      /* 0 = unmeasured */
+    float peak_gflops;             /* 0 = unmeasured */
+    uint32_t numeric_f32, numeric_int8_dot, numeric_f16, numeric_bf16;
+    uint32_t numeric_f16_storage, numeric_bf16_storage, numeric_coop_matrix;
+    uint64_t max_buffer_bytes;
+    uint64_t max_storage_binding_bytes;
+    char device_name[64];
+} bh_caps_t;
+int bh_caps(const bh_backend* be, bh_caps_t* caps);
+
+/* `storage(n)`: n zeroed f32 words. */
+int bh_storage(bh_backend* be, uint64_t n_words, bh_buffer** out);
+/* `storage_init(name, data)`. */
+int bh_storage_init(bh_backend* be, const char* label, const float* data, uint64_t n_words, bh_buffer** out);
+bh_buffer* bh_buffer_retain(bh_buffer* b); /* DeviceBuffer::clone */
+void bh_buffer_release(bh_buffer* b);      /* drop; memory freed on the last release */
+uint64_t bh_buffer_words(const bh_buffer* b);
+void* bh_buffer_device_ptr(const bh_buffer* b);
+/* `write` / `write_at` (crates/backend-api/src/lib.rs:704-721): ordered after prior submits. */
+int bh_write(bh_backend* be, bh_buffer* buf, const uint32_t* data, uint64_t n_words);
+int bh_write_at(bh_backend* be, bh_buffer* buf, uint64_t offset_words, const uint32_t* data, uint64_t n_words);
+/* `read(buf, n)`: blocks, copies the first n words back (as raw 32-bit words). */
+int bh_read(bh_backend* be, const bh_buffer* buf, void* dst, uint64_t n_words);
+
+/* `step(kind, bufs, params, threads)`. */
+int bh_step(bh_backend* be, uint32_t kind, bh_buffer* const* bufs, uint32_t nbufs, const uint32_t* params,
+            uint32_t nparams, uint32_t threads, bh_dispatch** out);
+/* `step_sliced`: offsets holds nbufs (offset, len) pairs in 4-byte WORDS,
+ * len 0 = to the end of the buffer (crates/backend-api/src/lib.rs:723-731;
+ * the words-not-bytes convention of crates/model/src/int8.rs:208-220).
+ * Every binding is bounds-checked against what the kernel will touch. */
+int bh_step_sliced(bh_backend* be, uint32_t kind, bh_buffer* const* bufs, const uint64_t* offsets,
+                   uint32_t nbufs, const uint32_t* params, uint32_t nparams, uint32_t threads, bh_dispatch** out);
+bh_dispatch* bh_step_retain(bh_dispatch* s);
+void bh_step_release(bh_dispatch* s);
+/* `submit(clears, steps)`: zero `clears`, then enqueue every step in order. */
+int bh_submit(bh_backend* be, bh_buffer* const* clears, uint32_t nclears, bh_dispatch* const* steps, uint32_t nsteps);
+int bh_flush(bh_backend* be);
+int bh_poll_wait(bh_backend* be);
+/* `poll_wait_timeout`: BH_OK if idle within timeout_ms, BH_ERR_TIMEOUT otherwise. */
+int bh_poll_wait_timeout(bh_backend* be, uint32_t timeout_ms);
+
+/* Per-kernel device timing (`set_kernel_timing` / `kernel_times` /
+ * `reset_kernel_times`, crates/backend-api/src/lib.rs:888-907; enabled at
+ * creation when BRAIN_PROFILE is set and not "0", lib.rs:917-919). */
+typedef struct {
+    char name[48];
+    double ms;
+    uint64_t calls;
+} bh_kernel_time_t;
+int bh_set_kernel_timing(bh_backend* be, int on); /* returns 1 if timing is now on */
+/* Writes up to cap entries; returns the number of kernels with calls > 0 (or <0 on error). */
+int bh_kernel_times(bh_backend* be, bh_kernel_time_t* out, uint32_t cap);
+void bh_reset_kernel_times(bh_backend* be);
+
+/* `DeviceStats` (crates/backend-api/src/lib.rs:924-931). */
+typedef struct {
+    uint64_t submits, dispatches, readbacks, bind_groups, uniform_allocs;
+} bh_stats_t;
+int bh_stats(const bh_backend* be, bh_stats_t* st);
+
+/* ======================================================================
+ * C. Host-side int8 helpers of the model layer.
+ * ====================================================================== */
+
+/* crates/model/src/int8.rs:33-59 — row-parallel host quantizer (ties AWAY). */
+int bh_quantize_weight(const float* w, uint64_t n, uint64_t k, uint32_t* packed, float* sw);
+/* crates/model/src/int8.rs:70-87 */
+int bh_dequantize_weight(const uint32_t* packed, const float* sw, uint64_t n, uint64_t k, float* w);
+
+/* `model::int8::quant_rows_steps` (crates/model/src/int8.rs:221-235): the
+ * max_abs_row -> quant_pack steps for rows r0..r1 of x [.., k], with x/xq
+ * offset in their own elements and sx in rows. r0 % 64 == 0 as in the
+ * reference. kernels = {max_abs_row index, quant_pack index}. */
+int bh_quant_rows_steps(bh_backend* be, const uint32_t kernels[2], bh_buffer* x, bh_buffer* sx, bh_buffer* xq,
+                        uint32_t r0, uint32_t r1, uint32_t k, bh_dispatch* out[2]);
+
+/* `model::dispatch::mm8_rows_off` (crates/model/src/dispatch.rs:119-130):
+ * rows xr0..xr0+m of the packed activation -> m*n floats of o at ooff. */
+int bh_mm8_rows_off(bh_backend* be, uint32_t kind, bh_buffer* xq, bh_buffer* wq, bh_buffer* sx, bh_buffer* sw,
+                    bh_buffer* o, uint32_t xr0, uint64_t ooff, uint32_t m, uint32_t k, uint32_t n, bh_dispatch** out);
+
+/* `backend_api::select::candidates` I8 arm (crates/backend-api/src/select.rs:323-331),
+ * with this backend's crossover. Variant codes: */
+enum { BH_VARIANT_PACKED_INT8 = 1, BH_VARIANT_WORKGROUP_PER_OUTPUT = 2 };
+/* Fills out[0..ret) with candidate variants, best first; returns the count. */
+int bh_select_i8(uint32_t m, uint32_t n, uint32_t k, int int8_dot, int workgroup_reductions, int out[2]);
+/* The kernel name a variant binds to (`Ops::bind`, crates/model/src/ops.rs:603-625). */
+const char* bh_variant_kernel(int variant);
+
+/* `gpu_core::cost` (crates/gpu-core/src/cost.rs:267-275) for the int8 family:
+ * flops, int_ops and bytes of one dispatch of `name` with `params`. */
+typedef struct {
+    uint64_t flops, int_ops, bytes;
+} bh_cost_t;
+int bh_cost(const char* name, const uint32_t* params, uint32_t nparams, bh_cost_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BRAIN_HIP_H */

@@ -1,0 +1,237 @@
+"""HIP kernels vs the CPU oracle on the same seeded inputs (MI355X only).
+
+Bar: bit-exact. Scales and packed activations byte-for-byte; i32 accumulators
+exactly (BH_OUT_I32); f32 outputs bit-for-bit; bf16 outputs equal to the RNE
+of the oracle's f32. Full BASELINE shapes are checked in full where the oracle
+is fast (float64-BLAS exact accumulators) and on a seeded sample of output
+entries otherwise.
+"""
+import numpy as np
+import pytest
+import torch
+
+from brain_amd import ops
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+
+def dev_u32(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(device)
+
+
+def host_u32(t):
+    return t.cpu().numpy().view(np.uint32)
+
+
+def dev_f32(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(device)
+
+
+def bf16_bits(t):
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def special_acts(m, k, seed):
+    x = o.synth_acts(m, k, seed)
+    if m > 1:
+        x[1] = 0.0                               # all-zero row -> sx = 1e-8/127, q = 0
+    if m > 2:
+        x[2, 0] = 1e30                           # one huge outlier
+    if m > 3 and k >= 8:
+        x[3, :8] = [127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5]  # exact ties at sx = 1
+    return x
+
+
+# ---------------------------------------------------------------- quantization
+QUANT_SHAPES = [(1, 4), (1, 1024), (3, 8), (4, 36), (16, 1024), (7, 3072), (64, 4096), (513, 1024), (5, 10240)]
+
+
+@pytest.mark.parametrize("m,k", QUANT_SHAPES)
+def test_quant_kernels_bit_exact(gpu, m, k):
+    x = special_acts(m, k, 100 + m + k)
+    sx_ref = o.max_abs_row(x)
+    xq_ref = o.quant_pack(x, sx_ref)
+    xd = dev_f32(x, gpu)
+    sx = ops.max_abs_rows(xd)
+    assert (sx.cpu().numpy().view(np.uint32) == sx_ref.view(np.uint32)).all()
+    xq = ops.quant_pack(xd, sx)
+    assert (host_u32(xq) == xq_ref).all()
+    sx2, xq2 = ops.quantize_rows(xd)
+    assert (sx2.cpu().numpy().view(np.uint32) == sx_ref.view(np.uint32)).all()
+    assert (host_u32(xq2) == xq_ref).all()
+
+
+def test_quant_ties_at_unit_scale(gpu):
+    x = np.array([[-2.5, -1.5, -0.5, 0.5, 1.5, 2.5, 3.5, 0.0]], np.float32)
+    xq = ops.quant_pack(dev_f32(x, gpu), dev_f32([1.0], gpu))
+    assert o.unpack_i8(host_u32(xq)).tolist() == [[-2, -2, 0, 0, 2, 2, 4, 0]]
+
+
+def test_quant_unaligned_rows_and_odd_k_scale(gpu):
+    # x starting one float into an allocation: the scalar (non-float4) paths.
+    m, k = 6, 132
+    x = special_acts(m, k, 7)
+    base = torch.zeros(m * k + 1, device=gpu)
+    base[1:] = dev_f32(x.reshape(-1), gpu)
+    xv = base[1:].view(m, k)
+    sx_ref = o.max_abs_row(x)
+    sx, xq = ops.quantize_rows(xv)
+    assert (sx.cpu().numpy() == sx_ref).all()
+    assert (host_u32(xq) == o.quant_pack(x, sx_ref)).all()
+    assert (host_u32(ops.quant_pack(xv, sx)) == o.quant_pack(x, sx_ref)).all()
+    # max_abs_row alone accepts any k (no packing)
+    x5 = o.synth_acts(3, 5, 9)
+    assert (ops.max_abs_rows(dev_f32(x5, gpu)).cpu().numpy() == o.max_abs_row(x5)).all()
+
+
+# ---------------------------------------------------------------- matmul helpers
+def run_and_check(gpu, m, k, n, variant, seed, bias=False, sample=None):
+    x = special_acts(m, k, seed)
+    sx = o.max_abs_row(x)
+    xq = o.quant_pack(x, sx)
+    wq, sw = o.synth_weights(n, k, seed + 1)
+    b = o.synth_acts(1, n, seed + 2)[0] if bias else None
+    dx, dw, dsx, dsw = dev_u32(xq, gpu), dev_u32(wq, gpu), dev_f32(sx, gpu), dev_f32(sw, gpu)
+    db = None if b is None else dev_f32(b, gpu)
+    acc_d = ops.matmul_i8(dx, dw, dsx, dsw, None, torch.int32, variant).cpu().numpy()
+    f32_d = ops.matmul_i8(dx, dw, dsx, dsw, db, torch.float32, variant).cpu().numpy()
+    bf_d = bf16_bits(ops.matmul_i8(dx, dw, dsx, dsw, db, torch.bfloat16, variant))
+    if sample is None:
+        rows, cols = np.arange(m), np.arange(n)
+    else:
+        rng = np.random.default_rng(seed)
+        rows = np.unique(np.concatenate([[0, m - 1], rng.integers(0, m, sample)]))
+        cols = np.unique(np.concatenate([[0, n - 1], rng.integers(0, n, sample)]))
+    acc = o.acc_exact(xq, wq, rows, cols)
+    bsub = None if b is None else b[cols]
+    assert (acc_d[np.ix_(rows, cols)] == acc).all(), "i32 accumulators differ"
+    want = o.epilogue(acc, sx[rows], sw[cols], bsub)
+    got = f32_d[np.ix_(rows, cols)]
+    assert (got.view(np.uint32) == want.view(np.uint32)).all(), "f32 outputs differ"
+    wantb = o.epilogue(acc, sx[rows], sw[cols], bsub, "bf16")
+    assert (bf_d[np.ix_(rows, cols)] == wantb).all(), "bf16 outputs differ"
+
+
+# Config 1 (decode GEMV sweep), full size.
+DECODE_KN = [(1024, 3072), (3072, 1024), (1024, 2048), (1024, 151936)]
+
+
+@pytest.mark.parametrize("k,n", DECODE_KN)
+@pytest.mark.parametrize("m", [1, 4, 8, 16])
+def test_gemv_decode_sweep_full(gpu, m, k, n):
+    run_and_check(gpu, m, k, n, "gemv", seed=m * 7 + k + n, bias=(m == 4))
+
+
+@pytest.mark.parametrize("m,k,n", [(17, 1024, 300), (32, 512, 257), (2, 8, 3), (6, 24, 13), (5, 36, 33),
+                                   (1, 4, 1), (31, 132, 70), (3, 2048 + 64, 100)])
+def test_gemv_edges(gpu, m, k, n):
+    run_and_check(gpu, m, k, n, "gemv", seed=m + k + n, bias=True)
+
+
+# Config 2 (prefill sweep): full check at M=512, sampled at larger M.
+PREFILL_KN = [(1024, 3072), (3072, 1024), (4096, 11008), (4096, 4096)]
+
+
+@pytest.mark.parametrize("k,n", PREFILL_KN)
+def test_gemm_prefill_m512_full(gpu, k, n):
+    run_and_check(gpu, 512, k, n, "dyn", seed=k + n, bias=True)
+
+
+@pytest.mark.parametrize("k,n", PREFILL_KN)
+@pytest.mark.parametrize("m", [2048, 8192])
+def test_gemm_prefill_sampled(gpu, m, k, n):
+    run_and_check(gpu, m, k, n, "dyn", seed=m + k + n, bias=True, sample=300)
+
+
+@pytest.mark.parametrize("m,k,n", [(37, 24, 41), (33, 132, 17), (1, 4, 1), (130, 64, 257), (128, 1024, 128),
+                                   (255, 520, 129), (64, 8, 300), (1152, 3840, 384)])
+def test_gemm_edges(gpu, m, k, n):
+    run_and_check(gpu, m, k, n, "dyn", seed=m * 3 + k + n, bias=True)
+
+
+def test_auto_variant_and_gemv_equals_gemm(gpu):
+    for m in (1, 16, 32, 33, 64):
+        run_and_check(gpu, m, 1024, 640, "auto", seed=m)
+    x = special_acts(24, 512, 5)
+    sx = o.max_abs_row(x)
+    xq = o.quant_pack(x, sx)
+    wq, sw = o.synth_weights(200, 512, 6)
+    args = [dev_u32(xq, gpu), dev_u32(wq, gpu), dev_f32(sx, gpu), dev_f32(sw, gpu)]
+    a = ops.matmul_i8(*args, variant="gemv").cpu().numpy()
+    b = ops.matmul_i8(*args, variant="dyn").cpu().numpy()
+    assert (a.view(np.uint32) == b.view(np.uint32)).all()
+
+
+def test_matmul_unaligned_operands(gpu):
+    # Packed operands starting one word into their allocations (step_sliced
+    # word offsets make this legal) take the dword-load path.
+    m, k, n = 40, 256, 96
+    x = special_acts(m, k, 3)
+    sx = o.max_abs_row(x)
+    xq = o.quant_pack(x, sx)
+    wq, sw = o.synth_weights(n, k, 4)
+    xb = torch.zeros(m * k // 4 + 1, dtype=torch.int32, device=gpu)
+    wb = torch.zeros(n * k // 4 + 1, dtype=torch.int32, device=gpu)
+    xb[1:] = dev_u32(xq.reshape(-1), gpu)
+    wb[1:] = dev_u32(wq.reshape(-1), gpu)
+    want = o.epilogue(o.acc_exact(xq, wq), sx, sw)
+    for variant, mm in (("gemv", 32), ("dyn", m)):
+        got = ops.matmul_i8(xb[1:].view(m, k // 4)[:mm], wb[1:].view(n, k // 4), dev_f32(sx[:mm], gpu),
+                            dev_f32(sw, gpu), variant=variant).cpu().numpy()
+        assert (got.view(np.uint32) == want[:mm].view(np.uint32)).all(), variant
+
+
+def test_matmul_k_zero_and_empty(gpu):
+    sx = dev_f32([0.5, 0.25], gpu)
+    sw = dev_f32([1.0, 2.0, 3.0], gpu)
+    bias = dev_f32([1.0, -2.0, 0.5], gpu)
+    xq = torch.zeros(2, 0, dtype=torch.int32, device=gpu)
+    wq = torch.zeros(3, 0, dtype=torch.int32, device=gpu)
+    for variant in ("gemv", "dyn"):
+        out = ops.matmul_i8(xq, wq, sx, sw, bias, variant=variant).cpu().numpy()
+        assert out.tolist() == [[1.0, -2.0, 0.5]] * 2
+    empty = ops.matmul_i8(torch.zeros(0, 4, dtype=torch.int32, device=gpu), torch.zeros(3, 4, dtype=torch.int32,
+                          device=gpu), torch.zeros(0, device=gpu), sw)
+    assert empty.shape == (0, 3)
+
+
+def test_gemv_rejects_more_than_32_rows(gpu):
+    from brain_amd import BrainHipError
+    xq = torch.zeros(33, 4, dtype=torch.int32, device=gpu)
+    with pytest.raises(BrainHipError, match="m=33"):
+        ops.matmul_i8(xq, xq[:5], torch.ones(33, device=gpu), torch.ones(5, device=gpu), variant="gemv")
+
+
+def test_static_scale_matmul(gpu):
+    m, k, n = 70, 264, 150
+    xq = o.quant_pack(o.synth_acts(m, k, 1), np.full(m, 0.02, np.float32))
+    wq, _ = o.synth_weights(n, k, 2)
+    sx, sw = np.float32(0.0123), np.float32(0.0071)
+    got = ops.matmul_i8_static(dev_u32(xq, gpu), dev_u32(wq, gpu), sx, sw).cpu().numpy()
+    want = o.epilogue_static(o.acc_exact(xq, wq), sx, sw)
+    assert (got.view(np.uint32) == want.view(np.uint32)).all()
+
+
+def test_linear_config0(gpu):
+    # Config 0: M=16, K=1024, N=3072, f32 activations quantized in-path, f32 out.
+    m, k, n = 16, 1024, 3072
+    x = o.synth_acts(m, k, 0)
+    wq, sw = o.synth_weights(n, k, 1)
+    got = ops.linear_i8(dev_f32(x, gpu), dev_u32(wq, gpu), dev_f32(sw, gpu)).cpu().numpy()
+    sx = o.max_abs_row(x)
+    want = o.matmul_i8(o.quant_pack(x, sx), wq, sx, sw)
+    assert (got.view(np.uint32) == want.view(np.uint32)).all()
+    assert (o.cpu_linear_gemv(x, wq, sw, 4).view(np.uint32) == want.view(np.uint32)).all()
+
+
+@pytest.mark.parametrize("n,k", [(1, 64), (3, 8), (17, 24), (64, 4096), (129, 128), (300, 1000)])
+def test_device_weight_quantizer(gpu, n, k):
+    rng = np.random.default_rng(n + k)
+    w = (rng.standard_normal((n, k)) * rng.uniform(0.1, 10, (n, 1))).astype(np.float32)
+    w[0, :4] = [0.5, -0.5, 1.5, -2.5]
+    w[-1, :4] = [127.0, 0.5, 1.5, 2.5] if n > 1 else w[-1, :4]
+    packed, sw = ops.quantize_weight_device(dev_f32(w, gpu))
+    wp, wsw = o.quantize_weight(w)
+    assert (host_u32(packed) == wp).all()
+    assert (sw.cpu().numpy() == wsw).all()
