@@ -1,0 +1,330 @@
+"""Benchmark of the int8 W8A8 linear on one MI355X.
+
+Headline workload (the decode GEMV sweep): one step =
+one int8 linear (per-token activation quantization + GEMV, bf16 out) for
+every M in {1,4,8,16} x (K,N) in {(1024,3072),(3072,1024),(1024,2048),
+(1024,151936)}: 16 linears. Every linear owns its own weight copy (656 MB in
+total), so a weight is re-read only after >256 MB of other traffic and comes
+from HBM, not the Infinity Cache.
+
+  value    = algorithmic bytes of the 16 linears / wall time per step (GB/s),
+             bytes per linear = N*K + 4N + 4*M*K + 2*M*N
+  roofline = the GEMV kernel alone: its algorithmic bytes (N*K + 4N + M*K + 2*M*N)
+             / its average launch duration, timed with HIP events on the stream
+             it runs on, vs 8 TB/s
+Also reported: the prefill GEMM sweep in TOPS vs the 5.0 POPS int8
+dense MFMA peak, an MFMA roof probe, and the CPU baseline (the restated
+backend-cpu decode path, OpenMP, timed on this host on a bounded sample).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+DECODE_M = [1, 4, 8, 16]
+DECODE_KN = [(1024, 3072), (3072, 1024), (1024, 2048), (1024, 151936)]
+PREFILL_M = [512, 2048, 8192]
+PREFILL_KN = [(1024, 3072), (3072, 1024), (4096, 11008), (4096, 4096)]
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--prefill-reps", type=int, default=10)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on CPU-baseline work")
+    ap.add_argument("--only", default="", help="profiling aid: 'decode' or 'prefill' only")
+    return ap.parse_args()
+
+
+def gemv_bytes(m, k, n):
+    return n * k + 4 * n + m * k + 2 * m * n
+
+
+def linear_bytes(m, k, n):
+    return n * k + 4 * n + 4 * m * k + 2 * m * n
+
+
+def make_decode_set(torch, dev, gen):
+    sets = []
+    for m in DECODE_M:
+        for k, n in DECODE_KN:
+            w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev, generator=gen)
+            sw = torch.empty(n, device=dev).uniform_(0.002, 0.02, generator=gen)
+            x = torch.randn(m, k, device=dev, generator=gen)
+            sets.append(dict(m=m, k=k, n=n, wq=w.view(torch.int32), sw=sw, x=x,
+                             sx=torch.empty(m, device=dev), xq=torch.empty(m, k // 4, dtype=torch.int32, device=dev),
+                             out=torch.empty(m, n, dtype=torch.bfloat16, device=dev)))
+    return sets
+
+
+def check_sample(torch, s, out_dtype):
+    """Correctness gate before timing: sampled outputs vs the oracle."""
+    import numpy as np
+    from oracle import oracle as o
+
+    x = s["x"].cpu().numpy()
+    sx = o.max_abs_row(x)
+    xq = o.quant_pack(x, sx)
+    assert (s["sx"].cpu().numpy() == sx).all()
+    cols = np.unique(np.random.default_rng(0).integers(0, s["n"], 256))
+    wq = s["wq"][torch.from_numpy(cols).to(s["wq"].device)].cpu().numpy().view(np.uint32)
+    sw = s["sw"].cpu().numpy()[cols]
+    want = o.epilogue(o.acc_exact(xq, wq), sx, sw, None, out_dtype)
+    got = s["out"].cpu()
+    got = (got.view(torch.int16).numpy().view(np.uint16) if out_dtype == "bf16" else got.numpy())[:, cols]
+    assert (got == want).all(), f"bench correctness gate failed at m={s['m']} k={s['k']} n={s['n']}"
+
+
+def bench_decode(torch, lib, sets, steps, warmup):
+    from brain_amd._lib import BH_OUT_BF16, check
+
+    def linear(s):
+        sp = torch.cuda.current_stream().cuda_stream
+        check(lib.bh_quantize_rows(sp, s["x"].data_ptr(), s["m"], s["k"], s["sx"].data_ptr(), s["xq"].data_ptr()))
+
+    def gemv(s):
+        sp = torch.cuda.current_stream().cuda_stream
+        check(lib.bh_matmul_i8_gemv(sp, s["xq"].data_ptr(), s["wq"].data_ptr(), s["sx"].data_ptr(),
+                                    s["sw"].data_ptr(), None, s["out"].data_ptr(), BH_OUT_BF16, s["m"],
+                                    s["k"] // 4, s["n"]))
+
+    def step():
+        for s in sets:
+            linear(s)
+            gemv(s)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    for s in sets:
+        check_sample(torch, s, "bf16")
+
+    # One step = 32 launches; the step is captured once as a HIP graph so the
+    # timed loop measures the GPU, not Python's launch rate.
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for s in sets:
+        s["out"].zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    for s in sets:
+        check_sample(torch, s, "bf16")
+
+    stream = torch.cuda.current_stream()
+    # Timed region: K graph replays, events at both ends.
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_ms = e0.elapsed_time(e1) / steps
+    for s in sets:
+        check_sample(torch, s, "bf16")
+
+    # Per-launch GEMV durations (events around each GEMV on the same stream),
+    # in a separate pass so the events do not perturb the step timing.
+    evs = []
+    for _ in range(max(3, steps // 5)):
+        for i, s in enumerate(sets):
+            linear(s)
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            gemv(s)
+            b.record(stream)
+            evs.append((i, a, b))
+    torch.cuda.synchronize()
+    per = {}
+    for i, a, b in evs:
+        per.setdefault(i, []).append(a.elapsed_time(b))
+    shapes = []
+    for i, s in enumerate(sets):
+        us = 1e3 * sorted(per[i])[len(per[i]) // 2]
+        shapes.append(dict(m=s["m"], k=s["k"], n=s["n"], gemv_us=round(us, 2),
+                           gemv_gbs=round(gemv_bytes(s["m"], s["k"], s["n"]) / us / 1e3, 1)))
+    mean_us = sum(sum(v) for v in per.values()) / sum(len(v) for v in per.values()) * 1e3
+    mean_bytes = sum(gemv_bytes(s["m"], s["k"], s["n"]) for s in sets) / len(sets)
+    step_bytes = sum(linear_bytes(s["m"], s["k"], s["n"]) for s in sets)
+    return dict(step_ms=step_ms, wall=wall, step_bytes=step_bytes, gemv_mean_us=mean_us,
+                gemv_mean_bytes=mean_bytes, shapes=shapes)
+
+
+def bench_prefill(torch, lib, dev, gen, reps):
+    from brain_amd._lib import BH_OUT_BF16, check
+
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    rows = []
+    for m in PREFILL_M:
+        for k, n in PREFILL_KN:
+            xq = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=dev, generator=gen).view(torch.int32)
+            wq = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev, generator=gen).view(torch.int32)
+            sx = torch.empty(m, device=dev).uniform_(0.001, 0.05, generator=gen)
+            sw = torch.empty(n, device=dev).uniform_(0.002, 0.02, generator=gen)
+            bias = torch.randn(n, device=dev, generator=gen)
+            out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+
+            def run():
+                check(lib.bh_matmul_i8_dyn(sp, xq.data_ptr(), wq.data_ptr(), sx.data_ptr(), sw.data_ptr(),
+                                           bias.data_ptr(), out.data_ptr(), BH_OUT_BF16, m, k // 4, n))
+
+            run()
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(reps):
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                run()
+                b.record(stream)
+                ts.append((a, b))
+            torch.cuda.synchronize()
+            us = 1e3 * sorted(a.elapsed_time(b) for a, b in ts)[reps // 2]
+            ops = 2.0 * m * n * k
+            byts = m * k + n * k + 2 * m * n + 4 * m + 8 * n
+            tops = ops / us / 1e6
+            bound = min(INT8_PEAK_TOPS, HBM_PEAK_GBS * ops / byts / 1e3)
+            rows.append(dict(m=m, k=k, n=n, us=round(us, 1), tops=round(tops, 1),
+                             frac_peak=round(tops / INT8_PEAK_TOPS, 3), frac_bound=round(tops / bound, 3)))
+            del xq, wq, out
+    tot_ops = sum(2.0 * r["m"] * r["n"] * r["k"] for r in rows)
+    tot_us = sum(r["us"] for r in rows)
+    return dict(tops=round(tot_ops / tot_us / 1e6, 1), frac_peak=round(tot_ops / tot_us / 1e6 / INT8_PEAK_TOPS, 3),
+                shapes=rows)
+
+
+def mfma_roof(torch, lib, dev):
+    from brain_amd._lib import check
+
+    blocks, iters = 256 * 8, 4096
+    out = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    sp = torch.cuda.current_stream().cuda_stream
+    check(lib.bh_roof_mfma_i8(sp, blocks, 64, out.data_ptr()))
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    check(lib.bh_roof_mfma_i8(sp, blocks, iters, out.data_ptr()))
+    b.record()
+    torch.cuda.synchronize()
+    ops = blocks * 4 * iters * 4 * 65536.0
+    return round(ops / (a.elapsed_time(b) * 1e-3) / 1e12, 1)
+
+
+def cpu_baseline(budget_s):
+    """The restated backend-cpu decode path (max_abs_row -> quant_pack ->
+    matmul_i8_gemv, OpenMP over output columns) on this host, on the same
+    16-linear sweep; repeated up to the time budget, median reported."""
+    import numpy as np
+    from oracle import oracle as o
+
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    data = []
+    for m in DECODE_M:
+        for k, n in DECODE_KN:
+            wq, sw = o.synth_weights(n, k, 1000 + m + n) if n * k <= 4 * 1024 * 1024 else _big_weights(n, k)
+            data.append((o.synth_acts(m, k, m + k), wq, sw))
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+        t0 = time.perf_counter()
+        for x, wq, sw in data:
+            o.cpu_linear_gemv(x, wq, sw, threads)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s and len(times) >= 1:
+            break
+    t = sorted(times)[len(times) // 2]
+    byts = sum(linear_bytes(m, k, n) for m in DECODE_M for k, n in DECODE_KN)
+    return dict(value=round(byts / t / 1e9, 2), unit="GB/s", cores=threads, kind="port",
+                sample=f"full 16-linear decode sweep, {len(times)} runs, median {t * 1e3:.1f} ms per sweep",
+                step_ms=round(t * 1e3, 2))
+
+
+def _big_weights(n, k):
+    import numpy as np
+
+    rng = np.random.default_rng(n + k)
+    q = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    return np.ascontiguousarray(q).view(np.uint32), rng.uniform(0.002, 0.02, n).astype(np.float32)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the int8 linear shards over output channels with no exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import brain_amd
+
+    lib = brain_amd.load()
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    res = {}
+    if args.only in ("", "decode"):
+        sets = make_decode_set(torch, dev, gen)
+        res["decode"] = bench_decode(torch, lib, sets, args.steps, args.warmup)
+        del sets
+    if args.only in ("", "prefill") and not args.no_prefill:
+        res["prefill"] = bench_prefill(torch, lib, dev, gen, args.prefill_reps)
+    if args.only:
+        print(json.dumps(res))
+        return
+    roof = mfma_roof(torch, lib, dev)
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+
+    d = res["decode"]
+    value = d["step_bytes"] / (d["step_ms"] * 1e-3) / 1e9
+    gemv_gbs = d["gemv_mean_bytes"] / (d["gemv_mean_us"] * 1e-6) / 1e9
+    line = {
+        "metric": "int8 GEMM TOPS & %peak (prefill); GEMV GB/s & %HBM (decode); vs CPU",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(d["step_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i8",
+        "data": "synthetic (seeded torch RNG: int8 W uniform [-127,127], sw U(0.002,0.02), x N(0,1))",
+        "config": {"workload": "configs[1] decode GEMV sweep: 16 int8 linears (quant + GEMV, bf16 out), "
+                               "M in {1,4,8,16} x (K,N) in {(1024,3072),(3072,1024),(1024,2048),(1024,151936)}",
+                   "weight_pool_mb": round(sum(k * n for k, n in DECODE_KN) * len(DECODE_M) / 1e6, 1),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_i8_kernel", "avg_launch_us": round(d["gemv_mean_us"], 2),
+                     "avg_algorithmic_bytes": round(d["gemv_mean_bytes"])},
+        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+        "decode_shapes": d["shapes"],
+        "mfma_roof_probe_tops": roof,
+    }
+    if "prefill" in res:
+        line["prefill"] = res["prefill"]
+    if cpu is not None:
+        line["gpu_vs_cpu"] = round(value / cpu["value"], 1)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -33,6 +33,62 @@ hipError_t launch_gemm_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
 hipError_t launch_gemm_i8_static(hipStream_t s, const uint32_t* xq, const uint32_t* wq, float ssx, float ssw,
                                  float* out, int m, int kg, int n);
 
+size_t gemm_workspace_ints(int m, int kg, int n, size_t* counters);
+
+// Split-K workspace, one per (device, stream): i32 sums plus per-tile arrival
+// counters. Zeroed once when (re)allocated; every kernel that uses it leaves
+// it zeroed again, so no per-call clear is needed. Calls on one stream are
+// ordered, so they never share it concurrently.
+struct SplitWs {
+    int device;
+    hipStream_t stream;
+    int* ws;
+    size_t ints;
+    int* counters;
+    size_t ncounters;
+};
+static std::mutex g_ws_mu;
+static std::vector<SplitWs> g_ws;
+thread_local hipStream_t g_cur_stream = nullptr;
+
+int* splitk_workspace(size_t ints, size_t counters, int** counters_out, hipError_t* err) {
+    int dev = 0;
+    *err = hipGetDevice(&dev);
+    if (*err != hipSuccess) return nullptr;
+    const hipStream_t st = g_cur_stream;  // bound by the C-ABI launcher on this thread
+    std::lock_guard<std::mutex> g(g_ws_mu);
+    SplitWs* w = nullptr;
+    for (auto& x : g_ws)
+        if (x.device == dev && x.stream == st) w = &x;
+    if (!w) {
+        g_ws.push_back(SplitWs{dev, st, nullptr, 0, nullptr, 0});
+        w = &g_ws.back();
+    }
+    if (w->ints < ints || w->ncounters < counters) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (st && hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+            // No allocation inside a capture: the caller reserves beforehand.
+            *err = hipErrorStreamCaptureUnsupported;
+            return nullptr;
+        }
+        // Growing: wait for this stream's queued users of the old buffers.
+        if ((*err = hipStreamSynchronize(st)) != hipSuccess) return nullptr;
+        if (w->ws) (void)hipFree(w->ws);
+        if (w->counters) (void)hipFree(w->counters);
+        w->ws = nullptr;
+        w->counters = nullptr;
+        w->ints = std::max(ints, w->ints);
+        w->ncounters = std::max(counters, w->ncounters);
+        if ((*err = hipMalloc(&w->ws, w->ints * 4)) != hipSuccess) { w->ints = 0; return nullptr; }
+        if ((*err = hipMalloc(&w->counters, w->ncounters * 4)) != hipSuccess) { w->ncounters = 0; return nullptr; }
+        if ((*err = hipMemset(w->ws, 0, w->ints * 4)) != hipSuccess) return nullptr;
+        if ((*err = hipMemset(w->counters, 0, w->ncounters * 4)) != hipSuccess) return nullptr;
+        if ((*err = hipDeviceSynchronize()) != hipSuccess) return nullptr;
+    }
+    *counters_out = w->counters;
+    return w->ws;
+}
+
 // ---------------------------------------------------------------- small kernels
 __global__ void fill_zero_kernel(uint32_t* p, uint64_t n) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
@@ -60,21 +116,24 @@ __global__ void roof_dp4a_kernel(const float* inp, float* out, uint32_t n, uint3
     out[idx] = inp[idx] + (float)s;
 }
 
-// Matrix-core roof: 8 independent accumulator chains per wave.
+// Matrix-core roof: 4 independent v_mfma_i32_32x32x32_i8 chains per wave
+// (65536 int ops each), the instruction the prefill GEMM is built on.
 __global__ __launch_bounds__(256) void roof_mfma_i8_kernel(uint32_t iters, int32_t* out) {
     const int lane = threadIdx.x & 63;
     v4i a = {lane, lane * 3 + 1, lane ^ 5, 7};
     v4i b = {lane + 2, 11, lane * 5, lane ^ 9};
-    v4i c[8];
+    v16i c[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) c[j] = v4i{j, 0, 0, 0};
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) c[j][e] = j + e;
     for (uint32_t i = 0; i < iters; ++i) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) c[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c[j], 0, 0, 0);
+        for (int j = 0; j < 4; ++j) c[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c[j], 0, 0, 0);
     }
     int s = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s += c[j][0] + c[j][1] + c[j][2] + c[j][3];
+    for (int j = 0; j < 4; ++j) s += c[j][0] + c[j][5] + c[j][10] + c[j][15];
     out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
@@ -162,9 +221,32 @@ int bh_matmul_i8_dyn(void* stream, const uint32_t* xq, const uint32_t* wq, const
     if (m == 0 || n == 0) return BH_OK;
     const uint64_t tiles = (((uint64_t)m + 127) / 128) * (((uint64_t)n + 127) / 128);
     if (tiles > I32MAX) return fail(BH_ERR_INVALID, "bh_matmul_i8_dyn: %llu tiles", (unsigned long long)tiles);
-    return hip_status(launch_gemm_i8((hipStream_t)stream, xq, wq, sx, sw, bias, out, out_dtype, (int)m, (int)kg,
-                                     (int)n),
-                      "gemm_i8 launch");
+    g_cur_stream = (hipStream_t)stream;
+    hipError_t e = launch_gemm_i8((hipStream_t)stream, xq, wq, sx, sw, bias, out, out_dtype, (int)m, (int)kg, (int)n);
+    if (e == hipErrorStreamCaptureUnsupported)
+        return fail(BH_ERR_INVALID,
+                    "bh_matmul_i8_dyn: m=%u kg=%u n=%u needs the split-K workspace, which cannot be allocated while "
+                    "the stream is capturing; call bh_reserve_workspace on this stream first",
+                    m, kg, n);
+    return hip_status(e, "gemm_i8 launch");
+}
+
+int bh_reserve_workspace(void* stream, uint32_t m, uint32_t kg, uint32_t n) {
+    if ((uint64_t)kg * 4 > I32MAX || m > I32MAX || n > I32MAX)
+        return fail(BH_ERR_INVALID, "bh_reserve_workspace: m=%u kg=%u n=%u out of range", m, kg, n);
+    size_t nc = 0;
+    const size_t ints = gemm_workspace_ints((int)m, (int)kg, (int)n, &nc);
+    if (!ints) return BH_OK;
+    g_cur_stream = (hipStream_t)stream;
+    hipError_t err = hipSuccess;
+    int* counters = nullptr;
+    if (!splitk_workspace(ints, nc, &counters, &err)) {
+        if (err == hipErrorStreamCaptureUnsupported)
+            return fail(BH_ERR_INVALID, "bh_reserve_workspace: stream is capturing; reserve before capture");
+        return fail(err == hipErrorOutOfMemory ? BH_ERR_NOMEM : BH_ERR_HIP, "bh_reserve_workspace: %s",
+                    hipGetErrorString(err));
+    }
+    return BH_OK;
 }
 
 int bh_select_i8(uint32_t m, uint32_t n, uint32_t k, int int8_dot, int workgroup_reductions, int out[2]) {

@@ -2,18 +2,27 @@
 //
 // Computes crates/kernels/wgsl/matmul_i8_dyn.wgsl:50-280 (and the static-scale
 // matmul_i8.wgsl:49-262):
-//   acc[m,n] = sum_k xq[m,k]*wq[n,k]           (exact i32)
-//   out[m,n] = (f32(acc)*sx[m])*sw[n] (+bias[n])  -> f32 | bf16 (RNE)
-// Both operands are K-contiguous ([M,K] and [N,K] int8), i.e. an "NT" GEMM,
-// which is exactly the operand layout v_mfma_i32_16x16x64_i8 wants: every lane
-// feeds 16 consecutive K bytes of one row.
+//   acc[m,n] = sum_k xq[m,k]*wq[n,k]              (exact i32)
+//   out[m,n] = (f32(acc)*sx[m])*sw[n] (+bias[n])  -> f32 | bf16 (RNE) | raw i32
+// Both operands are K-contiguous ([M,K] and [N,K] int8), an "NT" GEMM, which is
+// the operand layout v_mfma_i32_32x32x32_i8 wants: each lane feeds 16
+// consecutive K bytes of one row. (On gfx950 the 32x32x32 i8 MFMA sustains
+// about 1.5x the rate of the 16x16x64 one, so it is the only shape used here.)
 //
 // Block tile BM x BN, K staged BK=128 bytes at a time through LDS, double
-// buffered (one barrier per K step). LDS rows are 128 bytes; the 16-byte chunk
-// c of row r is stored at chunk c ^ (r & 7), so the 16 lanes of a fragment
-// read (16 rows, same logical chunk) and the 8 threads of a staging write
-// (one row, 8 chunks) each touch distinct bank groups.
-// The i32 accumulation is order-independent, so any tiling is bit-exact.
+// buffered with register prefetch (one barrier per stage). LDS rows are 128
+// bytes; 16-byte chunk c of row r lives at chunk c ^ ((r >> 1) & 7), so the
+// 16 lanes of an LDS phase (16 consecutive rows, one logical chunk) land in
+// 16 distinct 16-byte slots of a 256-byte bank line. This register-staged
+// kernel is the fallback for K % 128 != 0 or unaligned operands.
+//
+// Split-K (SPLITK): S workgroups share one output tile, each summing a slice of
+// K; partial sums are added with i32 atomics into a workspace (exact, so the
+// order does not matter); the last workgroup of a tile (per-tile arrival
+// counter) applies the epilogue and returns the workspace tile and its
+// counter to zero, so the workspace is always clean between calls.
+#include <cstdlib>
+
 #include "bh_common.h"
 
 namespace bh {
@@ -25,24 +34,25 @@ struct GemmCfg {
     static constexpr int NT = WM * WN * 64;
     static constexpr int WTM = BM / WM;  // wave tile rows
     static constexpr int WTN = BN / WN;  // wave tile cols
-    static constexpr int FM = WTM / 16;
-    static constexpr int FN = WTN / 16;
-    static constexpr int A_CHUNKS = BM * GM_BK / 16 / NT;  // 16-byte chunks per thread
+    static constexpr int FM = WTM / 32;  // 32x32 fragments per wave tile
+    static constexpr int FN = WTN / 32;
+    static constexpr int A_CHUNKS = BM * GM_BK / 16 / NT;  // 16-byte chunks per thread per stage
     static constexpr int B_CHUNKS = BN * GM_BK / 16 / NT;
     static constexpr int LDS_A = BM * GM_BK;
     static constexpr int LDS_B = BN * GM_BK;
+    static constexpr int STAGE = LDS_A + LDS_B;
+    static_assert(FM >= 1 && FN >= 1, "wave tile must hold whole 32x32 fragments");
     static_assert(A_CHUNKS >= 1 && B_CHUNKS >= 1, "tile too small for block");
+    static_assert(2 * STAGE <= 160 * 1024, "LDS budget");
 };
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * GM_BK + ((chunk ^ (row & 7)) << 4); }
+__device__ __forceinline__ int swz(int row, int chunk) { return row * GM_BK + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
-// Logical tile index from the hardware workgroup id. Workgroups are dispatched
-// round-robin over the 8 XCDs (each with its own L2); remap so that a run of
-// consecutive logical tiles lands on one XCD, then walk tiles in GROUP_M-row
-// groups so neighbouring workgroups share A rows and B columns in that L2.
-__device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int& tm, int& tn) {
-    int pid = blockIdx.x;
-    const int total = gridDim.x;
+// Logical tile from a linear tile id. Workgroups are dispatched round-robin
+// over the 8 XCDs (each with its own L2): remap so a run of consecutive tile
+// ids lands on one XCD, then walk tiles in GROUP_M-row groups so neighbouring
+// workgroups share A rows and B columns in that L2.
+__device__ __forceinline__ void tile_of(int pid, int total, int tiles_m, int tiles_n, int& tm, int& tn) {
     if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
     constexpr int GROUP_M = 8;
     const int in_group = GROUP_M * tiles_n;
@@ -54,30 +64,62 @@ __device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int& tm, int& 
     tn = r / gsz;
 }
 
-// STATIC: per-tensor scalar scales (matmul_i8.wgsl: out = f32(acc) * (sx*sw)).
-template <int BM, int BN, int WM, int WN, int OUT, bool HAS_BIAS, bool ALIGNED, bool STATIC>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_i8_kernel(
-    const uint32_t* __restrict__ xq, const uint32_t* __restrict__ wq, const float* __restrict__ sx,
-    const float* __restrict__ sw, const float* __restrict__ bias, void* __restrict__ out, int m, int kg, int n,
-    float ssx, float ssw) {
-    using C = GemmCfg<BM, BN, WM, WN>;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * (C::LDS_A + C::LDS_B)];
-    // Stage b: A tile at lds + b*STAGE, B tile right after it.
-    constexpr int STAGE = C::LDS_A + C::LDS_B;
+struct GemmArgs {
+    const uint32_t* xq;
+    const uint32_t* wq;
+    const float* sx;
+    const float* sw;
+    const float* bias;
+    void* out;
+    int m, kg, n;
+    float ssx, ssw;   // STATIC scales
+    int splits;       // S (1 = no split)
+    int* ws;          // [m*n] i32 split-K workspace (zero between calls)
+    int* counters;    // [tiles] arrival counters (zero between calls)
+    int dbg;          // tuning only: 1 = skip DMA, 2 = skip MFMA
+};
 
+// One output element through the epilogue.
+template <int OUT, bool HAS_BIAS, bool STATIC>
+__device__ __forceinline__ void emit(const GemmArgs& a, int row, int col, int acc, float sxm, float swn, float bn) {
+    const int64_t idx = (int64_t)row * a.n + col;
+    if constexpr (OUT == OUT_I32) {
+        reinterpret_cast<int*>(a.out)[idx] = acc;
+    } else {
+        float v;
+        if constexpr (STATIC) v = (float)acc * (a.ssx * a.ssw);
+        else v = dequant(acc, sxm, swn);
+        if constexpr (HAS_BIAS) v = v + bn;
+        store_out<OUT>(a.out, idx, v);
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int OUT, bool HAS_BIAS, bool ALIGNED, bool STATIC, bool SPLITK>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_i8_kernel(GemmArgs a) {
+    using C = GemmCfg<BM, BN, WM, WN>;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * C::STAGE];
+
+    const int m = a.m, n = a.n;
     const int tiles_m = (m + BM - 1) / BM;
     const int tiles_n = (n + BN - 1) / BN;
+    const int S = SPLITK ? a.splits : 1;
+    const int tile_id = blockIdx.x / S;
+    const int split = blockIdx.x - tile_id * S;
     int tm, tn;
-    tile_of(tiles_m, tiles_n, tm, tn);
+    tile_of(tile_id, gridDim.x / S, tiles_m, tiles_n, tm, tn);
     const int row0 = tm * BM, col0 = tn * BN;
-    const int kbytes = kg * 4;
-    const int nk = (kbytes + GM_BK - 1) / GM_BK;
+    const int kbytes = a.kg * 4;
+    const int nk_all = (kbytes + GM_BK - 1) / GM_BK;
+    const int kt0 = (int)(((int64_t)nk_all * split) / S);
+    const int kt1 = (int)(((int64_t)nk_all * (split + 1)) / S);
+    const int nk = kt1 - kt0;
 
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const int wm = wave / WN, wn = wave % WN;
 
-    // Staging assignment: chunk q = t + NT*i -> (row q/8, chunk q%8).
+    // Staging assignment: chunk q = t + NT*i -> (row q/8, chunk q%8); 8
+    // consecutive threads read one 128-byte row segment.
     const uint8_t* ag[C::A_CHUNKS];
     int a_lds[C::A_CHUNKS], a_cb[C::A_CHUNKS];
 #pragma unroll
@@ -85,7 +127,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_kernel(
         const int q = t + C::NT * i;
         const int r = q >> 3, cb = q & 7;
         const int gr = min(row0 + r, m - 1);
-        ag[i] = reinterpret_cast<const uint8_t*>(xq) + (int64_t)gr * kbytes;
+        ag[i] = reinterpret_cast<const uint8_t*>(a.xq) + (int64_t)gr * kbytes;
         a_cb[i] = cb * 16;
         a_lds[i] = swz(r, cb);
     }
@@ -96,16 +138,18 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_kernel(
         const int q = t + C::NT * i;
         const int r = q >> 3, cb = q & 7;
         const int gr = min(col0 + r, n - 1);
-        bg[i] = reinterpret_cast<const uint8_t*>(wq) + (int64_t)gr * kbytes;
+        bg[i] = reinterpret_cast<const uint8_t*>(a.wq) + (int64_t)gr * kbytes;
         b_cb[i] = cb * 16;
-        b_lds[i] = swz(r, cb);
+        b_lds[i] = C::LDS_A + swz(r, cb);
     }
 
-    v4i acc[C::FM][C::FN];
+    v16i acc[C::FM][C::FN];
 #pragma unroll
     for (int i = 0; i < C::FM; ++i)
 #pragma unroll
-        for (int j = 0; j < C::FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+        for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
 
     v4i ra[C::A_CHUNKS], rb[C::B_CHUNKS];
     auto gload = [&](int kt) {
@@ -116,95 +160,519 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_kernel(
         for (int i = 0; i < C::B_CHUNKS; ++i) rb[i] = load_k16<ALIGNED>(bg[i], k0 + b_cb[i], kbytes);
     };
     auto sstore = [&](int buf) {
+        uint8_t* base = lds + buf * C::STAGE;
 #pragma unroll
-        for (int i = 0; i < C::A_CHUNKS; ++i) *reinterpret_cast<v4i*>(lds + buf * STAGE + a_lds[i]) = ra[i];
+        for (int i = 0; i < C::A_CHUNKS; ++i) *reinterpret_cast<v4i*>(base + a_lds[i]) = ra[i];
 #pragma unroll
-        for (int i = 0; i < C::B_CHUNKS; ++i) *reinterpret_cast<v4i*>(lds + buf * STAGE + C::LDS_A + b_lds[i]) = rb[i];
+        for (int i = 0; i < C::B_CHUNKS; ++i) *reinterpret_cast<v4i*>(base + b_lds[i]) = rb[i];
     };
 
     if (nk > 0) {
-        gload(0);
+        gload(kt0);
         sstore(0);
     }
     __syncthreads();
 
-    const int frow = lane & 15;   // fragment row within a 16-row group
-    const int fchk = lane >> 4;   // fragment chunk within a 64-byte k step
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) gload(kt + 1);
+    const int frow = lane & 31;  // fragment row within a 32-row group
+    const int fchk = lane >> 5;  // fragment chunk within a 32-byte k step
+    for (int it = 0; it < nk; ++it) {
+        const int cur = it & 1;
+        if (it + 1 < nk) gload(kt0 + it + 1);
+        const uint8_t* base = lds + cur * C::STAGE;
 #pragma unroll
-        for (int ks = 0; ks < GM_BK / 64; ++ks) {
+        for (int ks = 0; ks < GM_BK / 32; ++ks) {
             v4i fa[C::FM], fb[C::FN];
 #pragma unroll
-            for (int i = 0; i < C::FM; ++i) {
-                const int r = wm * C::WTM + i * 16 + frow;
-                fa[i] = *reinterpret_cast<const v4i*>(lds + cur * STAGE + swz(r, ks * 4 + fchk));
-            }
+            for (int i = 0; i < C::FM; ++i)
+                fa[i] = *reinterpret_cast<const v4i*>(base + swz(wm * C::WTM + i * 32 + frow, ks * 2 + fchk));
 #pragma unroll
-            for (int j = 0; j < C::FN; ++j) {
-                const int r = wn * C::WTN + j * 16 + frow;
-                fb[j] = *reinterpret_cast<const v4i*>(lds + cur * STAGE + C::LDS_A + swz(r, ks * 4 + fchk));
-            }
+            for (int j = 0; j < C::FN; ++j)
+                fb[j] = *reinterpret_cast<const v4i*>(base + C::LDS_A + swz(wn * C::WTN + j * 32 + frow, ks * 2 + fchk));
 #pragma unroll
             for (int i = 0; i < C::FM; ++i)
 #pragma unroll
                 for (int j = 0; j < C::FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
         }
-        if (kt + 1 < nk) sstore(cur ^ 1);
+        if (it + 1 < nk) sstore(cur ^ 1);
         __syncthreads();
     }
 
-    // Epilogue: lane l, register e of fragment (i,j) holds
-    // row wm*WTM + 16i + 4(l/16) + e, column wn*WTN + 16j + l%16.
+    // Lane l, register e of fragment (i,j) holds
+    //   row wm*WTM + 32i + 8*(e/4) + 4*(l/32) + e%4,  column wn*WTN + 32j + l%32.
+    const int rbase = row0 + wm * C::WTM + 4 * (lane >> 5);
+    const int cbase = col0 + wn * C::WTN + (lane & 31);
+
+    if constexpr (SPLITK) {
+        if (S > 1) {
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int row = rbase + i * 32 + 8 * (e >> 2) + (e & 3);
+                    if (row >= m) continue;
+#pragma unroll
+                    for (int j = 0; j < C::FN; ++j) {
+                        const int col = cbase + j * 32;
+                        if (col < n) atomicAdd(&a.ws[(int64_t)row * n + col], acc[i][j][e]);
+                    }
+                }
+            __threadfence();
+            __syncthreads();
+            __shared__ int last;
+            if (t == 0) last = (atomicAdd(&a.counters[tile_id], 1) == S - 1);
+            __syncthreads();
+            if (!last) return;
+            __threadfence();
+            // Last arrival: read the complete sums back, clear the tile.
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int row = rbase + i * 32 + 8 * (e >> 2) + (e & 3);
+                    if (row >= m) continue;
+#pragma unroll
+                    for (int j = 0; j < C::FN; ++j) {
+                        const int col = cbase + j * 32;
+                        if (col >= n) continue;
+                        int* p = &a.ws[(int64_t)row * n + col];
+                        acc[i][j][e] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        *p = 0;
+                    }
+                }
+            if (t == 0) a.counters[tile_id] = 0;
+        }
+    }
+
     float swv[C::FN], bv[C::FN];
-    int cols[C::FN];
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) {
-        cols[j] = col0 + wn * C::WTN + j * 16 + (lane & 15);
-        const bool ok = cols[j] < n;
-        if constexpr (!STATIC && OUT != OUT_I32) swv[j] = ok ? sw[cols[j]] : 0.0f;
-        if constexpr (HAS_BIAS) bv[j] = ok ? bias[cols[j]] : 0.0f;
+        const int col = cbase + j * 32;
+        const bool ok = col < n;
+        swv[j] = 0.0f;
+        bv[j] = 0.0f;
+        if constexpr (!STATIC && OUT != OUT_I32) swv[j] = ok ? a.sw[col] : 0.0f;
+        if constexpr (HAS_BIAS && OUT != OUT_I32) bv[j] = ok ? a.bias[col] : 0.0f;
     }
-    const float sc = ssx * ssw;
 #pragma unroll
     for (int i = 0; i < C::FM; ++i)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int row = row0 + wm * C::WTM + i * 16 + 4 * (lane >> 4) + e;
+        for (int e = 0; e < 16; ++e) {
+            const int row = rbase + i * 32 + 8 * (e >> 2) + (e & 3);
             if (row >= m) continue;
             float sxm = 0.0f;
-            if constexpr (!STATIC && OUT != OUT_I32) sxm = sx[row];
+            if constexpr (!STATIC && OUT != OUT_I32) sxm = a.sx[row];
 #pragma unroll
             for (int j = 0; j < C::FN; ++j) {
-                if (cols[j] >= n) continue;
-                if constexpr (OUT == OUT_I32) {
-                    reinterpret_cast<int*>(out)[(int64_t)row * n + cols[j]] = acc[i][j][e];
-                    continue;
-                }
-                float v;
-                if constexpr (STATIC) v = (float)acc[i][j][e] * sc;
-                else v = dequant(acc[i][j][e], sxm, swv[j]);
-                if constexpr (HAS_BIAS) v = v + bv[j];
-                store_out<OUT>(out, (int64_t)row * n + cols[j], v);
+                const int col = cbase + j * 32;
+                if (col < n) emit<OUT, HAS_BIAS, STATIC>(a, row, col, acc[i][j][e], sxm, swv[j], bv[j]);
             }
         }
 }
 
-template <int OUT, bool HAS_BIAS, bool STATIC>
-static hipError_t gemm_go(hipStream_t s, bool aligned, const uint32_t* xq, const uint32_t* wq, const float* sx,
-                          const float* sw, const float* bias, void* out, int m, int kg, int n, float ssx,
-                          float ssw) {
-    constexpr int BM = 128, BN = 128, WM = 2, WN = 2;
-    const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+// ---------------------------------------------------------------- pipelined DMA kernel
+// The main path for K % DK == 0 and 16-byte aligned operands. Global memory
+// is copied straight into LDS with global_load_lds_dwordx4 (no staging
+// registers), STAGES buffers of DK K-bytes deep, so the loads of the next
+// STAGES-1 stages are in flight while one stage is multiplied. A DMA
+// instruction writes 64 lanes x 16 bytes to consecutive LDS slots, so the
+// bank swizzle is applied on the global side: LDS slot (row r, chunk p)
+// receives logical K-chunk p ^ f(r).
+//   DK=64  (4 chunks/row): f(r) = (r>>2) & 3
+//   DK=128 (8 chunks/row): f(r) = (r>>1) & 7
+// gfx950 LDS serves a ds_read_b128 16 lanes at a time from 64 four-byte banks
+// (one 256-byte line); a fragment read has 16 lanes on 16 consecutive rows
+// and one logical chunk, and f sends them to 16 distinct 16-byte slots of the
+// line, so the read takes the minimum 4 cycles (measured with
+// SQ_LDS_BANK_CONFLICT = 0; the ((r>>1)^(r>>3)) and r&7 variants cost +4).
+//
+// Within a stage the fragment reads for k-step ks+1 are issued before the
+// MFMAs of k-step ks (sched_barrier keeps the compiler from sinking them), so
+// LDS latency hides behind matrix-core work.
+//
+// The MFMA is fed B (weights) as its first operand, so each 32x32 result is
+// the transposed tile: lane l, register e holds row m = l%32 and column
+// n = 8*(e/4) + 4*(l/32) + e%4, i.e. four consecutive columns per lane, which
+// the epilogue writes with one 8-byte (bf16) or 16-byte (f32) store.
+template <int DK>
+__device__ __forceinline__ int dswz(int r) {
+    if constexpr (DK == 64) return (r >> 2) & 3;
+    else return (r >> 1) & 7;
+}
+template <int DK>
+__device__ __forceinline__ int dslot(int r, int c) { return r * DK + ((c ^ dswz<DK>(r)) << 4); }
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES, int DK>
+struct DmaCfg {
+    static constexpr int NT = WM * WN * 64;
+    static constexpr int WTM = BM / WM, WTN = BN / WN;
+    static constexpr int FM = WTM / 32, FN = WTN / 32;
+    static constexpr int CPR = DK / 16;  // 16-byte chunks per LDS row
+    static constexpr int A_BYTES = BM * DK, B_BYTES = BN * DK;
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int A_LOADS = A_BYTES / 16 / NT;  // DMA instructions per thread per stage
+    static constexpr int B_LOADS = B_BYTES / 16 / NT;
+    static constexpr int LOADS = A_LOADS + B_LOADS;
+    static constexpr int KSTEPS = DK / 32;
+    static_assert(A_LOADS * 16 * NT == A_BYTES && B_LOADS * 16 * NT == B_BYTES, "whole DMA waves");
+    static_assert(STAGES * STAGE <= 160 * 1024, "LDS budget");
+    static_assert((STAGES - 2) * LOADS < 64, "vmcnt range");
+    static_assert(STAGES >= 3, "the next stage's first k-step is read during this one");
+};
+
+template <int N>
+__device__ __forceinline__ void wait_ahead(int ahead) {
+    // Wait until at most `ahead` stages (N loads each) remain in flight.
+    if constexpr (N * 2 < 64) {
+        if (ahead >= 2) { wait_vmcnt<2 * N>(); return; }
+    }
+    if (ahead >= 1) wait_vmcnt<N>();
+    else wait_vmcnt<0>();
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES, int DK, int OUT, bool HAS_BIAS, bool STATIC, bool SPLITK>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the LDS-DMA builtins exist only in the device pass
+    using C = DmaCfg<BM, BN, WM, WN, STAGES, DK>;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * C::STAGE];
+
+    const int m = a.m, n = a.n;
+    const int tiles_m = (m + BM - 1) / BM;
+    const int tiles_n = (n + BN - 1) / BN;
+    const int S = SPLITK ? a.splits : 1;
+    const int tile_id = blockIdx.x / S;
+    const int split = blockIdx.x - tile_id * S;
+    int tm, tn;
+    tile_of(tile_id, gridDim.x / S, tiles_m, tiles_n, tm, tn);
+    const int row0 = tm * BM, col0 = tn * BN;
+    const int kbytes = a.kg * 4;
+    const int nk_all = kbytes / DK;
+    const int kt0 = (int)(((int64_t)nk_all * split) / S);
+    const int kt1 = (int)(((int64_t)nk_all * (split + 1)) / S);
+    const int nk = kt1 - kt0;
+
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+
+    // DMA source addresses: thread t's i-th load fills LDS slot q = t + NT*i
+    // (16-byte slots, CPR per row) of the A (then B) tile.
+    const uint8_t* asrc[C::A_LOADS];
+    const uint8_t* bsrc[C::B_LOADS];
+#pragma unroll
+    for (int i = 0; i < C::A_LOADS; ++i) {
+        const int q = t + C::NT * i, r = q / C::CPR, p = q % C::CPR;
+        const int gr = min(row0 + r, m - 1);
+        asrc[i] = reinterpret_cast<const uint8_t*>(a.xq) + (int64_t)gr * kbytes + ((p ^ dswz<DK>(r)) << 4);
+    }
+#pragma unroll
+    for (int i = 0; i < C::B_LOADS; ++i) {
+        const int q = t + C::NT * i, r = q / C::CPR, p = q % C::CPR;
+        const int gr = min(col0 + r, n - 1);
+        bsrc[i] = reinterpret_cast<const uint8_t*>(a.wq) + (int64_t)gr * kbytes + ((p ^ dswz<DK>(r)) << 4);
+    }
+    // The wave-uniform LDS base of load i (the hardware adds lane*16). The
+    // DMA is issued through inline asm so the compiler does not track it:
+    // its completion is ordered only by the explicit vmcnt waits + barrier
+    // below (hardware vmcnt covers the LDS write of an LDS-DMA load).
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds + wave * 64 * 16;
+    auto dma = [&](const uint8_t* src, uint32_t ldsaddr) {
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                     :
+                     : "v"(src), "s"(__builtin_amdgcn_readfirstlane(ldsaddr))
+                     : "memory", "m0");
+    };
+    auto issue = [&](int kt, int buf) {
+        const uint32_t base = lds_base + buf * C::STAGE;
+        const int64_t koff = (int64_t)kt * DK;
+#pragma unroll
+        for (int i = 0; i < C::A_LOADS; ++i) dma(asrc[i] + koff, base + i * C::NT * 16);
+#pragma unroll
+        for (int i = 0; i < C::B_LOADS; ++i) dma(bsrc[i] + koff, base + C::A_BYTES + i * C::NT * 16);
+    };
+
+    v16i acc[C::FM][C::FN];
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
+
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < nk) issue(kt0 + s, s);
+
+    const int frow = lane & 31, fchk = lane >> 5;
+    auto read_frags = [&](const uint8_t* A, int ks, v4i* fa, v4i* fb) {
+        const uint8_t* B = A + C::A_BYTES;
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i)
+            fa[i] = *reinterpret_cast<const v4i*>(A + dslot<DK>(wm * C::WTM + i * 32 + frow, 2 * ks + fchk));
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j)
+            fb[j] = *reinterpret_cast<const v4i*>(B + dslot<DK>(wn * C::WTN + j * 32 + frow, 2 * ks + fchk));
+    };
+    // One k-step of MFMAs with the next k-step's fragment reads interleaved:
+    // MFMA, read, MFMA, read, ... then the remaining MFMAs.
+    auto mfma_step = [&](const v4i* fa, const v4i* fb) {
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j], fa[i], acc[i][j], 0, 0, 0);
+    };
+    auto interleave = [&]() {
+#pragma unroll
+        for (int q = 0; q < C::FM + C::FN; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, C::FM * C::FN - (C::FM + C::FN), 0);
+    };
+
+    v4i fa[2][C::FM], fb[2][C::FN];
+    if (nk > 0) {
+        wait_ahead<C::LOADS>(min(nk - 1, STAGES - 2));
+        __builtin_amdgcn_s_barrier();
+        read_frags(lds + (0 % STAGES) * C::STAGE, 0, fa[0], fb[0]);
+    }
+    for (int it = 0; it < nk; ++it) {
+        // Stages it and it+1 must have landed (the tail of this iteration
+        // reads stage it+1's first k-step); later ones may still be in flight.
+        wait_ahead<C::LOADS>(min(nk - 2 - it, STAGES - 3));
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        if (it + STAGES - 1 < nk && !(a.dbg & 1)) issue(kt0 + it + STAGES - 1, (it + STAGES - 1) % STAGES);
+        const uint8_t* A = lds + (it % STAGES) * C::STAGE;
+        const uint8_t* An = lds + ((it + 1) % STAGES) * C::STAGE;
+#pragma unroll
+        for (int ks = 0; ks < C::KSTEPS; ++ks) {
+            const int cur = ks & 1, nxt = cur ^ 1;
+            __builtin_amdgcn_sched_barrier(0);
+            // The last k-step reads the next stage's first fragments (on the
+            // final iteration that buffer holds stale data that is never used).
+            read_frags(ks + 1 < C::KSTEPS ? A : An, ks + 1 < C::KSTEPS ? ks + 1 : 0, fa[nxt], fb[nxt]);
+            if (!(a.dbg & 2)) {
+                mfma_step(fa[cur], fb[cur]);
+                interleave();
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (C::KSTEPS % 2 == 1) {
+            // keep fa[0]/fb[0] as "current" for the next stage
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i) fa[0][i] = fa[1][i];
+#pragma unroll
+            for (int j = 0; j < C::FN; ++j) fb[0][j] = fb[1][j];
+        }
+    }
+
+    // Lane l, register e of fragment (i,j): row rbase + 32i, columns
+    // cbase + 32j + 8*(e/4) + (e%4).
+    const int rbase = row0 + wm * C::WTM + (lane & 31);
+    const int cbase = col0 + wn * C::WTN + 4 * (lane >> 5);
+
+    if constexpr (SPLITK) {
+        if (S > 1) {
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i) {
+                const int row = rbase + i * 32;
+                if (row >= m) continue;
+#pragma unroll
+                for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int col = cbase + j * 32 + 8 * (e >> 2) + (e & 3);
+                        if (col < n) atomicAdd(&a.ws[(int64_t)row * n + col], acc[i][j][e]);
+                    }
+            }
+            __threadfence();
+            __syncthreads();
+            __shared__ int last;
+            if (t == 0) last = (atomicAdd(&a.counters[tile_id], 1) == S - 1);
+            __syncthreads();
+            if (!last) return;
+            __threadfence();
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i) {
+                const int row = rbase + i * 32;
+                if (row >= m) continue;
+#pragma unroll
+                for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int col = cbase + j * 32 + 8 * (e >> 2) + (e & 3);
+                        if (col >= n) continue;
+                        int* p = &a.ws[(int64_t)row * n + col];
+                        acc[i][j][e] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        *p = 0;
+                    }
+            }
+            if (t == 0) a.counters[tile_id] = 0;
+        }
+    }
+
+    // Epilogue: four consecutive columns per (fragment, e/4) group.
+    // Vector stores/loads need every 4-column group 16-byte aligned (8 for bf16):
+    // n % 4 == 0 and aligned base pointers (a step_sliced word offset may break that).
+    const bool vec_ok = (n % 4) == 0 && (reinterpret_cast<uintptr_t>(a.out) & (OUT == OUT_BF16 ? 7u : 15u)) == 0;
+    const bool vec_sw = (reinterpret_cast<uintptr_t>(a.sw) & 15u) == 0;
+    const bool vec_b = (reinterpret_cast<uintptr_t>(a.bias) & 15u) == 0;
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int col = cbase + j * 32 + 8 * g;
+            float4 swv = make_float4(0.f, 0.f, 0.f, 0.f), bv = make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (!STATIC && OUT != OUT_I32) {
+                if (vec_sw && col + 3 < n) swv = *reinterpret_cast<const float4*>(a.sw + col);
+                else {
+                    if (col + 0 < n) swv.x = a.sw[col + 0];
+                    if (col + 1 < n) swv.y = a.sw[col + 1];
+                    if (col + 2 < n) swv.z = a.sw[col + 2];
+                    if (col + 3 < n) swv.w = a.sw[col + 3];
+                }
+            }
+            if constexpr (HAS_BIAS && OUT != OUT_I32) {
+                if (vec_b && col + 3 < n) bv = *reinterpret_cast<const float4*>(a.bias + col);
+                else {
+                    if (col + 0 < n) bv.x = a.bias[col + 0];
+                    if (col + 1 < n) bv.y = a.bias[col + 1];
+                    if (col + 2 < n) bv.z = a.bias[col + 2];
+                    if (col + 3 < n) bv.w = a.bias[col + 3];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i) {
+                const int row = rbase + i * 32;
+                if (row >= m || col >= n) continue;
+                float sxm = 0.0f;
+                if constexpr (!STATIC && OUT != OUT_I32) sxm = a.sx[row];
+                const int v0 = acc[i][j][4 * g + 0], v1 = acc[i][j][4 * g + 1];
+                const int v2 = acc[i][j][4 * g + 2], v3 = acc[i][j][4 * g + 3];
+                const int64_t idx = (int64_t)row * n + col;
+                if (vec_ok && col + 3 < n) {
+                    if constexpr (OUT == OUT_I32) {
+                        *reinterpret_cast<v4i*>(reinterpret_cast<int*>(a.out) + idx) = v4i{v0, v1, v2, v3};
+                    } else {
+                        float f0, f1, f2, f3;
+                        if constexpr (STATIC) {
+                            const float sc = a.ssx * a.ssw;
+                            f0 = (float)v0 * sc; f1 = (float)v1 * sc; f2 = (float)v2 * sc; f3 = (float)v3 * sc;
+                        } else {
+                            f0 = dequant(v0, sxm, swv.x); f1 = dequant(v1, sxm, swv.y);
+                            f2 = dequant(v2, sxm, swv.z); f3 = dequant(v3, sxm, swv.w);
+                        }
+                        if constexpr (HAS_BIAS) { f0 = f0 + bv.x; f1 = f1 + bv.y; f2 = f2 + bv.z; f3 = f3 + bv.w; }
+                        if constexpr (OUT == OUT_F32) {
+                            *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + idx) = make_float4(f0, f1, f2, f3);
+                        } else {
+                            const uint32_t lo = (uint32_t)f32_to_bf16_rne(f0) | ((uint32_t)f32_to_bf16_rne(f1) << 16);
+                            const uint32_t hi = (uint32_t)f32_to_bf16_rne(f2) | ((uint32_t)f32_to_bf16_rne(f3) << 16);
+                            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.out) + idx) = make_uint2(lo, hi);
+                        }
+                    }
+                } else {
+                    const int vv[4] = {v0, v1, v2, v3};
+                    const float sv[4] = {swv.x, swv.y, swv.z, swv.w};
+                    const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (col + q < n) emit<OUT, HAS_BIAS, STATIC>(a, row, col + q, vv[q], sxm, sv[q], bb[q]);
+                }
+            }
+        }
+#endif
+}
+
+// ---------------------------------------------------------------- host side
+struct TileChoice {
+    int cfg;     // 0: 256x256 (4 waves, 128x128 each), 1: 128x128 (4 waves, 64x64 each)
+    int splits;  // split-K factor
+};
+
+// Pick a tile shape and split-K factor that fill the 256 CUs. Big problems use
+// 256x256 tiles (half the L2->LDS traffic per op of 128x128); when those give
+// too few workgroups, 128x128 tiles, then split K until ~2 workgroups per CU
+// while keeping >= 4 LDS stages (512 K-bytes) per split.
+static TileChoice choose_tiles(int m, int kg, int n) {
+    constexpr int CUS = 256;
+    const int kbytes = kg * 4;
+    const int nk = (kbytes + GM_BK - 1) / GM_BK;
+    const long t256 = (long)((m + 255) / 256) * ((n + 255) / 256);
+    if (t256 >= CUS) return {0, 1};
+    const long t128 = (long)((m + 127) / 128) * ((n + 127) / 128);
+    int s = 1;
+    while (t128 * s < 2 * CUS && nk / (s * 2) >= 4) s *= 2;
+    return {1, s};
+}
+
+template <int BM, int BN, int WM, int WN, int OUT, bool HAS_BIAS, bool STATIC, bool SPLITK>
+static hipError_t go(hipStream_t s, bool aligned, const GemmArgs& a) {
+    const long tiles = (long)((a.m + BM - 1) / BM) * ((a.n + BN - 1) / BN);
+    const unsigned grid = (unsigned)(tiles * (SPLITK ? a.splits : 1));
+    constexpr int NT = WM * WN * 64;
     if (aligned)
-        gemm_i8_kernel<BM, BN, WM, WN, OUT, HAS_BIAS, true, STATIC>
-            <<<tiles, WM * WN * 64, 0, s>>>(xq, wq, sx, sw, bias, out, m, kg, n, ssx, ssw);
+        gemm_i8_kernel<BM, BN, WM, WN, OUT, HAS_BIAS, true, STATIC, SPLITK><<<grid, NT, 0, s>>>(a);
     else
-        gemm_i8_kernel<BM, BN, WM, WN, OUT, HAS_BIAS, false, STATIC>
-            <<<tiles, WM * WN * 64, 0, s>>>(xq, wq, sx, sw, bias, out, m, kg, n, ssx, ssw);
+        gemm_i8_kernel<BM, BN, WM, WN, OUT, HAS_BIAS, false, STATIC, SPLITK><<<grid, NT, 0, s>>>(a);
     return hipGetLastError();
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES, int DK, int OUT, bool HAS_BIAS, bool STATIC, bool SPLITK>
+static hipError_t go_dma(hipStream_t s, const GemmArgs& a) {
+    const long tiles = (long)((a.m + BM - 1) / BM) * ((a.n + BN - 1) / BN);
+    const unsigned grid = (unsigned)(tiles * (SPLITK ? a.splits : 1));
+    gemm_i8_dma_kernel<BM, BN, WM, WN, STAGES, DK, OUT, HAS_BIAS, STATIC, SPLITK><<<grid, WM * WN * 64, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+static int dbg_flags() {
+    static int v = [] {
+        const char* e = getenv("BH_GEMM_DBG");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
+// Tuning knob for the large-tile DMA configuration (read once):
+// BH_GEMM_BIG=0: 256x256, 4 waves, DK=64, 4 stages (default)
+// BH_GEMM_BIG=1: 256x128, 4 waves (128x64 each), DK=128, 3 stages
+// BH_GEMM_BIG=2: 256x256, 8 waves (128x64 each), DK=64, 4 stages
+static int big_cfg() {
+    static int v = [] {
+        const char* e = getenv("BH_GEMM_BIG");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
+// dma: K % 64 == 0 and both operands 16-byte aligned (the DMA path cannot
+// zero-fill a K tail, so anything else takes the register-staged kernel).
+template <int OUT, bool HAS_BIAS, bool STATIC>
+static hipError_t go_cfg(hipStream_t s, bool aligned, bool dma, const TileChoice& tc, const GemmArgs& a) {
+    if (dma) {
+        if (tc.cfg == 0) {
+            switch (big_cfg()) {
+                case 1: return go_dma<256, 128, 2, 2, 3, 128, OUT, HAS_BIAS, STATIC, false>(s, a);
+                case 2: return go_dma<256, 256, 2, 4, 4, 64, OUT, HAS_BIAS, STATIC, false>(s, a);
+                default: return go_dma<256, 256, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, false>(s, a);
+            }
+        }
+        if (tc.splits > 1) return go_dma<128, 128, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, true>(s, a);
+        return go_dma<128, 128, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, false>(s, a);
+    }
+    if (tc.cfg == 0) return go<256, 256, 2, 2, OUT, HAS_BIAS, STATIC, false>(s, aligned, a);
+    if (tc.splits > 1) return go<128, 128, 2, 2, OUT, HAS_BIAS, STATIC, true>(s, aligned, a);
+    return go<128, 128, 2, 2, OUT, HAS_BIAS, STATIC, false>(s, aligned, a);
 }
 
 static inline bool gemm_aligned(const void* xq, const void* wq, int kg) {
@@ -212,23 +680,51 @@ static inline bool gemm_aligned(const void* xq, const void* wq, int kg) {
            ((reinterpret_cast<uintptr_t>(wq) & 15u) == 0);
 }
 
+// Split-K workspace of one device: [m*n] i32 sums plus per-tile counters,
+// zeroed once at allocation and left zeroed by every kernel that uses them.
+int* splitk_workspace(size_t ints, size_t counters, int** counters_out, hipError_t* err);
+
+// Workspace elements the GEMM needs for this shape (0 = no split-K).
+size_t gemm_workspace_ints(int m, int kg, int n, size_t* counters) {
+    TileChoice tc = choose_tiles(m, kg, n);
+    if (tc.splits <= 1) {
+        *counters = 0;
+        return 0;
+    }
+    *counters = (size_t)((m + 127) / 128) * ((n + 127) / 128);
+    return (size_t)m * n;
+}
+
 hipError_t launch_gemm_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n) {
+    GemmArgs a{xq, wq, sx, sw, bias, out, m, kg, n, 0.f, 0.f, 1, nullptr, nullptr, dbg_flags()};
     const bool al = gemm_aligned(xq, wq, kg);
-    if (out_dtype == OUT_I32)
-        return gemm_go<OUT_I32, false, false>(s, al, xq, wq, sx, sw, nullptr, out, m, kg, n, 0.f, 0.f);
-    if (out_dtype == OUT_F32) {
-        if (bias) return gemm_go<OUT_F32, true, false>(s, al, xq, wq, sx, sw, bias, out, m, kg, n, 0.f, 0.f);
-        return gemm_go<OUT_F32, false, false>(s, al, xq, wq, sx, sw, bias, out, m, kg, n, 0.f, 0.f);
+    const bool dma = al && ((kg * 4) % 128 == 0);
+    TileChoice tc = choose_tiles(m, kg, n);
+    if (tc.splits > 1) {
+        hipError_t err = hipSuccess;
+        size_t nc = 0;
+        const size_t ints = gemm_workspace_ints(m, kg, n, &nc);
+        a.ws = splitk_workspace(ints, nc, &a.counters, &err);
+        if (!a.ws) return err == hipSuccess ? hipErrorOutOfMemory : err;
+        a.splits = tc.splits;
     }
-    if (bias) return gemm_go<OUT_BF16, true, false>(s, al, xq, wq, sx, sw, bias, out, m, kg, n, 0.f, 0.f);
-    return gemm_go<OUT_BF16, false, false>(s, al, xq, wq, sx, sw, bias, out, m, kg, n, 0.f, 0.f);
+    if (out_dtype == OUT_I32) return go_cfg<OUT_I32, false, false>(s, al, dma, tc, a);
+    if (out_dtype == OUT_F32) {
+        if (bias) return go_cfg<OUT_F32, true, false>(s, al, dma, tc, a);
+        return go_cfg<OUT_F32, false, false>(s, al, dma, tc, a);
+    }
+    if (bias) return go_cfg<OUT_BF16, true, false>(s, al, dma, tc, a);
+    return go_cfg<OUT_BF16, false, false>(s, al, dma, tc, a);
 }
 
 hipError_t launch_gemm_i8_static(hipStream_t s, const uint32_t* xq, const uint32_t* wq, float ssx, float ssw,
                                  float* out, int m, int kg, int n) {
+    GemmArgs a{xq, wq, nullptr, nullptr, nullptr, out, m, kg, n, ssx, ssw, 1, nullptr, nullptr, 0};
+    TileChoice tc = choose_tiles(m, kg, n);
+    tc.splits = 1;  // the static variant stays on plain tiles
     const bool al = gemm_aligned(xq, wq, kg);
-    return gemm_go<OUT_F32, false, true>(s, al, xq, wq, nullptr, nullptr, nullptr, out, m, kg, n, ssx, ssw);
+    return go_cfg<OUT_F32, false, true>(s, al, al && ((kg * 4) % 128 == 0), tc, a);
 }
 
 }  // namespace bh

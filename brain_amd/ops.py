@@ -123,3 +123,10 @@ def quantize_weight_device(w):
     sw = torch.empty(n, device=w.device, dtype=torch.float32)
     check(load().bh_quantize_weight_device(_stream(), _ptr(w), n, k, _ptr(packed), _ptr(sw)))
     return packed, sw
+
+
+def reserve_workspace(m, k, n, stream=None):
+    """Pre-size the split-K workspace of `stream` (default: current) for an
+    [m,k] x [n,k] GEMM; required before capturing such a GEMM in a graph."""
+    sp = (stream or torch.cuda.current_stream()).cuda_stream
+    check(load().bh_reserve_workspace(sp, m, k // 4, n))

@@ -94,6 +94,14 @@ int bh_matmul_i8_gemv(void* stream, const uint32_t* xq, const uint32_t* wq, cons
 int bh_matmul_i8_dyn(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
                      const float* bias, void* out, int out_dtype, uint32_t m, uint32_t kg, uint32_t n);
 
+/* Pre-size the library-held split-K workspace of `stream` for a
+ * bh_matmul_i8_dyn call of this shape (a no-op for shapes that do not split
+ * K). The workspace is allocated per (device, stream) on first need and
+ * grows on demand; a growth cannot happen while the stream is being captured
+ * into a HIP graph, so callers that capture reserve for their largest shape
+ * first. */
+int bh_reserve_workspace(void* stream, uint32_t m, uint32_t kg, uint32_t n);
+
 /* Static per-tensor scales: out = f32(acc) * (sx*sw). Replaces `matmul_i8`,
  * bindings [x, w, out], params [m, kg, n, sx_bits, sw_bits]
  * (crates/kernels/wgsl/matmul_i8.wgsl:49-262). */
@@ -113,9 +121,9 @@ int bh_linear_i8(void* stream, const float* x, const uint32_t* wq, const float* 
 int bh_quantize_weight_device(void* stream, const float* w, uint32_t n, uint32_t k, uint32_t* packed, float* sw);
 
 /* Int8 matrix-core roof probe: `blocks` workgroups of 256 threads each run
- * `iters` dependent-free v_mfma_i32_16x16x64_i8 chains; out[blocks*256] i32
+ * `iters` rounds of 4 independent v_mfma_i32_32x32x32_i8 chains; out[blocks*256] i32
  * receives a data-dependent sum so nothing folds. Ops executed =
- * blocks*4*iters*8*32768. The MI355X counterpart of the `roof_dp4a` probe
+ * blocks*4*iters*4*65536. The MI355X counterpart of the `roof_dp4a` probe
  * (crates/kernels/wgsl/roof_dp4a.wgsl:28-63, crates/gpu-core/src/roof.rs:99-130). */
 int bh_roof_mfma_i8(void* stream, uint32_t blocks, uint32_t iters, int32_t* out);
 

@@ -1,0 +1,63 @@
+"""The int8 linear captured in a HIP graph: every replay (with eager work and
+synchronisations between replays) must equal the eager result bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+from brain_amd import ops
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+
+def test_graph_replays_match_eager(gpu):
+    shapes = [(1, 1024, 3072), (16, 3072, 1024), (64, 1024, 640), (512, 1024, 1024)]
+    data = []
+    for i, (m, k, n) in enumerate(shapes):
+        x = torch.from_numpy(o.synth_acts(m, k, 10 + i)).to(gpu)
+        wq, sw = o.synth_weights(n, k, 20 + i)
+        data.append(dict(x=x, wq=torch.from_numpy(wq.view(np.int32)).to(gpu), sw=torch.from_numpy(sw).to(gpu),
+                         bias=torch.randn(n, device=gpu), sx=torch.empty(m, device=gpu),
+                         xq=torch.empty(m, k // 4, dtype=torch.int32, device=gpu),
+                         out=torch.empty(m, n, dtype=torch.bfloat16, device=gpu)))
+
+    def run():
+        for d in data:
+            ops.linear_i8(d["x"], d["wq"], d["sw"], d["bias"], torch.bfloat16, sx=d["sx"], xq=d["xq"], out=d["out"])
+
+    run()
+    torch.cuda.synchronize()
+    eager = [d["out"].clone() for d in data]
+    cap = torch.cuda.Stream()
+    for (m, k, n) in shapes:
+        ops.reserve_workspace(m, k, n, cap)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap):
+        run()
+    for rep in range(4):
+        for d in data:
+            d["out"].fill_(0)
+        _ = torch.randn(1000, device=gpu).sum()  # unrelated eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        for d, e in zip(data, eager):
+            assert torch.equal(d["out"].view(torch.int16), e.view(torch.int16)), f"replay {rep} differs"
+
+
+def test_split_k_inside_capture_without_reserve_fails_cleanly(gpu):
+    from brain_amd import BrainHipError
+    m, k, n = 384, 2048, 768   # a split-K shape
+    xq = torch.zeros(m, k // 4, dtype=torch.int32, device=gpu)
+    wq = torch.zeros(n, k // 4, dtype=torch.int32, device=gpu)
+    sx = torch.ones(m, device=gpu)
+    sw = torch.ones(n, device=gpu)
+    cap = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(Exception):
+        with torch.cuda.graph(g, stream=cap):
+            try:
+                ops.matmul_i8(xq, wq, sx, sw, variant="dyn")
+            except BrainHipError as e:
+                assert "bh_reserve_workspace" in str(e)
+                raise
+    torch.cuda.synchronize()

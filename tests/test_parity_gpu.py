@@ -235,3 +235,28 @@ def test_device_weight_quantizer(gpu, n, k):
     wp, wsw = o.quantize_weight(w)
     assert (host_u32(packed) == wp).all()
     assert (sw.cpu().numpy() == wsw).all()
+
+
+@pytest.mark.parametrize("variant,m", [("dyn", 300), ("dyn", 1024), ("gemv", 7)])
+def test_matmul_unaligned_scales_bias_and_output(gpu, variant, m):
+    # sw, bias and out one word into their allocations (legal with step_sliced
+    # word offsets): the vector epilogue must fall back to scalar accesses.
+    k, n = 1024, 516
+    x = special_acts(m, k, 8)
+    sx = o.max_abs_row(x)
+    xq = o.quant_pack(x, sx)
+    wq, sw = o.synth_weights(n, k, 9)
+    bias = o.synth_acts(1, n, 10)[0]
+    swb = torch.zeros(n + 1, device=gpu)
+    swb[1:] = dev_f32(sw, gpu)
+    bb = torch.zeros(n + 1, device=gpu)
+    bb[1:] = dev_f32(bias, gpu)
+    acc = o.acc_exact(xq, wq)
+    for dt, want in ((torch.float32, o.epilogue(acc, sx, sw, bias).view(np.uint32)),
+                     (torch.bfloat16, o.epilogue(acc, sx, sw, bias, "bf16"))):
+        ob = torch.zeros(m * n + 1, dtype=dt, device=gpu)
+        ops.matmul_i8(dev_u32(xq, gpu), dev_u32(wq, gpu), dev_f32(sx, gpu), swb[1:], bb[1:], dt, variant,
+                      out=ob[1:].view(m, n))
+        got = ob[1:].view(m, n).cpu()
+        got = got.numpy().view(np.uint32) if dt == torch.float32 else bf16_bits(got)
+        assert (got == want).all(), dt
