@@ -42,7 +42,7 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on CPU-baseline work")
-    ap.add_argument("--only", default="", help="profiling aid: 'decode' or 'prefill' only")
+    ap.add_argument("--only", default="", help="profiling aid: 'decode', 'prefill' or 'copy' only")
     return ap.parse_args()
 
 
@@ -137,28 +137,45 @@ def bench_decode(torch, lib, sets, steps, warmup):
     for s in sets:
         check_sample(torch, s, "bf16")
 
-    # Per-launch GEMV durations (events around each GEMV on the same stream),
-    # in a separate pass so the events do not perturb the step timing.
-    evs = []
-    for _ in range(max(3, steps // 5)):
-        for i, s in enumerate(sets):
-            linear(s)
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record(stream)
+    # GEMV kernel duration: the step's 16 GEMV launches alone (activations
+    # already quantized) captured as a second graph and replayed; events on the
+    # replay stream bracket the replays, so the per-launch average counts the
+    # kernel plus the dispatch gap to the next node (a slight overestimate of
+    # the kernel-only time rocprofv3 reports). Per-shape times come from a
+    # graph of 8 launches of one shape each.
+    ggraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(ggraph):
+        for s in sets:
             gemv(s)
-            b.record(stream)
-            evs.append((i, a, b))
+    ggraph.replay()
     torch.cuda.synchronize()
-    per = {}
-    for i, a, b in evs:
-        per.setdefault(i, []).append(a.elapsed_time(b))
+    reps = max(5, steps // 2)
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps):
+        ggraph.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    mean_us = a.elapsed_time(b) * 1e3 / (reps * len(sets))
     shapes = []
-    for i, s in enumerate(sets):
-        us = 1e3 * sorted(per[i])[len(per[i]) // 2]
+    for s in sets:
+        g1 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g1):
+            for _ in range(8):
+                gemv(s)
+        g1.replay()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(3):
+            g1.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / 24
         shapes.append(dict(m=s["m"], k=s["k"], n=s["n"], gemv_us=round(us, 2),
                            gemv_gbs=round(gemv_bytes(s["m"], s["k"], s["n"]) / us / 1e3, 1)))
-    mean_us = sum(sum(v) for v in per.values()) / sum(len(v) for v in per.values()) * 1e3
+        del g1
     mean_bytes = sum(gemv_bytes(s["m"], s["k"], s["n"]) for s in sets) / len(sets)
     step_bytes = sum(linear_bytes(s["m"], s["k"], s["n"]) for s in sets)
     return dict(step_ms=step_ms, wall=wall, step_bytes=step_bytes, gemv_mean_us=mean_us,
@@ -279,6 +296,15 @@ def main():
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
     res = {}
+    if args.only == "copy":
+        # Counter calibration: a plain 256 MiB device-to-device copy, 3 times.
+        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": src.numel() * 4}))
+        return
     if args.only in ("", "decode"):
         sets = make_decode_set(torch, dev, gen)
         res["decode"] = bench_decode(torch, lib, sets, args.steps, args.warmup)
@@ -316,7 +342,7 @@ def main():
                      "kernel": "gemv_i8_kernel", "avg_launch_us": round(d["gemv_mean_us"], 2),
                      "avg_algorithmic_bytes": round(d["gemv_mean_bytes"])},
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
-        "decode_shapes": d["shapes"],
+        "decode_shapes_warm": d["shapes"],
         "mfma_roof_probe_tops": roof,
     }
     if "prefill" in res:

@@ -21,6 +21,8 @@
 //     for a column group before its first MFMA; the first group's loads are
 //     issued before the activation staging so the two overlap;
 //   - fused epilogue: dequant, bias, bf16 RNE.
+#include <cstdlib>
+
 #include "bh_common.h"
 
 namespace bh {
@@ -39,15 +41,15 @@ struct GemvArgs {
     int m, kg, n;
 };
 
-template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int KSPLIT, bool XLDS>
+template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int KSPLIT, bool XLDS, int U, int CG>
 __global__ __launch_bounds__(GV_THREADS) void gemv_i8_kernel(GemvArgs a) {
-    constexpr int SLOTS = GV_WAVES / KSPLIT;  // column groups per workgroup pass
+    constexpr int SLOTS = GV_WAVES / KSPLIT;  // wave slots per workgroup, each CG column groups
     extern __shared__ __attribute__((aligned(16))) uint8_t xs[];  // [MT*16][kbytes+16] when XLDS
-    __shared__ int red[GV_WAVES][MT * 4][64];
+    __shared__ int red[KSPLIT > 1 ? GV_WAVES : 1][CG * MT * 4][64];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int slot = wave / KSPLIT;   // which column group of this pass
+    const int slot = wave / KSPLIT;   // which column group of this workgroup
     const int ks = wave % KSPLIT;     // which K slice
     const int m = a.m, n = a.n;
     const int kbytes = a.kg * 4;
@@ -55,28 +57,27 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_i8_kernel(GemvArgs a) {
     const int ngroups = (n + 15) >> 4;
     const int xstride = kbytes + 16;
     const int ksub = (lane >> 4) * 16;  // this lane's 16-byte slice of a 64-byte chunk
+    const int g0 = (blockIdx.x * SLOTS + slot) * CG;  // first of this wave's CG column groups
 
-    auto wrow_ptr = [&](int g) {
-        int r = g * 16 + (lane & 15);
-        r = r < n ? r : n - 1;  // clamped rows are loaded but never stored
-        return reinterpret_cast<const uint8_t*>(a.wq) + (int64_t)r * kbytes;
-    };
-
-    // First pass's weight loads, issued before the activation staging.
-    int g = blockIdx.x * SLOTS + slot;
-    v4i wf[GV_MAXC];
-    const int my_chunks = (nchunks - ks + KSPLIT - 1) / KSPLIT;  // chunks c = ks + KSPLIT*j
-    const bool single_pass = my_chunks <= GV_MAXC;
-    if (single_pass && g < ngroups) {
-        const uint8_t* wp = wrow_ptr(g);
+    const uint8_t* wp[CG];
 #pragma unroll
-        for (int j = 0; j < GV_MAXC; ++j)
-            if (j < my_chunks) wf[j] = load_k16<ALIGNED>(wp, (ks + KSPLIT * j) * 64 + ksub, kbytes);
+    for (int c = 0; c < CG; ++c) {
+        int wr = (g0 + c) * 16 + (lane & 15);
+        wr = wr < n ? wr : n - 1;  // clamped rows are loaded but never stored
+        wp[c] = reinterpret_cast<const uint8_t*>(a.wq) + (int64_t)wr * kbytes;
     }
+    const int my_chunks = g0 < ngroups ? (nchunks - ks + KSPLIT - 1) / KSPLIT : 0;  // chunks ks + KSPLIT*j
+
+    // The first batch of weight loads goes out before the activation staging.
+    v4i wf[U][CG];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        if (u < my_chunks)
+#pragma unroll
+            for (int c = 0; c < CG; ++c) wf[u][c] = load_k16<ALIGNED>(wp[c], (ks + KSPLIT * u) * 64 + ksub, kbytes);
 
     if constexpr (XLDS) {
-        // Stage xq rows 0..MT*16-1 (zero past m) as 16-byte pieces.
-        const int pieces = (kbytes >> 4);
+        const int pieces = kbytes >> 4;
         const int total = MT * 16 * pieces;
         for (int p = threadIdx.x; p < total; p += GV_THREADS) {
             const int r = p / pieces, c = p - r * pieces;
@@ -86,7 +87,6 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_i8_kernel(GemvArgs a) {
         }
         __syncthreads();
     }
-
     auto xfrag = [&](int t, int kb) -> v4i {
         const int r = (lane & 15) + 16 * t;
         if constexpr (XLDS) {
@@ -98,127 +98,118 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_i8_kernel(GemvArgs a) {
         }
     };
 
-    for (int gb = blockIdx.x; gb * SLOTS < ngroups; gb += gridDim.x) {
-        g = gb * SLOTS + slot;
-        v4i acc[MT];
+    v4i acc[CG][MT];
 #pragma unroll
-        for (int t = 0; t < MT; ++t) acc[t] = v4i{0, 0, 0, 0};
-        if (g < ngroups) {
-            const uint8_t* wp = wrow_ptr(g);
-            if (single_pass) {
-                if (gb != (int)blockIdx.x) {
+    for (int c = 0; c < CG; ++c)
 #pragma unroll
-                    for (int j = 0; j < GV_MAXC; ++j)
-                        if (j < my_chunks) wf[j] = load_k16<ALIGNED>(wp, (ks + KSPLIT * j) * 64 + ksub, kbytes);
-                }
+        for (int t = 0; t < MT; ++t) acc[c][t] = v4i{0, 0, 0, 0};
+#pragma unroll 1
+    for (int j0 = 0; j0 < my_chunks; j0 += U) {
+        if (j0 > 0) {
 #pragma unroll
-                for (int j = 0; j < GV_MAXC; ++j) {
-                    if (j < my_chunks) {
-                        const int kb = (ks + KSPLIT * j) * 64 + ksub;
+            for (int u = 0; u < U; ++u)
+                if (j0 + u < my_chunks)
 #pragma unroll
-                        for (int t = 0; t < MT; ++t)
-                            acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xfrag(t, kb), wf[j], acc[t], 0, 0, 0);
-                    }
-                }
+                    for (int c = 0; c < CG; ++c)
+                        wf[u][c] = load_k16<ALIGNED>(wp[c], (ks + KSPLIT * (j0 + u)) * 64 + ksub, kbytes);
+        }
+        v4i xf[U][MT];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                xf[u][t] = (j0 + u < my_chunks) ? xfrag(t, (ks + KSPLIT * (j0 + u)) * 64 + ksub) : v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (j0 + u < my_chunks)
+#pragma unroll
+                for (int c = 0; c < CG; ++c)
+#pragma unroll
+                    for (int t = 0; t < MT; ++t)
+                        acc[c][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xf[u][t], wf[u][c], acc[c][t], 0, 0, 0);
+    }
+
+    // Lane l, register i of a 16x16 i32 result holds row 4*(l/16)+i, column l%16.
+    auto emit = [&](int c, int ri, int s) {
+        const int col = (g0 + c) * 16 + (lane & 15);
+        const int row = 16 * (ri >> 2) + 4 * (lane >> 4) + (ri & 3);
+        if (row < m && col < n) {
+            const int64_t idx = (int64_t)row * n + col;
+            if constexpr (OUT == OUT_I32) {
+                reinterpret_cast<int*>(a.out)[idx] = s;
             } else {
-                // Long K: passes of GV_MAXC chunks.
-                for (int j0 = 0; j0 < my_chunks; j0 += GV_MAXC) {
-#pragma unroll
-                    for (int j = 0; j < GV_MAXC; ++j)
-                        if (j0 + j < my_chunks)
-                            wf[j] = load_k16<ALIGNED>(wp, (ks + KSPLIT * (j0 + j)) * 64 + ksub, kbytes);
-#pragma unroll
-                    for (int j = 0; j < GV_MAXC; ++j) {
-                        if (j0 + j < my_chunks) {
-                            const int kb = (ks + KSPLIT * (j0 + j)) * 64 + ksub;
-#pragma unroll
-                            for (int t = 0; t < MT; ++t)
-                                acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xfrag(t, kb), wf[j], acc[t], 0, 0, 0);
-                        }
-                    }
-                }
+                float v = dequant(s, a.sx[row], a.sw[col]);
+                if constexpr (HAS_BIAS) v = v + a.bias[col];
+                store_out<OUT>(a.out, idx, v);
             }
         }
-
-        // Lane l, register i of a 16x16 i32 result holds row 4*(l/16)+i, column l%16.
-        const int col = g * 16 + (lane & 15);
-        if constexpr (KSPLIT == 1) {
-            if (g < ngroups) {
+    };
+    if constexpr (KSPLIT == 1) {
 #pragma unroll
-                for (int ri = 0; ri < MT * 4; ++ri) {
-                    const int row = 16 * (ri >> 2) + 4 * (lane >> 4) + (ri & 3);
-                    if (row < m && col < n) {
-                        const int s = acc[ri >> 2][ri & 3];
-                        const int64_t idx = (int64_t)row * n + col;
-                        if constexpr (OUT == OUT_I32) {
-                            reinterpret_cast<int*>(a.out)[idx] = s;
-                        } else {
-                            float v = dequant(s, a.sx[row], a.sw[col]);
-                            if constexpr (HAS_BIAS) v = v + a.bias[col];
-                            store_out<OUT>(a.out, idx, v);
-                        }
-                    }
-                }
-            }
-        } else {
+        for (int c = 0; c < CG; ++c)
+            if (g0 + c < ngroups)
+#pragma unroll
+                for (int ri = 0; ri < MT * 4; ++ri) emit(c, ri, acc[c][ri >> 2][ri & 3]);
+    } else {
+#pragma unroll
+        for (int c = 0; c < CG; ++c)
 #pragma unroll
             for (int t = 0; t < MT; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) red[wave][t * 4 + i][lane] = acc[t][i];
-            __syncthreads();
-            if (g < ngroups) {
-                for (int ri = ks; ri < MT * 4; ri += KSPLIT) {
-                    int s = 0;
+                for (int i = 0; i < 4; ++i) red[wave][(c * MT + t) * 4 + i][lane] = acc[c][t][i];
+        __syncthreads();
+        for (int q = ks; q < CG * MT * 4; q += KSPLIT) {
+            const int c = q / (MT * 4), ri = q % (MT * 4);
+            if (g0 + c >= ngroups) continue;
+            int s = 0;
 #pragma unroll
-                    for (int w = 0; w < KSPLIT; ++w) s += red[slot * KSPLIT + w][ri][lane];
-                    const int row = 16 * (ri >> 2) + 4 * (lane >> 4) + (ri & 3);
-                    if (row < m && col < n) {
-                        const int64_t idx = (int64_t)row * n + col;
-                        if constexpr (OUT == OUT_I32) {
-                            reinterpret_cast<int*>(a.out)[idx] = s;
-                        } else {
-                            float v = dequant(s, a.sx[row], a.sw[col]);
-                            if constexpr (HAS_BIAS) v = v + a.bias[col];
-                            store_out<OUT>(a.out, idx, v);
-                        }
-                    }
-                }
-            }
-            __syncthreads();
+            for (int w = 0; w < KSPLIT; ++w) s += red[slot * KSPLIT + w][q][lane];
+            emit(c, ri, s);
         }
     }
 }
 
 // ---------------------------------------------------------------- host side
-constexpr int GV_CUS = 256;
-constexpr int GV_XLDS_MAX = 64 * 1024;
 
-template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int KSPLIT>
+static int gv_cfg() {
+    static int v = [] {
+        const char* e = getenv("BH_GEMV_CFG");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
+template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int U, int CG>
 static hipError_t gv_go(hipStream_t s, const GemvArgs& a) {
-    constexpr int SLOTS = GV_WAVES / KSPLIT;
+    constexpr int KSPLIT = 4;
+    constexpr int per_wg = (GV_WAVES / KSPLIT) * CG;
     const int ngroups = (a.n + 15) / 16;
-    const int passes_needed = (ngroups + SLOTS - 1) / SLOTS;
-    // One pass per workgroup: a workgroup's weight loads are all issued up
-    // front and fresh workgroups keep the memory pipeline full, which beats a
-    // persistent grid whose passes serialise load latency. (The grid-stride
-    // loop only engages past the grid-size limit.)
-    const int grid = passes_needed < 2147483647 ? passes_needed : 2147483647;
-    const int kbytes = a.kg * 4;
-    const size_t xlds = (size_t)MT * 16 * (kbytes + 16);
-    if (ALIGNED && xlds <= (size_t)GV_XLDS_MAX) {
-        gemv_i8_kernel<MT, OUT, HAS_BIAS, ALIGNED, KSPLIT, true><<<grid, GV_THREADS, xlds, s>>>(a);
-    } else {
-        gemv_i8_kernel<MT, OUT, HAS_BIAS, ALIGNED, KSPLIT, false><<<grid, GV_THREADS, 0, s>>>(a);
-    }
+    const int grid = (ngroups + per_wg - 1) / per_wg;
+    gemv_i8_kernel<MT, OUT, HAS_BIAS, ALIGNED, KSPLIT, false, U, CG><<<grid, GV_THREADS, 0, s>>>(a);
     return hipGetLastError();
 }
 
+// Launch policy (measured on MI355X with rotating >256 MB weight pools):
+//  - wide N (>= 1024 column groups, e.g. the LM head): each wave covers two
+//    column groups, halving activation (L2) traffic per weight byte; batches
+//    of 4 K-chunks keep VGPRs low (8 waves/SIMD) so ~16 KB per workgroup is
+//    in flight across many resident workgroups;
+//  - narrow N: one column group per wave; when a wave owns more than 4
+//    K-chunks (few workgroups, long K) it issues up to 16 at once, so the
+//    whole weight slice is a single memory round trip.
 template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED>
 static hipError_t gv_split(hipStream_t s, const GemvArgs& a) {
     const int ngroups = (a.n + 15) / 16;
-    if (ngroups >= 4 * GV_CUS) return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 1>(s, a);
-    if (ngroups >= 2 * GV_CUS) return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 2>(s, a);
-    return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4>(s, a);
+    const int wave_chunks = ((a.kg * 4 + 63) / 64 + 3) / 4;
+    switch (gv_cfg()) {  // tuning override (BH_GEMV_CFG), 0 = policy
+        case 1: return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 1>(s, a);
+        case 2: return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 2>(s, a);
+        case 3: return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 16, 1>(s, a);
+        default: break;
+    }
+    if (ngroups >= 1024) return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 2>(s, a);
+    if (wave_chunks > 4) return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 16, 1>(s, a);
+    return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 1>(s, a);
 }
 
 template <int MT, int OUT, bool HAS_BIAS>

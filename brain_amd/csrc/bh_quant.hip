@@ -85,8 +85,45 @@ __global__ __launch_bounds__(QT) void quant_pack_kernel(const float* __restrict_
     }
 }
 
-// max_abs_row and quant_pack fused: one block per row, the row is read twice
-// (the second read hits L2), sx written once. Same arithmetic as the pair.
+// max_abs_row and quant_pack fused, single pass: one block per row, each
+// thread keeps its NV float4s of the row in registers across the block max,
+// so the row is read from memory once. Same arithmetic as the pair.
+template <int NV>
+__global__ __launch_bounds__(QT) void quantize_rows_reg_kernel(const float* __restrict__ x, int m, int k,
+                                                               float* __restrict__ sx, uint32_t* __restrict__ xq) {
+    const int row = blockIdx.x;
+    if (row >= m) return;
+    const int kg = k >> 2;
+    const float4* xr = reinterpret_cast<const float4*>(x + (int64_t)row * k);
+    float4 v[NV];
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int g = threadIdx.x + i * QT;
+        v[i] = g < kg ? xr[g] : make_float4(0.f, 0.f, 0.f, 0.f);
+        a = fmaxf(a, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
+    __shared__ float red[QT / 64];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = a;
+    __syncthreads();
+    float mx = red[0];
+#pragma unroll
+    for (int w = 1; w < QT / 64; ++w) mx = fmaxf(mx, red[w]);
+    const float s = fmaxf(mx, 1e-8f) / 127.0f;
+    if (threadIdx.x == 0) sx[row] = s;
+    const float inv = 1.0f / s;
+    uint32_t* q = xq + (int64_t)row * kg;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int g = threadIdx.x + i * QT;
+        if (g < kg) q[g] = quant_word(v[i], inv);
+    }
+}
+
+// max_abs_row and quant_pack fused, two passes (long or unaligned rows): the
+// row is read twice (the second read hits L2), sx written once.
 template <bool VEC>
 __global__ __launch_bounds__(QT) void quantize_rows_kernel(const float* __restrict__ x, int m, int k,
                                                            float* __restrict__ sx,
@@ -162,7 +199,12 @@ hipError_t launch_quant_pack(hipStream_t s, const float* x, const float* sx, int
 
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, float* sx, uint32_t* xq) {
     if (m <= 0) return hipSuccess;
-    if (al16(x)) quantize_rows_kernel<true><<<m, QT, 0, s>>>(x, m, k, sx, xq);
+    const int kg = k / 4;
+    if (al16(x) && kg <= 4 * QT) {
+        if (kg <= QT) quantize_rows_reg_kernel<1><<<m, QT, 0, s>>>(x, m, k, sx, xq);
+        else if (kg <= 2 * QT) quantize_rows_reg_kernel<2><<<m, QT, 0, s>>>(x, m, k, sx, xq);
+        else quantize_rows_reg_kernel<4><<<m, QT, 0, s>>>(x, m, k, sx, xq);
+    } else if (al16(x)) quantize_rows_kernel<true><<<m, QT, 0, s>>>(x, m, k, sx, xq);
     else quantize_rows_kernel<false><<<m, QT, 0, s>>>(x, m, k, sx, xq);
     return hipGetLastError();
 }
