@@ -319,6 +319,15 @@ def main():
 
     d = res["decode"]
     value = d["step_bytes"] / (d["step_ms"] * 1e-3) / 1e9
+    # HBM bytes per GEMV launch from the committed rocprofv3 FETCH_SIZE /
+    # WRITE_SIZE runs of this workload (counters cannot be read live here).
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gemv_traffic.txt")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    traffic = int(line.split(":")[1])
     gemv_gbs = d["gemv_mean_bytes"] / (d["gemv_mean_us"] * 1e-6) / 1e9
     line = {
         "metric": "int8 GEMM TOPS & %peak (prefill); GEMV GB/s & %HBM (decode); vs CPU",
@@ -338,7 +347,7 @@ def main():
                    "weight_pool_mb": round(sum(k * n for k, n in DECODE_KN) * len(DECODE_M) / 1e6, 1),
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "gemv_i8_kernel", "avg_launch_us": round(d["gemv_mean_us"], 2),
                      "avg_algorithmic_bytes": round(d["gemv_mean_bytes"])},
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
