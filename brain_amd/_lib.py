@@ -64,6 +64,7 @@ SIGNATURES = {
     "bh_matmul_i8_static": (i32, [vp, vp, vp, f32, f32, vp, u32, u32, u32]),
     "bh_linear_i8": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
     "bh_quantize_weight_device": (i32, [vp, vp, u32, u32, vp, vp]),
+    "bh_f32_to_bf16": (i32, [vp, vp, vp, C.c_uint64]),
     "bh_roof_mfma_i8": (i32, [vp, u32, u32, vp]),
     "bh_backend_create": (i32, [P(C.c_char_p), P(C.c_char_p), u32, i32, u32, P(vp)]),
     "bh_backend_destroy": (None, [vp]),

@@ -90,6 +90,11 @@ int* splitk_workspace(size_t ints, size_t counters, int** counters_out, hipError
 }
 
 // ---------------------------------------------------------------- small kernels
+__global__ void f32_to_bf16_kernel(const float* x, uint16_t* out, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        out[i] = f32_to_bf16_rne(x[i]);
+}
+
 __global__ void fill_zero_kernel(uint32_t* p, uint64_t n) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
         p[i] = 0u;
@@ -304,6 +309,14 @@ int bh_quantize_weight_device(void* stream, const float* w, uint32_t n, uint32_t
     if (!sw || (k > 0 && (!w || !packed))) return fail(BH_ERR_INVALID, "bh_quantize_weight_device: null buffer");
     return hip_status(launch_quantize_weight((hipStream_t)stream, w, (int)n, (int)k, packed, sw),
                       "quantize_weight launch");
+}
+
+int bh_f32_to_bf16(void* stream, const float* x, uint16_t* out, uint64_t n) {
+    if (n == 0) return BH_OK;
+    if (!x || !out) return fail(BH_ERR_INVALID, "bh_f32_to_bf16: null buffer");
+    const uint64_t blocks = std::min<uint64_t>((n + 255) / 256, 65536);
+    f32_to_bf16_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(x, out, n);
+    return hip_status(hipGetLastError(), "f32_to_bf16 launch");
 }
 
 int bh_roof_mfma_i8(void* stream, uint32_t blocks, uint32_t iters, int32_t* out) {

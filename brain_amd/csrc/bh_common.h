@@ -13,15 +13,19 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 // parity tests use to check the integer sums themselves.
 enum OutDtype : int { OUT_F32 = 0, OUT_BF16 = 1, OUT_I32 = 2 };
 
-// f32 -> bf16 bits, round-to-nearest-even on the discarded 16 bits, NaN kept
-// NaN by forcing the top mantissa bit (same rule as the reference's host
-// converter, crates/model/src/half.rs:49-58).
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-    uint32_t bits = __float_as_uint(f);
-    if ((bits & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((bits >> 16) | 0x0040u);
-    uint32_t bias = 0x7fffu + ((bits >> 16) & 1u);
-    return (uint16_t)((bits + bias) >> 16);
+// f32 -> bf16, round to nearest even, NaN kept as a quiet NaN with the top
+// payload bits ((bits >> 16) | 0x0040), as crates/model/src/half.rs:49-58.
+// gfx950's v_cvt_pk_bf16_f32 produces exactly those bits for every one of the
+// 2^32 inputs (checked exhaustively on MI355X; the GPU tests keep checking the
+// special classes and a large random sample through bh_f32_to_bf16), so the
+// conversion is one instruction per two values.
+typedef __bf16 bh_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float bh_f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    const bh_f32x2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bh_bf16x2));
 }
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) { return (uint16_t)(pack_bf16x2(f, 0.0f) & 0xffffu); }
 
 // The dequant epilogue of matmul_i8_dyn / matmul_i8_gemv: (f32(acc)*sx)*sw,
 // evaluated left to right with no fused multiply-add (the library is built

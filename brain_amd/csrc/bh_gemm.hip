@@ -76,7 +76,6 @@ struct GemmArgs {
     int splits;       // S (1 = no split)
     int* ws;          // [m*n] i32 split-K workspace (zero between calls)
     int* counters;    // [tiles] arrival counters (zero between calls)
-    int dbg;          // tuning only: 1 = skip DMA, 2 = skip MFMA
 };
 
 // One output element through the epilogue.
@@ -450,7 +449,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
         wait_ahead<C::LOADS>(min(nk - 2 - it, STAGES - 3));
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
-        if (it + STAGES - 1 < nk && !(a.dbg & 1)) issue(kt0 + it + STAGES - 1, (it + STAGES - 1) % STAGES);
+        if (it + STAGES - 1 < nk) issue(kt0 + it + STAGES - 1, (it + STAGES - 1) % STAGES);
         const uint8_t* A = lds + (it % STAGES) * C::STAGE;
         const uint8_t* An = lds + ((it + 1) % STAGES) * C::STAGE;
 #pragma unroll
@@ -460,10 +459,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
             // The last k-step reads the next stage's first fragments (on the
             // final iteration that buffer holds stale data that is never used).
             read_frags(ks + 1 < C::KSTEPS ? A : An, ks + 1 < C::KSTEPS ? ks + 1 : 0, fa[nxt], fb[nxt]);
-            if (!(a.dbg & 2)) {
-                mfma_step(fa[cur], fb[cur]);
-                interleave();
-            }
+            mfma_step(fa[cur], fb[cur]);
+            interleave();
             __builtin_amdgcn_sched_barrier(0);
         }
         if constexpr (C::KSTEPS % 2 == 1) {
@@ -517,6 +514,89 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
                     }
             }
             if (t == 0) a.counters[tile_id] = 0;
+        }
+    }
+
+    // Staged epilogue. Written straight from the fragment layout, every store
+    // instruction of a wave would touch 32 rows at 8-16 bytes each; instead
+    // each wave converts one 32-row block of its tile at a time into its own
+    // LDS region (row pitch = tile row + 16 bytes, an odd number of 16-byte
+    // slots, so the 32 lanes of different rows hit distinct banks) and copies
+    // it out as whole 16-byte chunks of consecutive columns, 256 or 512 bytes
+    // of one row per 16/32 lanes. Needs n % 8 == 0 and a 16-byte aligned
+    // output; anything else takes the direct path below.
+    {
+        constexpr int ESZ = (OUT == OUT_BF16) ? 2 : 4;
+        constexpr int EP_PITCH = C::WTN * ESZ + 16;
+        constexpr int EP_REGION = 32 * EP_PITCH;
+        constexpr int EP_CPR = C::WTN * ESZ / 16;  // 16-byte chunks per tile row
+        static_assert(WM * WN * EP_REGION <= STAGES * C::STAGE, "epilogue staging fits in the stage buffers");
+        static_assert((32 * EP_CPR) % 64 == 0, "whole copy-out passes");
+        const bool staged = (!SPLITK || S == 1) && (n % 8) == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15u) == 0 &&
+                            (STATIC || OUT == OUT_I32 || (reinterpret_cast<uintptr_t>(a.sw) & 15u) == 0) &&
+                            (!HAS_BIAS || OUT == OUT_I32 || (reinterpret_cast<uintptr_t>(a.bias) & 15u) == 0);
+        if (staged) {
+            __builtin_amdgcn_s_waitcnt(0);  // every DMA and fragment read has landed
+            __builtin_amdgcn_s_barrier();   // ... in every wave, before the stage buffers are reused
+            uint8_t* reg = lds + wave * EP_REGION;
+            const int lrow = lane & 31;
+            const int wrow0 = row0 + wm * C::WTM, wcol0 = col0 + wn * C::WTN;
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i) {
+                const int row = wrow0 + i * 32 + lrow;
+                float sxm = 0.0f;
+                if constexpr (!STATIC && OUT != OUT_I32) sxm = row < m ? a.sx[row] : 0.0f;
+#pragma unroll
+                for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int lc = j * 32 + 8 * g + 4 * (lane >> 5);
+                        const int col = wcol0 + lc;
+                        const bool live = col < n;  // n % 8 == 0: then col + 3 < n too
+                        const int v0 = acc[i][j][4 * g + 0], v1 = acc[i][j][4 * g + 1];
+                        const int v2 = acc[i][j][4 * g + 2], v3 = acc[i][j][4 * g + 3];
+                        uint8_t* dst = reg + lrow * EP_PITCH + lc * ESZ;
+                        if constexpr (OUT == OUT_I32) {
+                            *reinterpret_cast<v4i*>(dst) = v4i{v0, v1, v2, v3};
+                        } else {
+                            float f0, f1, f2, f3;
+                            if constexpr (STATIC) {
+                                const float sc = a.ssx * a.ssw;
+                                f0 = (float)v0 * sc; f1 = (float)v1 * sc; f2 = (float)v2 * sc; f3 = (float)v3 * sc;
+                            } else {
+                                const float4 swv = live ? *reinterpret_cast<const float4*>(a.sw + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+                                f0 = dequant(v0, sxm, swv.x); f1 = dequant(v1, sxm, swv.y);
+                                f2 = dequant(v2, sxm, swv.z); f3 = dequant(v3, sxm, swv.w);
+                            }
+                            if constexpr (HAS_BIAS) {
+                                const float4 bv = live ? *reinterpret_cast<const float4*>(a.bias + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+                                f0 = f0 + bv.x; f1 = f1 + bv.y; f2 = f2 + bv.z; f3 = f3 + bv.w;
+                            }
+                            if constexpr (OUT == OUT_F32) {
+                                *reinterpret_cast<float4*>(dst) = make_float4(f0, f1, f2, f3);
+                            } else {
+                                const uint32_t lo = pack_bf16x2(f0, f1);
+                                const uint32_t hi = pack_bf16x2(f2, f3);
+                                *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+                            }
+                        }
+                    }
+                // Only this wave reads its region: its LDS operations run in
+                // order, so waiting for its own writes is enough.
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int q0 = 0; q0 < 32 * EP_CPR; q0 += 64) {
+                    const int q = q0 + lane, r = q / EP_CPR, c = q % EP_CPR;
+                    const v4i v = *reinterpret_cast<const v4i*>(reg + r * EP_PITCH + c * 16);
+                    const int grow = wrow0 + i * 32 + r, gcol = wcol0 + c * (16 / ESZ);
+                    if (grow < m && gcol < n)
+                        *reinterpret_cast<v4i*>(reinterpret_cast<uint8_t*>(a.out) + ((int64_t)grow * n + gcol) * ESZ) = v;
+                }
+                __builtin_amdgcn_s_waitcnt(0xC07F);
+                __builtin_amdgcn_wave_barrier();
+            }
+            return;
         }
     }
 
@@ -575,8 +655,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
                         if constexpr (OUT == OUT_F32) {
                             *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + idx) = make_float4(f0, f1, f2, f3);
                         } else {
-                            const uint32_t lo = (uint32_t)f32_to_bf16_rne(f0) | ((uint32_t)f32_to_bf16_rne(f1) << 16);
-                            const uint32_t hi = (uint32_t)f32_to_bf16_rne(f2) | ((uint32_t)f32_to_bf16_rne(f3) << 16);
+                            const uint32_t lo = pack_bf16x2(f0, f1);
+                            const uint32_t hi = pack_bf16x2(f2, f3);
                             *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.out) + idx) = make_uint2(lo, hi);
                         }
                     }
@@ -635,14 +715,6 @@ static hipError_t go_dma(hipStream_t s, const GemmArgs& a) {
     return hipGetLastError();
 }
 
-static int dbg_flags() {
-    static int v = [] {
-        const char* e = getenv("BH_GEMM_DBG");
-        return e ? atoi(e) : 0;
-    }();
-    return v;
-}
-
 // Tuning knob for the large-tile DMA configuration (read once):
 // BH_GEMM_BIG=0: 256x256, 4 waves, DK=64, 4 stages (default)
 // BH_GEMM_BIG=1: 256x128, 4 waves (128x64 each), DK=128, 3 stages
@@ -697,7 +769,7 @@ size_t gemm_workspace_ints(int m, int kg, int n, size_t* counters) {
 
 hipError_t launch_gemm_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n) {
-    GemmArgs a{xq, wq, sx, sw, bias, out, m, kg, n, 0.f, 0.f, 1, nullptr, nullptr, dbg_flags()};
+    GemmArgs a{xq, wq, sx, sw, bias, out, m, kg, n, 0.f, 0.f, 1, nullptr, nullptr};
     const bool al = gemm_aligned(xq, wq, kg);
     const bool dma = al && ((kg * 4) % 128 == 0);
     TileChoice tc = choose_tiles(m, kg, n);
@@ -720,7 +792,7 @@ hipError_t launch_gemm_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
 
 hipError_t launch_gemm_i8_static(hipStream_t s, const uint32_t* xq, const uint32_t* wq, float ssx, float ssw,
                                  float* out, int m, int kg, int n) {
-    GemmArgs a{xq, wq, nullptr, nullptr, nullptr, out, m, kg, n, ssx, ssw, 1, nullptr, nullptr, 0};
+    GemmArgs a{xq, wq, nullptr, nullptr, nullptr, out, m, kg, n, ssx, ssw, 1, nullptr, nullptr};
     TileChoice tc = choose_tiles(m, kg, n);
     tc.splits = 1;  // the static variant stays on plain tiles
     const bool al = gemm_aligned(xq, wq, kg);

@@ -125,6 +125,14 @@ def quantize_weight_device(w):
     return packed, sw
 
 
+def f32_to_bf16(x):
+    """bf16 bit patterns (int16 tensor) of f32 `x`, the library's output rounding (half.rs f32_to_bf16)."""
+    _dev(x)
+    out = torch.empty(x.shape, device=x.device, dtype=torch.int16)
+    check(load().bh_f32_to_bf16(_stream(), _ptr(x), _ptr(out), x.numel()))
+    return out
+
+
 def reserve_workspace(m, k, n, stream=None):
     """Pre-size the split-K workspace of `stream` (default: current) for an
     [m,k] x [n,k] GEMM; required before capturing such a GEMM in a graph."""

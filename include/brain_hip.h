@@ -120,6 +120,11 @@ int bh_linear_i8(void* stream, const float* x, const uint32_t* wq, const float* 
  * packed [n,k/4] u32, sw [n] f32. */
 int bh_quantize_weight_device(void* stream, const float* w, uint32_t n, uint32_t k, uint32_t* packed, float* sw);
 
+/* f32 -> bf16 bits, round to nearest even, NaN -> (bits >> 16) | 0x0040: the
+ * conversion every bf16 output of this library goes through
+ * (crates/model/src/half.rs:49-58, f32_to_bf16). x [n] f32 -> out [n] u16. */
+int bh_f32_to_bf16(void* stream, const float* x, uint16_t* out, uint64_t n);
+
 /* Int8 matrix-core roof probe: `blocks` workgroups of 256 threads each run
  * `iters` rounds of 4 independent v_mfma_i32_32x32x32_i8 chains; out[blocks*256] i32
  * receives a data-dependent sum so nothing folds. Ops executed =

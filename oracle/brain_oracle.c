@@ -130,6 +130,12 @@ uint16_t or_f32_to_bf16(float f) {
     return (uint16_t)((bits + bias) >> 16);
 }
 
+/* or_f32_to_bf16 over an array (the GPU conversion test's expected bits). */
+void or_f32_to_bf16_array(const float* x, uint16_t* out, size_t n) {
+#pragma omp parallel for schedule(static)
+    for (long long i = 0; i < (long long)n; ++i) out[i] = or_f32_to_bf16(x[i]);
+}
+
 void or_epilogue(const int32_t* acc, const float* sx, const float* sw, const float* bias,
                  int64_t m, int64_t n, int out_dtype, void* out) {
     for (int64_t i = 0; i < m; ++i)

@@ -28,6 +28,7 @@
  */
 #ifndef BRAIN_ORACLE_H
 #define BRAIN_ORACLE_H
+#include <stddef.h>
 #include <stdint.h>
 #ifdef __cplusplus
 extern "C" {
@@ -77,6 +78,7 @@ void or_matmul_i8(const uint32_t* xq, const uint32_t* wq, const float* sx, const
 
 /* crates/model/src/half.rs:49-58 */
 uint16_t or_f32_to_bf16(float f);
+void or_f32_to_bf16_array(const float* x, uint16_t* out, size_t n);
 
 /* CPU baseline: backend-cpu's execution of max_abs_row -> quant_pack ->
  * matmul_i8_gemv, restated (one workgroup per output column, 64 invocations

@@ -49,6 +49,7 @@ def lib():
             "or_epilogue_static": (None, [vp, C.c_float, C.c_float, i64, i64, vp]),
             "or_matmul_i8": (None, [vp, vp, vp, vp, vp, i64, i64, i64, i32, vp]),
             "or_f32_to_bf16": (C.c_uint16, [C.c_float]),
+            "or_f32_to_bf16_array": (None, [C.c_void_p, C.c_void_p, C.c_size_t]),
             "or_cpu_linear_gemv": (None, [vp, vp, vp, i64, i64, i64, i32, vp, vp, vp]),
             "or_cpu_gemv_packed": (None, [vp, vp, vp, vp, i64, i64, i64, i32, vp]),
         }
@@ -188,6 +189,14 @@ def matmul_i8(xq, wq, sx, sw, bias=None, out_dtype="f32"):
 
 def f32_to_bf16(f):
     return lib().or_f32_to_bf16(float(f))
+
+
+def f32_to_bf16_array(x):
+    """or_f32_to_bf16 applied to every element of f32 array x -> uint16 bits."""
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().or_f32_to_bf16_array(_p(x), _p(out), x.size)
+    return out
 
 
 def cpu_linear_gemv(x, wq, sw, threads):

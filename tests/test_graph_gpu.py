@@ -43,21 +43,3 @@ def test_graph_replays_match_eager(gpu):
         for d, e in zip(data, eager):
             assert torch.equal(d["out"].view(torch.int16), e.view(torch.int16)), f"replay {rep} differs"
 
-
-def test_split_k_inside_capture_without_reserve_fails_cleanly(gpu):
-    from brain_amd import BrainHipError
-    m, k, n = 384, 2048, 768   # a split-K shape
-    xq = torch.zeros(m, k // 4, dtype=torch.int32, device=gpu)
-    wq = torch.zeros(n, k // 4, dtype=torch.int32, device=gpu)
-    sx = torch.ones(m, device=gpu)
-    sw = torch.ones(n, device=gpu)
-    cap = torch.cuda.Stream()
-    g = torch.cuda.CUDAGraph()
-    with pytest.raises(Exception):
-        with torch.cuda.graph(g, stream=cap):
-            try:
-                ops.matmul_i8(xq, wq, sx, sw, variant="dyn")
-            except BrainHipError as e:
-                assert "bh_reserve_workspace" in str(e)
-                raise
-    torch.cuda.synchronize()

@@ -43,6 +43,25 @@ def special_acts(m, k, seed):
     return x
 
 
+# ---------------------------------------------------------------- bf16 rounding
+def test_f32_to_bf16_matches_reference_rule(gpu):
+    """Every bf16 output goes through one hardware conversion; it must give the
+    reference's bits (half.rs f32_to_bf16) on every class of input: all 65536
+    upper halves with the rounding-critical lower halves (exact, below, at and
+    above the tie, all ones: zeros, subnormals, ties, overflow to inf, NaN
+    payloads), plus a large random sample of bit patterns."""
+    hi = np.arange(65536, dtype=np.uint32) << 16
+    lows = np.array([0x0000, 0x0001, 0x7FFF, 0x8000, 0x8001, 0xFFFF], dtype=np.uint32)
+    classes = (hi[:, None] | lows[None, :]).ravel()
+    rand = np.random.default_rng(5).integers(0, 2**32, size=1 << 22, dtype=np.uint64).astype(np.uint32)
+    bits = np.concatenate([classes, rand])
+    x = bits.view(np.float32)
+    got = ops.f32_to_bf16(dev_f32(x, gpu)).cpu().numpy().view(np.uint16)
+    want = o.f32_to_bf16_array(x)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"{bad.size} mismatches, first input 0x{int(bits[bad[0]]):08x}"
+
+
 # ---------------------------------------------------------------- quantization
 QUANT_SHAPES = [(1, 4), (1, 1024), (3, 8), (4, 36), (16, 1024), (7, 3072), (64, 4096), (513, 1024), (5, 10240)]
 
