@@ -44,6 +44,11 @@ class StatsT(C.Structure):
     _fields_ = [(n, C.c_uint64) for n in ("submits", "dispatches", "readbacks", "bind_groups", "uniform_allocs")]
 
 
+class Qwen3ConfigT(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("vocab", "n_layers", "d_model", "n_heads", "n_kv_heads", "head_dim", "d_ff")] + \
+               [("rope_theta", C.c_float), ("rms_eps", C.c_float), ("tie_embeddings", C.c_uint32), ("qk_norm", C.c_uint32)]
+
+
 class CostT(C.Structure):
     _fields_ = [("flops", C.c_uint64), ("int_ops", C.c_uint64), ("bytes", C.c_uint64)]
 
@@ -66,6 +71,16 @@ SIGNATURES = {
     "bh_quantize_weight_device": (i32, [vp, vp, u32, u32, vp, vp]),
     "bh_f32_to_bf16": (i32, [vp, vp, vp, C.c_uint64]),
     "bh_roof_mfma_i8": (i32, [vp, u32, u32, vp]),
+    "bh_qwen3_create": (i32, [vp, u32, u32, u32, i32, vp]),
+    "bh_qwen3_destroy": (None, [vp]),
+    "bh_qwen3_set_weight": (i32, [vp, C.c_char_p, vp, u64]),
+    "bh_qwen3_set_weight_i8": (i32, [vp, C.c_char_p, vp, vp, u32, u32]),
+    "bh_qwen3_init_random": (i32, [vp, u64]),
+    "bh_qwen3_prefill": (i32, [vp, vp, u32, u32, vp]),
+    "bh_qwen3_decode": (i32, [vp, u32, u32, vp]),
+    "bh_qwen3_logits": (i32, [vp, vp, u64]),
+    "bh_qwen3_lengths": (i32, [vp, vp, u32]),
+    "bh_qwen3_stream": (vp, [vp]),
     "bh_backend_create": (i32, [P(C.c_char_p), P(C.c_char_p), u32, i32, u32, P(vp)]),
     "bh_backend_destroy": (None, [vp]),
     "bh_backend_kind": (C.c_char_p, [vp]),

@@ -145,7 +145,7 @@ __global__ __launch_bounds__(256) void roof_mfma_i8_kernel(uint32_t iters, int32
 // ---------------------------------------------------------------- errors
 static thread_local std::string g_err;
 
-static int fail(int code, const char* fmt, ...) {
+int fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
     va_start(ap, fmt);

@@ -5,6 +5,9 @@
 
 namespace bh {
 
+// Records the message returned by bh_last_error() and returns `code`.
+int fail(int code, const char* fmt, ...);
+
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
@@ -26,6 +29,18 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bh_bf16x2));
 }
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) { return (uint16_t)(pack_bf16x2(f, 0.0f) & 0xffffu); }
+
+// One activation byte of quant_pack (crates/kernels/wgsl/quant_pack.wgsl:36-43):
+// clamp(round_ties_even(v * inv), -127, 127) as two's-complement int8.
+__device__ __forceinline__ uint32_t quant_byte(float v, float inv) {
+    float q = rintf(v * inv);                 // ties to even
+    q = fminf(fmaxf(q, -127.0f), 127.0f);
+    return (uint32_t)((int)q & 0xff);
+}
+__device__ __forceinline__ uint32_t quant_word(float4 v, float inv) {
+    return quant_byte(v.x, inv) | (quant_byte(v.y, inv) << 8) | (quant_byte(v.z, inv) << 16) |
+           (quant_byte(v.w, inv) << 24);
+}
 
 // The dequant epilogue of matmul_i8_dyn / matmul_i8_gemv: (f32(acc)*sx)*sw,
 // evaluated left to right with no fused multiply-add (the library is built

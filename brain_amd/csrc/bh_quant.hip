@@ -43,17 +43,6 @@ __device__ __forceinline__ float row_absmax(const float* __restrict__ row, int k
     return m;
 }
 
-__device__ __forceinline__ uint32_t quant_byte(float v, float inv) {
-    float q = rintf(v * inv);                 // ties to even
-    q = fminf(fmaxf(q, -127.0f), 127.0f);
-    return (uint32_t)((int)q & 0xff);
-}
-
-__device__ __forceinline__ uint32_t quant_word(float4 v, float inv) {
-    return quant_byte(v.x, inv) | (quant_byte(v.y, inv) << 8) | (quant_byte(v.z, inv) << 16) |
-           (quant_byte(v.w, inv) << 24);
-}
-
 template <bool VEC>
 __global__ __launch_bounds__(QT) void max_abs_rows_kernel(const float* __restrict__ x, int m, int k,
                                                           float* __restrict__ sx) {

@@ -1,0 +1,961 @@
+// The int8 Qwen3 decoder on gfx950: the host step tape of
+// qwen3::serve::Engine (crates/qwen3/src/serve.rs:1194-1310) with int8
+// weights, rebuilt around fused row kernels, the library's int8 GEMV/GEMM, and
+// one HIP graph per decode step.
+//
+// Per layer (rows = tokens in flight; decode: one per sequence, prefill: one
+// per prompt position):
+//   norm_quant      [residual add +] RMSNorm + per-token int8 quant of the
+//                   result (rmsnorm_rows.wgsl + max_abs_row + quant_pack)
+//   linear qkv      one int8 linear over the q|k|v weights stacked by rows
+//                   (the reference runs three; per-row weight scales make the
+//                   stacked product column-for-column identical)
+//   qk_rope_append  per head: QK-norm, RoPE (rope_paged.wgsl), K/V append
+//   attention       causal GQA over the f32 cache, one workgroup per
+//                   (row, kv head): scores, softmax, weighted V
+//                   (paged_decode_scores_wg / decode_softmax_batched /
+//                   paged_decode_apply_batched)
+//   quantize ctx    -> linear o
+//   norm_quant      residual add + RMSNorm + quant
+//   linear gate|up  stacked like qkv
+//   swiglu_quant    silu(g)*u (silu_mul.wgsl) + quant
+//   linear down     (its residual add is fused into the next norm_quant)
+// then norm_quant (final norm, only the rows whose logits are wanted), the
+// int8 head and a two-stage greedy argmax that also advances the position and
+// records the token, so decode steps chain on the device.
+//
+// The attention reductions, RMSNorm sums and transcendental functions are
+// evaluated in a different order / with different libm than the reference's
+// shaders, so activations agree to f32 rounding, not bit for bit; every int8
+// linear is the bit-exact path of the rest of the library.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/brain_hip.h"
+#include "bh_common.h"
+
+namespace bh {
+hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, float* sx, uint32_t* xq);
+hipError_t launch_quantize_weight(hipStream_t s, const float* w, int n, int k, uint32_t* packed, float* sw);
+hipError_t launch_gemv_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
+                          const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n);
+hipError_t launch_gemm_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
+                          const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n);
+
+namespace {
+
+constexpr int RT = 256;       // threads of the row kernels
+constexpr int AM_CH = 64;     // argmax chunks per row
+constexpr int MAX_GROUP = 8;  // query heads per kv head
+constexpr uint32_t NO_INDEX = 0xffffffffu;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+// Block-wide reductions over RT threads; `red` holds RT/64 floats. Safe to
+// call back to back (the leading barrier retires the previous use of red).
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = red[0];
+#pragma unroll
+    for (int w = 1; w < RT / 64; ++w) s += red[w];
+    return s;
+}
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = red[0];
+#pragma unroll
+    for (int w = 1; w < RT / 64; ++w) s = fmaxf(s, red[w]);
+    return s;
+}
+
+__device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
+__device__ __forceinline__ float absmax4(float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); }
+
+// Per-token quantization of a row held in registers (G float4 per thread):
+// sx = max(max|y|, 1e-8)/127, q = clamp(rne(y * (1/sx))) as quant_pack.
+template <int G>
+__device__ __forceinline__ void quant_row(const float4 (&y)[G], int d4, float* red, float* sx, uint32_t* xq) {
+    float am = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        if (threadIdx.x + g * RT < d4) am = fmaxf(am, absmax4(y[g]));
+    am = block_max(am, red);
+    const float s = fmaxf(am, 1e-8f) / 127.0f;
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int i = threadIdx.x + g * RT;
+        if (i < d4) xq[i] = quant_word(y[g], inv);
+    }
+    if (threadIdx.x == 0) *sx = s;
+}
+
+struct NormQuantArgs {
+    const float* a;        // x = a[ir] (+ b[ir]) ...
+    const float* b;
+    const uint32_t* tok;   // ... or x = emb[tok[ir]]
+    const float* emb;
+    const int* row_map;    // ir = row_map[r] (null: ir = r)
+    float* res_out;        // x written back at row ir (may alias a)
+    const float* w;        // RMSNorm gain [d]
+    float eps;
+    int d;
+    float* sx;             // [rows]
+    uint32_t* xq;          // [rows, xq_words]
+    int xq_words;
+};
+
+// rmsnorm_rows.wgsl:24-44 (y = x * (1/sqrt(mean(x^2) + eps)) * w) on x = a + b
+// (add2.wgsl) or an embedding row (embed.wgsl), then the row's int8 quant.
+template <int G>
+__global__ __launch_bounds__(RT) void norm_quant_kernel(NormQuantArgs p) {
+    __shared__ float red[RT / 64];
+    const int r = blockIdx.x;
+    const int ir = p.row_map ? p.row_map[r] : r;
+    const int d4 = p.d >> 2;
+    const float4* src = p.tok ? reinterpret_cast<const float4*>(p.emb + (size_t)p.tok[ir] * p.d)
+                              : reinterpret_cast<const float4*>(p.a + (size_t)ir * p.d);
+    const float4* add = p.b ? reinterpret_cast<const float4*>(p.b + (size_t)ir * p.d) : nullptr;
+    float4 x[G];
+    float ss = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int i = threadIdx.x + g * RT;
+        x[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i < d4) {
+            float4 v = src[i];
+            if (add) v = add4(v, add[i]);
+            x[g] = v;
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+    }
+    if (p.res_out) {
+        float4* o = reinterpret_cast<float4*>(p.res_out + (size_t)ir * p.d);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int i = threadIdx.x + g * RT;
+            if (i < d4) o[i] = x[g];
+        }
+    }
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)p.d + p.eps);
+    const float4* w4 = reinterpret_cast<const float4*>(p.w);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int i = threadIdx.x + g * RT;
+        if (i < d4) {
+            const float4 wv = w4[i];
+            x[g] = make_float4(x[g].x * inv * wv.x, x[g].y * inv * wv.y, x[g].z * inv * wv.z, x[g].w * inv * wv.w);
+        }
+    }
+    quant_row<G>(x, d4, red, p.sx + r, p.xq + (size_t)r * p.xq_words);
+}
+
+// silu_mul.wgsl (h = g / (1 + exp(-g)) * u) over the stacked gate|up output,
+// then the row's int8 quant.
+template <int G>
+__global__ __launch_bounds__(RT) void swiglu_quant_kernel(const float* gu, int ff, float* sx, uint32_t* xq, int xq_words) {
+    __shared__ float red[RT / 64];
+    const int r = blockIdx.x;
+    const int d4 = ff >> 2;
+    const float4* g4 = reinterpret_cast<const float4*>(gu + (size_t)r * 2 * ff);
+    const float4* u4 = g4 + d4;
+    float4 h[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int i = threadIdx.x + g * RT;
+        h[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i < d4) {
+            const float4 a = g4[i], b = u4[i];
+            h[g] = make_float4(a.x / (1.0f + expf(-a.x)) * b.x, a.y / (1.0f + expf(-a.y)) * b.y,
+                               a.z / (1.0f + expf(-a.z)) * b.z, a.w / (1.0f + expf(-a.w)) * b.w);
+        }
+    }
+    quant_row<G>(h, d4, red, sx + r, xq + (size_t)r * xq_words);
+}
+
+struct RopeArgs {
+    const float* qkv;  // [rows, hq + 2 hkv]
+    float* q;          // [rows, hq]
+    float* kc;         // this layer's K cache [max_batch, max_seq, hkv]
+    float* vc;
+    const float* qn;   // q_norm / k_norm gains [hd]
+    const float* kn;
+    const uint32_t* pos;
+    const uint32_t* seq;
+    int nh, nkv, hd, hq, hkv, max_seq, qk_norm;
+    float eps, theta;
+};
+
+// One wave per (row, head): heads [0,nh) are queries, [nh, nh+nkv) keys,
+// [nh+nkv, nh+2nkv) values. Queries and keys get the per-head RMSNorm and the
+// rotate-half RoPE of rope_paged.wgsl:27-38 (pair (m, m+hd/2), angle
+// pos * theta^(-2m/hd)); keys and values land in the cache at (seq, pos)
+// (paged_kv_append_batched.wgsl with a contiguous slab per sequence).
+__global__ __launch_bounds__(64) void qk_rope_append_kernel(RopeArgs p) {
+    const int r = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int W = p.hq + 2 * p.hkv, half = p.hd >> 1;
+    const uint32_t pos = p.pos[r];
+    const size_t slot = ((size_t)p.seq[r] * p.max_seq + pos) * p.hkv;
+    const float* src;
+    float* dst;
+    const float* nw;
+    if (h < p.nh) {
+        src = p.qkv + (size_t)r * W + h * p.hd;
+        dst = p.q + (size_t)r * p.hq + h * p.hd;
+        nw = p.qn;
+    } else if (h < p.nh + p.nkv) {
+        const int kh = h - p.nh;
+        src = p.qkv + (size_t)r * W + p.hq + kh * p.hd;
+        dst = p.kc + slot + kh * p.hd;
+        nw = p.kn;
+    } else {
+        const int kh = h - p.nh - p.nkv;
+        src = p.qkv + (size_t)r * W + p.hq + p.hkv + kh * p.hd;
+        dst = p.vc + slot + kh * p.hd;
+        for (int i = lane; i < p.hd; i += 64) dst[i] = src[i];
+        return;
+    }
+    float x0[2], x1[2];
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int m = lane + 64 * u;
+        x0[u] = x1[u] = 0.0f;
+        if (m < half) {
+            x0[u] = src[m];
+            x1[u] = src[m + half];
+            ss += x0[u] * x0[u] + x1[u] * x1[u];
+        }
+    }
+    float inv = 1.0f;
+    if (p.qk_norm) {
+        ss = wave_sum(ss);
+        inv = 1.0f / sqrtf(ss / (float)p.hd + p.eps);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int m = lane + 64 * u;
+        if (m >= half) continue;
+        float a = x0[u], b = x1[u];
+        if (p.qk_norm) {
+            a = a * inv * nw[m];
+            b = b * inv * nw[m + half];
+        }
+        const float angle = (float)pos * powf(p.theta, -(float)(2 * m) / (float)p.hd);
+        const float c = cosf(angle), s = sinf(angle);
+        dst[m] = a * c - b * s;
+        dst[m + half] = b * c + a * s;
+    }
+}
+
+struct AttnArgs {
+    const float* q;    // [rows, hq]
+    const float* kc;   // this layer's caches
+    const float* vc;
+    const uint32_t* pos;
+    const uint32_t* seq;
+    float* ctx;        // [rows, hq]
+    int nh, nkv, hd, hq, hkv, max_seq;
+    int sstride;  // LDS floats per query head's scores: max_seq rounded up to 4 (keeps qs 16-byte aligned)
+    float scale;
+};
+
+// Causal GQA for one (row, kv head): the row attends positions 0..pos of its
+// sequence. Scores q.k * scale for every query head of the group (16 lanes per
+// key, float4 loads along head_dim), softmax with the max subtracted, then
+// ctx = sum_j p_j v_j. LDS: scores [group][max_seq] + queries [group][hd].
+__global__ __launch_bounds__(RT) void attention_kernel(AttnArgs p) {
+    extern __shared__ float sm[];
+    __shared__ float red[RT / 64];
+    const int r = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x;
+    const int G = p.nh / p.nkv;
+    const int t = (int)p.pos[r] + 1;
+    float* s = sm;
+    float* qs = sm + (size_t)G * p.sstride;
+    for (int i = tid; i < G * p.hd; i += RT) qs[i] = p.q[(size_t)r * p.hq + (size_t)kh * G * p.hd + i];
+    __syncthreads();
+    const size_t base = (size_t)p.seq[r] * p.max_seq * p.hkv + (size_t)kh * p.hd;
+    const float* Kb = p.kc + base;
+    const float* Vb = p.vc + base;
+    const int li = tid & 15, slot = tid >> 4;
+    for (int j = slot; j < t; j += RT / 16) {
+        const float* kr = Kb + (size_t)j * p.hkv;
+        float acc[MAX_GROUP];
+#pragma unroll
+        for (int g = 0; g < MAX_GROUP; ++g) acc[g] = 0.0f;
+        for (int c = li * 4; c < p.hd; c += 64) {
+            const float4 kv = *reinterpret_cast<const float4*>(kr + c);
+#pragma unroll
+            for (int g = 0; g < MAX_GROUP; ++g) {
+                if (g >= G) break;
+                const float4 qv = *reinterpret_cast<const float4*>(qs + g * p.hd + c);
+                acc[g] += qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < MAX_GROUP; ++g) {
+            if (g >= G) break;
+            float v = acc[g];
+            v += __shfl_xor(v, 8, 64);
+            v += __shfl_xor(v, 4, 64);
+            v += __shfl_xor(v, 2, 64);
+            v += __shfl_xor(v, 1, 64);
+            if (li == 0) s[(size_t)g * p.sstride + j] = v * p.scale;
+        }
+    }
+    __syncthreads();
+    for (int g = 0; g < G; ++g) {
+        float* sg = s + (size_t)g * p.sstride;
+        float mx = -3.4e38f;
+        for (int j = tid; j < t; j += RT) mx = fmaxf(mx, sg[j]);
+        mx = block_max(mx, red);
+        float sum = 0.0f;
+        for (int j = tid; j < t; j += RT) sum += expf(sg[j] - mx);
+        sum = block_sum(sum, red);
+        const float inv = 1.0f / sum;
+        for (int j = tid; j < t; j += RT) sg[j] = expf(sg[j] - mx) * inv;
+    }
+    __syncthreads();
+    for (int i = tid; i < G * p.hd; i += RT) {
+        const int g = i / p.hd, d = i - g * p.hd;
+        const float* pg = s + (size_t)g * p.sstride;
+        float acc = 0.0f;
+        for (int j = 0; j < t; ++j) acc += pg[j] * Vb[(size_t)j * p.hkv + d];
+        p.ctx[(size_t)r * p.hq + (size_t)(kh * G + g) * p.hd + d] = acc;
+    }
+}
+
+// Greedy argmax, stage 1: chunk c of row b -> (value, index) with the
+// argmax_row.wgsl rule (first index of the largest value strictly above
+// -FLT_MAX; NaN never wins).
+__device__ __forceinline__ bool am_better(float v, uint32_t i, float bv, uint32_t bi) {
+    if (i == NO_INDEX) return false;
+    if (bi == NO_INDEX) return true;
+    return v > bv || (v == bv && i < bi);
+}
+__device__ __forceinline__ void am_wave(float& v, uint32_t& i) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(v, off, 64);
+        const uint32_t oi = __shfl_xor(i, off, 64);
+        if (am_better(ov, oi, v, i)) {
+            v = ov;
+            i = oi;
+        }
+    }
+}
+__global__ __launch_bounds__(RT) void argmax_part_kernel(const float* logits, int vocab, float* pv, uint32_t* pi) {
+    __shared__ float rv[RT / 64];
+    __shared__ uint32_t ri[RT / 64];
+    const int b = blockIdx.y, c = blockIdx.x;
+    const int chunk = (vocab + AM_CH - 1) / AM_CH;
+    const int lo = c * chunk, hi = min(vocab, lo + chunk);
+    const float* row = logits + (size_t)b * vocab;
+    float bv = -FLT_MAX;
+    uint32_t bi = NO_INDEX;
+    for (int j = lo + threadIdx.x; j < hi; j += RT) {
+        const float v = row[j];
+        if (v > bv) {
+            bv = v;
+            bi = (uint32_t)j;
+        }
+    }
+    am_wave(bv, bi);
+    if ((threadIdx.x & 63) == 0) {
+        rv[threadIdx.x >> 6] = bv;
+        ri[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < RT / 64; ++w)
+            if (am_better(rv[w], ri[w], bv, bi)) {
+                bv = rv[w];
+                bi = ri[w];
+            }
+        pv[b * AM_CH + c] = bv;
+        pi[b * AM_CH + c] = bi;
+    }
+}
+
+// Stage 2: fold the chunks; tok[b] = winner (0 when nothing beat -FLT_MAX, as
+// argmax_row.wgsl). With `hist`, also record the token at generation index
+// pos[b] - ctl[0] and advance pos[b] (decode_feed / decode_advance).
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float* pv, const uint32_t* pi, uint32_t* tok,
+                                                          uint32_t* pos, uint32_t* hist, const uint32_t* ctl,
+                                                          int batch) {
+    const int b = blockIdx.x, lane = threadIdx.x;
+    float v = pv[b * AM_CH + lane];
+    uint32_t i = pi[b * AM_CH + lane];
+    am_wave(v, i);
+    if (lane == 0) {
+        const uint32_t idx = i == NO_INDEX ? 0u : i;
+        tok[b] = idx;
+        if (hist) {
+            const uint32_t p = pos[b];
+            const uint32_t k = p - ctl[0];
+            if (k < ctl[1]) hist[(size_t)k * batch + b] = idx;
+            pos[b] = p + 1;
+        }
+    }
+}
+
+// Counter-based normal generator for the random init: SplitMix64 of
+// (key + i), two 24-bit uniforms, Box-Muller.
+__device__ __forceinline__ uint64_t splitmix(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+__global__ void init_normal_kernel(float* w, size_t n, uint64_t key, float stdv) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const uint64_t z = splitmix(key + i);
+        const float u1 = (float)((z >> 40) + 1) * (1.0f / 16777216.0f);
+        const float u2 = (float)((z >> 16) & 0xffffffull) * (1.0f / 16777216.0f);
+        w[i] = sqrtf(-2.0f * logf(u1)) * cosf(6.28318530718f * u2) * stdv;
+    }
+}
+__global__ void fill_kernel(float* w, size_t n, float v) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) w[i] = v;
+}
+
+unsigned grid_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 8192); }
+
+}  // namespace
+}  // namespace bh
+
+using namespace bh;
+
+struct bh_qwen3 {
+    bh_qwen3_config c{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    uint32_t max_batch = 0, max_seq = 0, max_rows = 0;
+    uint32_t hq = 0, hkv = 0, W = 0, xq_words = 0;
+
+    struct Layer {
+        float *ln1, *ln2, *qn, *kn;
+        uint32_t *wqkv, *wo, *wgu, *wdown;
+        float *sqkv, *so, *sgu, *sdown;
+    };
+    std::vector<Layer> L;
+    float* emb = nullptr;
+    float* norm = nullptr;
+    uint32_t* head = nullptr;
+    float* shead = nullptr;
+    float *kc = nullptr, *vc = nullptr;
+    size_t layer_kv = 0;  // floats per layer per cache
+
+    float *res = nullptr, *qkv = nullptr, *q = nullptr, *ctx = nullptr, *proj = nullptr, *gu = nullptr;
+    float *sx = nullptr, *logits = nullptr, *tmpw = nullptr, *am_v = nullptr;
+    uint32_t *xq = nullptr, *am_i = nullptr;  // xq: every producer writes rows of width/4 words
+    uint32_t *tok_rows = nullptr, *pos_rows = nullptr, *seq_rows = nullptr;
+    int* row_map = nullptr;
+    uint32_t *tok_dec = nullptr, *pos_dec = nullptr, *seq_dec = nullptr, *hist = nullptr, *ctl = nullptr;
+    size_t tmpw_floats = 0;
+
+    uint32_t batch = 0, prompt_len = 0, decoded = 0;
+    hipGraphExec_t graph = nullptr;
+    uint32_t graph_batch = 0;
+    std::vector<void*> allocs;
+
+    ~bh_qwen3() {
+        (void)hipSetDevice(device);
+        if (graph) (void)hipGraphExecDestroy(graph);
+        if (stream) (void)hipStreamSynchronize(stream);
+        for (void* p : allocs) (void)hipFree(p);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+};
+
+namespace {
+
+template <typename T>
+int dalloc(bh_qwen3* e, T** p, size_t count) {
+    void* v = nullptr;
+    const size_t bytes = std::max<size_t>(count * sizeof(T), 256);
+    if (hipMalloc(&v, bytes) != hipSuccess) return fail(BH_ERR_NOMEM, "bh_qwen3: hipMalloc of %zu bytes failed", bytes);
+    e->allocs.push_back(v);
+    if (hipMemset(v, 0, bytes) != hipSuccess) return fail(BH_ERR_HIP, "bh_qwen3: hipMemset failed");
+    *p = static_cast<T*>(v);
+    return BH_OK;
+}
+
+#define BH_TRY(x)                 \
+    do {                          \
+        int _rc = (x);            \
+        if (_rc != BH_OK) return _rc; \
+    } while (0)
+#define BH_HIP(x, what)                                                                        \
+    do {                                                                                       \
+        hipError_t _e = (x);                                                                   \
+        if (_e != hipSuccess) return fail(BH_ERR_HIP, "bh_qwen3: %s: %s", what, hipGetErrorString(_e)); \
+    } while (0)
+
+int launch_linear(bh_qwen3* e, const uint32_t* w, const float* sw, float* out, int m, int k, int n) {
+    hipError_t err = m <= 32 ? launch_gemv_i8(e->stream, e->xq, w, e->sx, sw, nullptr, out, OUT_F32, m, k / 4, n)
+                             : launch_gemm_i8(e->stream, e->xq, w, e->sx, sw, nullptr, out, OUT_F32, m, k / 4, n);
+    BH_HIP(err, "int8 linear launch");
+    return BH_OK;
+}
+
+int launch_norm_quant(bh_qwen3* e, const NormQuantArgs& a, int rows) {
+    const int groups = (a.d / 4 + RT - 1) / RT;
+    if (groups <= 1) norm_quant_kernel<1><<<rows, RT, 0, e->stream>>>(a);
+    else if (groups <= 2) norm_quant_kernel<2><<<rows, RT, 0, e->stream>>>(a);
+    else if (groups <= 4) norm_quant_kernel<4><<<rows, RT, 0, e->stream>>>(a);
+    else norm_quant_kernel<8><<<rows, RT, 0, e->stream>>>(a);
+    BH_HIP(hipGetLastError(), "norm_quant launch");
+    return BH_OK;
+}
+
+int launch_swiglu_quant(bh_qwen3* e, int rows) {
+    const int ff = (int)e->c.d_ff;
+    const int groups = (ff / 4 + RT - 1) / RT;
+    if (groups <= 1) swiglu_quant_kernel<1><<<rows, RT, 0, e->stream>>>(e->gu, ff, e->sx, e->xq, ff / 4);
+    else if (groups <= 2) swiglu_quant_kernel<2><<<rows, RT, 0, e->stream>>>(e->gu, ff, e->sx, e->xq, ff / 4);
+    else if (groups <= 4) swiglu_quant_kernel<4><<<rows, RT, 0, e->stream>>>(e->gu, ff, e->sx, e->xq, ff / 4);
+    else swiglu_quant_kernel<8><<<rows, RT, 0, e->stream>>>(e->gu, ff, e->sx, e->xq, ff / 4);
+    BH_HIP(hipGetLastError(), "swiglu_quant launch");
+    return BH_OK;
+}
+
+// The layer stack over `rows` token rows (tok/pos/seq per row), then, if
+// n_out > 0, the final norm of rows out_map[0..n_out) (null: rows 0..n_out),
+// the head and the argmax into tok_dec (advancing pos_dec and recording into
+// hist when `decode`).
+int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, const uint32_t* seq, int n_out,
+             const int* out_map, bool decode) {
+    const bh_qwen3_config& c = e->c;
+    const int d = (int)c.d_model, ff = (int)c.d_ff, hd = (int)c.head_dim;
+    const int nh = (int)c.n_heads, nkv = (int)c.n_kv_heads, G = nh / nkv;
+    const float scale = 1.0f / sqrtf((float)hd);
+    const int sstride = (int)((e->max_seq + 3) & ~3u);
+    const size_t attn_lds = ((size_t)G * sstride + (size_t)G * hd) * sizeof(float);
+    for (uint32_t l = 0; l < c.n_layers; ++l) {
+        const bh_qwen3::Layer& Ly = e->L[l];
+        float* kc = e->kc + l * e->layer_kv;
+        float* vc = e->vc + l * e->layer_kv;
+        NormQuantArgs na{};
+        if (l == 0) {
+            na.tok = tok;
+            na.emb = e->emb;
+        } else {
+            na.a = e->res;
+            na.b = e->proj;  // previous layer's down projection
+        }
+        na.res_out = e->res;
+        na.w = Ly.ln1;
+        na.eps = c.rms_eps;
+        na.d = d;
+        na.sx = e->sx;
+        na.xq = e->xq;
+        na.xq_words = d / 4;
+        BH_TRY(launch_norm_quant(e, na, rows));
+        BH_TRY(launch_linear(e, Ly.wqkv, Ly.sqkv, e->qkv, rows, d, (int)e->W));
+        RopeArgs ra{e->qkv, e->q, kc, vc, Ly.qn, Ly.kn, pos, seq, nh, nkv, hd, (int)e->hq, (int)e->hkv,
+                    (int)e->max_seq, (int)c.qk_norm, c.rms_eps, c.rope_theta};
+        qk_rope_append_kernel<<<dim3(rows, nh + 2 * nkv), 64, 0, e->stream>>>(ra);
+        BH_HIP(hipGetLastError(), "qk_rope_append launch");
+        AttnArgs aa{e->q, kc, vc, pos, seq, e->ctx, nh, nkv, hd, (int)e->hq, (int)e->hkv, (int)e->max_seq, sstride, scale};
+        attention_kernel<<<dim3(rows, nkv), RT, attn_lds, e->stream>>>(aa);
+        BH_HIP(hipGetLastError(), "attention launch");
+        BH_HIP(launch_quantize_rows(e->stream, e->ctx, rows, (int)e->hq, e->sx, e->xq), "quantize ctx");
+        BH_TRY(launch_linear(e, Ly.wo, Ly.so, e->proj, rows, (int)e->hq, d));
+        NormQuantArgs nb{};
+        nb.a = e->res;
+        nb.b = e->proj;
+        nb.res_out = e->res;
+        nb.w = Ly.ln2;
+        nb.eps = c.rms_eps;
+        nb.d = d;
+        nb.sx = e->sx;
+        nb.xq = e->xq;
+        nb.xq_words = d / 4;
+        BH_TRY(launch_norm_quant(e, nb, rows));
+        BH_TRY(launch_linear(e, Ly.wgu, Ly.sgu, e->gu, rows, d, 2 * ff));
+        BH_TRY(launch_swiglu_quant(e, rows));
+        BH_TRY(launch_linear(e, Ly.wdown, Ly.sdown, e->proj, rows, ff, d));
+    }
+    if (n_out <= 0) return BH_OK;
+    NormQuantArgs nf{};
+    nf.a = e->res;
+    nf.b = e->proj;
+    nf.row_map = out_map;
+    nf.w = e->norm;
+    nf.eps = c.rms_eps;
+    nf.d = d;
+    nf.sx = e->sx;
+    nf.xq = e->xq;
+    nf.xq_words = d / 4;
+    BH_TRY(launch_norm_quant(e, nf, n_out));
+    BH_TRY(launch_linear(e, e->head, e->shead, e->logits, n_out, d, (int)c.vocab));
+    argmax_part_kernel<<<dim3(AM_CH, n_out), RT, 0, e->stream>>>(e->logits, (int)c.vocab, e->am_v, e->am_i);
+    BH_HIP(hipGetLastError(), "argmax_part launch");
+    argmax_final_kernel<<<n_out, 64, 0, e->stream>>>(e->am_v, e->am_i, e->tok_dec, e->pos_dec,
+                                                     decode ? e->hist : nullptr, e->ctl, n_out);
+    BH_HIP(hipGetLastError(), "argmax_final launch");
+    return BH_OK;
+}
+
+int quantize_into(bh_qwen3* e, const float* dev_w, uint32_t n, uint32_t k, uint32_t* packed, float* sw) {
+    BH_HIP(launch_quantize_weight(e->stream, dev_w, (int)n, (int)k, packed, sw), "weight quantization");
+    return BH_OK;
+}
+
+// Where a named parameter lives: f32 destination (norm gains, embedding) or
+// an int8 slice (packed rows + scales) of a stacked weight.
+struct Target {
+    float* f32 = nullptr;
+    uint32_t* packed = nullptr;
+    float* scale = nullptr;
+    uint64_t n = 0, k = 0;  // int8: rows x cols; f32: numel in n
+    bool is_emb = false;
+    float init_std = 0.0f;  // random init: 0 -> gain of 1
+};
+
+int resolve(bh_qwen3* e, const std::string& name, Target* t) {
+    const bh_qwen3_config& c = e->c;
+    const uint64_t d = c.d_model, ff = c.d_ff, hq = e->hq, hkv = e->hkv, hd = c.head_dim;
+    const float std0 = 0.02f, stdp = 0.02f / sqrtf(2.0f * (float)c.n_layers);
+    if (name == "tok.weight") {
+        t->f32 = e->emb;
+        t->n = (uint64_t)c.vocab * d;
+        t->is_emb = true;
+        t->init_std = std0;
+        return BH_OK;
+    }
+    if (name == "norm.weight") {
+        t->f32 = e->norm;
+        t->n = d;
+        return BH_OK;
+    }
+    if (name == "lm_head.weight") {
+        if (c.tie_embeddings) return fail(BH_ERR_INVALID, "bh_qwen3: lm_head.weight with tied embeddings");
+        t->packed = e->head;
+        t->scale = e->shead;
+        t->n = c.vocab;
+        t->k = d;
+        t->init_std = std0;
+        return BH_OK;
+    }
+    unsigned l = 0;
+    int used = 0;
+    char rest[64] = {0};
+    if (sscanf(name.c_str(), "blocks.%u.%63s%n", &l, rest, &used) != 2 || l >= c.n_layers || (size_t)used != name.size())
+        return fail(BH_ERR_INVALID, "bh_qwen3: unknown parameter '%s'", name.c_str());
+    bh_qwen3::Layer& Ly = e->L[l];
+    const std::string s(rest);
+    auto lin = [&](uint32_t* base, float* sbase, uint64_t row0, uint64_t n, uint64_t k, float sd) {
+        t->packed = base + row0 * (k / 4);
+        t->scale = sbase + row0;
+        t->n = n;
+        t->k = k;
+        t->init_std = sd;
+        return BH_OK;
+    };
+    if (s == "ln1.weight") { t->f32 = Ly.ln1; t->n = d; return BH_OK; }
+    if (s == "ln2.weight") { t->f32 = Ly.ln2; t->n = d; return BH_OK; }
+    if (s == "attn.q_norm.weight") { t->f32 = Ly.qn; t->n = hd; return BH_OK; }
+    if (s == "attn.k_norm.weight") { t->f32 = Ly.kn; t->n = hd; return BH_OK; }
+    if (s == "attn.wq.weight") return lin(Ly.wqkv, Ly.sqkv, 0, hq, d, std0);
+    if (s == "attn.wk.weight") return lin(Ly.wqkv, Ly.sqkv, hq, hkv, d, std0);
+    if (s == "attn.wv.weight") return lin(Ly.wqkv, Ly.sqkv, hq + hkv, hkv, d, std0);
+    if (s == "attn.wo.weight") return lin(Ly.wo, Ly.so, 0, d, hq, stdp);
+    if (s == "mlp.gate.weight") return lin(Ly.wgu, Ly.sgu, 0, ff, d, std0);
+    if (s == "mlp.up.weight") return lin(Ly.wgu, Ly.sgu, ff, ff, d, std0);
+    if (s == "mlp.down.weight") return lin(Ly.wdown, Ly.sdown, 0, d, ff, stdp);
+    return fail(BH_ERR_INVALID, "bh_qwen3: unknown parameter '%s'", name.c_str());
+}
+
+std::vector<std::string> param_names(const bh_qwen3_config& c) {
+    std::vector<std::string> v;
+    static const char* per_layer[] = {"ln1.weight", "attn.wq.weight", "attn.wk.weight", "attn.wv.weight",
+                                      "attn.q_norm.weight", "attn.k_norm.weight", "attn.wo.weight", "ln2.weight",
+                                      "mlp.gate.weight", "mlp.up.weight", "mlp.down.weight"};
+    for (uint32_t l = 0; l < c.n_layers; ++l)
+        for (const char* s : per_layer) v.push_back("blocks." + std::to_string(l) + "." + s);
+    v.push_back("norm.weight");
+    v.push_back("tok.weight");
+    if (!c.tie_embeddings) v.push_back("lm_head.weight");
+    return v;
+}
+
+uint64_t splitmix_host(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+uint64_t fnv1a(const std::string& s) {
+    uint64_t h = 0xcbf29ce484222325ull;
+    for (unsigned char ch : s) h = (h ^ ch) * 0x100000001b3ull;
+    return h;
+}
+
+int sync(bh_qwen3* e) {
+    BH_HIP(hipStreamSynchronize(e->stream), "stream synchronize");
+    return BH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int bh_qwen3_create(const bh_qwen3_config* cfg, uint32_t max_batch, uint32_t max_seq, uint32_t max_rows, int device,
+                    bh_qwen3** out) {
+    if (!cfg || !out) return fail(BH_ERR_INVALID, "bh_qwen3_create: null argument");
+    *out = nullptr;
+    const bh_qwen3_config& c = *cfg;
+    if (!c.vocab || !c.n_layers || !c.d_model || !c.n_heads || !c.n_kv_heads || !c.head_dim || !c.d_ff)
+        return fail(BH_ERR_INVALID, "bh_qwen3_create: zero dimension");
+    if (c.head_dim % 64 || c.head_dim > 256 || c.n_heads % c.n_kv_heads || c.n_heads / c.n_kv_heads > MAX_GROUP)
+        return fail(BH_ERR_INVALID, "bh_qwen3_create: head_dim %u / heads %u / kv heads %u unsupported", c.head_dim,
+                    c.n_heads, c.n_kv_heads);
+    const uint64_t hq = (uint64_t)c.n_heads * c.head_dim;
+    if (c.d_model % 4 || c.d_ff % 4 || c.d_model > 8192 || c.d_ff > 8192 || hq > 8192)
+        return fail(BH_ERR_INVALID, "bh_qwen3_create: widths must be multiples of 4 and <= 8192");
+    if (!max_batch || !max_seq || max_rows < max_batch)
+        return fail(BH_ERR_INVALID, "bh_qwen3_create: max_batch %u max_seq %u max_rows %u", max_batch, max_seq, max_rows);
+    const uint64_t G = c.n_heads / c.n_kv_heads;
+    if ((G * ((max_seq + 3) & ~3u) + G * c.head_dim) * 4 > 64 * 1024)
+        return fail(BH_ERR_INVALID, "bh_qwen3_create: max_seq %u too long for the attention kernel's LDS", max_seq);
+    if (hipSetDevice(device) != hipSuccess) return fail(BH_ERR_HIP, "bh_qwen3_create: hipSetDevice(%d)", device);
+    bh_qwen3* e = new bh_qwen3();
+    e->c = c;
+    e->device = device;
+    e->max_batch = max_batch;
+    e->max_seq = max_seq;
+    e->max_rows = max_rows;
+    e->hq = (uint32_t)hq;
+    e->hkv = c.n_kv_heads * c.head_dim;
+    e->W = e->hq + 2 * e->hkv;
+    e->xq_words = std::max(std::max(c.d_model, e->hq), c.d_ff) / 4;
+    auto bail = [&](int rc) {
+        delete e;
+        return rc;
+    };
+    if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess)
+        return bail(fail(BH_ERR_HIP, "bh_qwen3_create: stream"));
+    const uint64_t d = c.d_model, ff = c.d_ff;
+    e->L.resize(c.n_layers);
+    int rc = BH_OK;
+    for (auto& Ly : e->L) {
+        if ((rc = dalloc(e, &Ly.ln1, d)) || (rc = dalloc(e, &Ly.ln2, d)) || (rc = dalloc(e, &Ly.qn, c.head_dim)) ||
+            (rc = dalloc(e, &Ly.kn, c.head_dim)) || (rc = dalloc(e, &Ly.wqkv, (uint64_t)e->W * d / 4)) ||
+            (rc = dalloc(e, &Ly.sqkv, e->W)) || (rc = dalloc(e, &Ly.wo, d * hq / 4)) || (rc = dalloc(e, &Ly.so, d)) ||
+            (rc = dalloc(e, &Ly.wgu, 2 * ff * d / 4)) || (rc = dalloc(e, &Ly.sgu, 2 * ff)) ||
+            (rc = dalloc(e, &Ly.wdown, d * ff / 4)) || (rc = dalloc(e, &Ly.sdown, d)))
+            return bail(rc);
+    }
+    e->layer_kv = (size_t)max_batch * max_seq * e->hkv;
+    e->tmpw_floats = std::max<uint64_t>(std::max<uint64_t>((uint64_t)e->W * d, 2 * ff * d), d * std::max<uint64_t>(hq, ff));
+    if (!c.tie_embeddings) e->tmpw_floats = std::max<uint64_t>(e->tmpw_floats, (uint64_t)c.vocab * d);
+    const uint64_t R = max_rows;
+    if ((rc = dalloc(e, &e->emb, (uint64_t)c.vocab * d)) || (rc = dalloc(e, &e->norm, d)) ||
+        (rc = dalloc(e, &e->head, (uint64_t)c.vocab * d / 4)) || (rc = dalloc(e, &e->shead, c.vocab)) ||
+        (rc = dalloc(e, &e->kc, e->layer_kv * c.n_layers)) || (rc = dalloc(e, &e->vc, e->layer_kv * c.n_layers)) ||
+        (rc = dalloc(e, &e->res, R * d)) || (rc = dalloc(e, &e->qkv, R * e->W)) || (rc = dalloc(e, &e->q, R * hq)) ||
+        (rc = dalloc(e, &e->ctx, R * hq)) || (rc = dalloc(e, &e->proj, R * d)) || (rc = dalloc(e, &e->gu, R * 2 * ff)) ||
+        (rc = dalloc(e, &e->sx, R)) || (rc = dalloc(e, &e->xq, R * e->xq_words)) ||
+        (rc = dalloc(e, &e->logits, (uint64_t)max_batch * c.vocab)) || (rc = dalloc(e, &e->tmpw, e->tmpw_floats)) ||
+        (rc = dalloc(e, &e->am_v, (uint64_t)max_batch * AM_CH)) || (rc = dalloc(e, &e->am_i, (uint64_t)max_batch * AM_CH)) ||
+        (rc = dalloc(e, &e->tok_rows, R)) || (rc = dalloc(e, &e->pos_rows, R)) || (rc = dalloc(e, &e->seq_rows, R)) ||
+        (rc = dalloc(e, &e->row_map, max_batch)) || (rc = dalloc(e, &e->tok_dec, max_batch)) ||
+        (rc = dalloc(e, &e->pos_dec, max_batch)) || (rc = dalloc(e, &e->seq_dec, max_batch)) ||
+        (rc = dalloc(e, &e->hist, (uint64_t)max_seq * max_batch)) || (rc = dalloc(e, &e->ctl, 2)))
+        return bail(rc);
+    std::vector<uint32_t> seq(max_batch);
+    for (uint32_t b = 0; b < max_batch; ++b) seq[b] = b;
+    if (hipMemcpy(e->seq_dec, seq.data(), max_batch * 4, hipMemcpyHostToDevice) != hipSuccess)
+        return bail(fail(BH_ERR_HIP, "bh_qwen3_create: upload"));
+    *out = e;
+    return BH_OK;
+}
+
+void bh_qwen3_destroy(bh_qwen3* e) { delete e; }
+
+void* bh_qwen3_stream(bh_qwen3* e) { return e ? (void*)e->stream : nullptr; }
+
+int bh_qwen3_set_weight(bh_qwen3* e, const char* name, const float* host, uint64_t numel) {
+    if (!e || !name || !host) return fail(BH_ERR_INVALID, "bh_qwen3_set_weight: null argument");
+    (void)hipSetDevice(e->device);
+    Target t;
+    BH_TRY(resolve(e, name, &t));
+    if (t.f32) {
+        if (numel != t.n) return fail(BH_ERR_INVALID, "bh_qwen3_set_weight: %s has %llu elements, got %llu", name,
+                                      (unsigned long long)t.n, (unsigned long long)numel);
+        BH_HIP(hipMemcpyAsync(t.f32, host, numel * 4, hipMemcpyHostToDevice, e->stream), "upload");
+        if (t.is_emb && e->c.tie_embeddings)
+            BH_TRY(quantize_into(e, e->emb, e->c.vocab, e->c.d_model, e->head, e->shead));
+        return sync(e);
+    }
+    if (numel != t.n * t.k) return fail(BH_ERR_INVALID, "bh_qwen3_set_weight: %s has %llu elements, got %llu", name,
+                                        (unsigned long long)(t.n * t.k), (unsigned long long)numel);
+    BH_HIP(hipMemcpyAsync(e->tmpw, host, numel * 4, hipMemcpyHostToDevice, e->stream), "upload");
+    BH_TRY(quantize_into(e, e->tmpw, (uint32_t)t.n, (uint32_t)t.k, t.packed, t.scale));
+    return sync(e);
+}
+
+int bh_qwen3_set_weight_i8(bh_qwen3* e, const char* name, const uint32_t* packed, const float* scale, uint32_t n,
+                           uint32_t k) {
+    if (!e || !name || !packed || !scale) return fail(BH_ERR_INVALID, "bh_qwen3_set_weight_i8: null argument");
+    (void)hipSetDevice(e->device);
+    Target t;
+    BH_TRY(resolve(e, name, &t));
+    if (!t.packed) return fail(BH_ERR_INVALID, "bh_qwen3_set_weight_i8: %s is not an int8 linear", name);
+    if (n != t.n || k != t.k) return fail(BH_ERR_INVALID, "bh_qwen3_set_weight_i8: %s is [%llu,%llu], got [%u,%u]", name,
+                                          (unsigned long long)t.n, (unsigned long long)t.k, n, k);
+    BH_HIP(hipMemcpyAsync(t.packed, packed, (size_t)n * k, hipMemcpyHostToDevice, e->stream), "upload");
+    BH_HIP(hipMemcpyAsync(t.scale, scale, (size_t)n * 4, hipMemcpyHostToDevice, e->stream), "upload");
+    return sync(e);
+}
+
+int bh_qwen3_init_random(bh_qwen3* e, uint64_t seed) {
+    if (!e) return fail(BH_ERR_INVALID, "bh_qwen3_init_random: null engine");
+    (void)hipSetDevice(e->device);
+    for (const std::string& name : param_names(e->c)) {
+        Target t;
+        BH_TRY(resolve(e, name, &t));
+        const uint64_t key = splitmix_host(seed ^ fnv1a(name));
+        if (t.f32) {
+            if (t.is_emb) {
+                init_normal_kernel<<<grid_for(t.n), 256, 0, e->stream>>>(t.f32, t.n, key, t.init_std);
+                if (e->c.tie_embeddings) BH_TRY(quantize_into(e, e->emb, e->c.vocab, e->c.d_model, e->head, e->shead));
+            } else {
+                fill_kernel<<<grid_for(t.n), 256, 0, e->stream>>>(t.f32, t.n, 1.0f);
+            }
+        } else {
+            const uint64_t n = t.n * t.k;
+            if (n > e->tmpw_floats) return fail(BH_ERR_INVALID, "bh_qwen3_init_random: %s exceeds the staging buffer", name.c_str());
+            init_normal_kernel<<<grid_for(n), 256, 0, e->stream>>>(e->tmpw, n, key, t.init_std);
+            BH_TRY(quantize_into(e, e->tmpw, (uint32_t)t.n, (uint32_t)t.k, t.packed, t.scale));
+        }
+        BH_HIP(hipGetLastError(), "init launch");
+    }
+    return sync(e);
+}
+
+int bh_qwen3_prefill(bh_qwen3* e, const uint32_t* tokens, uint32_t batch, uint32_t len, uint32_t* next) {
+    if (!e || !tokens || !next) return fail(BH_ERR_INVALID, "bh_qwen3_prefill: null argument");
+    if (!batch || batch > e->max_batch || !len || len > e->max_seq)
+        return fail(BH_ERR_INVALID, "bh_qwen3_prefill: batch %u (max %u), len %u (max %u)", batch, e->max_batch, len,
+                    e->max_seq);
+    for (uint64_t i = 0; i < (uint64_t)batch * len; ++i)
+        if (tokens[i] >= e->c.vocab) return fail(BH_ERR_INVALID, "bh_qwen3_prefill: token %u outside the vocabulary (%u)", tokens[i], e->c.vocab);
+    (void)hipSetDevice(e->device);
+    const uint32_t chunk = std::max<uint32_t>(1, e->max_rows / batch);
+    std::vector<uint32_t> tok, pos, seq;
+    std::vector<int> map(batch);
+    for (uint32_t p0 = 0; p0 < len; p0 += chunk) {
+        const uint32_t cc = std::min(chunk, len - p0);
+        const uint32_t rows = batch * cc;
+        tok.resize(rows);
+        pos.resize(rows);
+        seq.resize(rows);
+        for (uint32_t b = 0; b < batch; ++b)
+            for (uint32_t i = 0; i < cc; ++i) {
+                const uint32_t r = b * cc + i;
+                tok[r] = tokens[(size_t)b * len + p0 + i];
+                pos[r] = p0 + i;
+                seq[r] = b;
+            }
+        const bool last = p0 + cc == len;
+        for (uint32_t b = 0; b < batch; ++b) map[b] = (int)(b * cc + cc - 1);
+        BH_HIP(hipMemcpyAsync(e->tok_rows, tok.data(), rows * 4, hipMemcpyHostToDevice, e->stream), "upload");
+        BH_HIP(hipMemcpyAsync(e->pos_rows, pos.data(), rows * 4, hipMemcpyHostToDevice, e->stream), "upload");
+        BH_HIP(hipMemcpyAsync(e->seq_rows, seq.data(), rows * 4, hipMemcpyHostToDevice, e->stream), "upload");
+        if (last) BH_HIP(hipMemcpyAsync(e->row_map, map.data(), batch * 4, hipMemcpyHostToDevice, e->stream), "upload");
+        BH_TRY(run_rows(e, (int)rows, e->tok_rows, e->pos_rows, e->seq_rows, last ? (int)batch : 0, e->row_map, false));
+        BH_TRY(sync(e));  // the host vectors are reused by the next chunk
+    }
+    std::vector<uint32_t> pdec(batch, len);
+    const uint32_t ctl[2] = {len, e->max_seq};
+    BH_HIP(hipMemcpyAsync(e->pos_dec, pdec.data(), batch * 4, hipMemcpyHostToDevice, e->stream), "upload");
+    BH_HIP(hipMemcpyAsync(e->ctl, ctl, sizeof ctl, hipMemcpyHostToDevice, e->stream), "upload");
+    BH_HIP(hipMemcpyAsync(next, e->tok_dec, batch * 4, hipMemcpyDeviceToHost, e->stream), "download");
+    BH_TRY(sync(e));
+    e->batch = batch;
+    e->prompt_len = len;
+    e->decoded = 0;
+    return BH_OK;
+}
+
+int bh_qwen3_decode(bh_qwen3* e, uint32_t steps, uint32_t flags, uint32_t* out) {
+    if (!e || (steps && !out)) return fail(BH_ERR_INVALID, "bh_qwen3_decode: null argument");
+    if (!e->batch) return fail(BH_ERR_INVALID, "bh_qwen3_decode: no live sequences (call bh_qwen3_prefill)");
+    if ((uint64_t)e->prompt_len + e->decoded + steps > e->max_seq)
+        return fail(BH_ERR_INVALID, "bh_qwen3_decode: %u more steps exceed max_seq %u", steps, e->max_seq);
+    if (!steps) return BH_OK;
+    (void)hipSetDevice(e->device);
+    const int b = (int)e->batch;
+    if (flags & BH_QWEN3_EAGER) {
+        for (uint32_t s = 0; s < steps; ++s) BH_TRY(run_rows(e, b, e->tok_dec, e->pos_dec, e->seq_dec, b, nullptr, true));
+    } else {
+        if (!e->graph || e->graph_batch != e->batch) {
+            if (e->graph) {
+                (void)hipGraphExecDestroy(e->graph);
+                e->graph = nullptr;
+            }
+            hipGraph_t g = nullptr;
+            BH_HIP(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal), "begin capture");
+            const int rc = run_rows(e, b, e->tok_dec, e->pos_dec, e->seq_dec, b, nullptr, true);
+            const hipError_t ce = hipStreamEndCapture(e->stream, &g);
+            if (rc != BH_OK) {
+                if (g) (void)hipGraphDestroy(g);
+                return rc;
+            }
+            BH_HIP(ce, "end capture");
+            const hipError_t ie = hipGraphInstantiate(&e->graph, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            BH_HIP(ie, "graph instantiate");
+            e->graph_batch = e->batch;
+        }
+        for (uint32_t s = 0; s < steps; ++s) BH_HIP(hipGraphLaunch(e->graph, e->stream), "graph launch");
+    }
+    BH_HIP(hipMemcpyAsync(out, e->hist + (size_t)e->decoded * b, (size_t)steps * b * 4, hipMemcpyDeviceToHost, e->stream),
+           "download");
+    BH_TRY(sync(e));
+    e->decoded += steps;
+    return BH_OK;
+}
+
+int bh_qwen3_logits(bh_qwen3* e, float* out, uint64_t n) {
+    if (!e || !out) return fail(BH_ERR_INVALID, "bh_qwen3_logits: null argument");
+    const uint64_t want = (uint64_t)e->batch * e->c.vocab;
+    if (!e->batch || n < want) return fail(BH_ERR_INVALID, "bh_qwen3_logits: need %llu floats", (unsigned long long)want);
+    (void)hipSetDevice(e->device);
+    BH_HIP(hipMemcpyAsync(out, e->logits, want * 4, hipMemcpyDeviceToHost, e->stream), "download");
+    return sync(e);
+}
+
+int bh_qwen3_lengths(bh_qwen3* e, uint32_t* len, uint32_t batch) {
+    if (!e || !len || batch < e->batch) return fail(BH_ERR_INVALID, "bh_qwen3_lengths: bad argument");
+    for (uint32_t b = 0; b < e->batch; ++b) len[b] = e->prompt_len + e->decoded;
+    return BH_OK;
+}
+
+}  // extern "C"

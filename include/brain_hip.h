@@ -274,6 +274,71 @@ typedef struct {
 } bh_cost_t;
 int bh_cost(const char* name, const uint32_t* params, uint32_t nparams, bh_cost_t* out);
 
+/* ======================================================================
+ * D. The int8 Qwen3 decoder (the caller of sections A-C the reference runs
+ *    most): `qwen3::serve::Engine` with int8 weights
+ *    (crates/qwen3/src/serve.rs:1194-1367 step tape, :1557-1620 prefill,
+ *    :1332-1367 greedy head; config crates/qwen3/src/config.rs:100-118).
+ *    Per layer: RMSNorm -> int8 q/k/v -> QK-norm -> RoPE -> KV append ->
+ *    causal GQA attention -> int8 o -> residual -> RMSNorm -> int8 gate/up ->
+ *    SwiGLU -> int8 down -> residual; then RMSNorm, the int8 head and a
+ *    greedy argmax on the device. Activations f32; every linear quantizes its
+ *    input per token (max_abs_row + quant_pack semantics) and runs
+ *    bh_matmul_i8 with f32 output. The KV cache is f32, one contiguous
+ *    [max_seq, kv_dim] slab per (layer, sequence).
+ * ====================================================================== */
+typedef struct bh_qwen3 bh_qwen3;
+
+/* `QwenConfig` fields the forward reads. head_dim % 64 == 0, head_dim <= 256,
+ * n_heads % n_kv_heads == 0, d_model, q_dim, d_ff multiples of 4 and <= 8192. */
+typedef struct {
+    uint32_t vocab, n_layers, d_model, n_heads, n_kv_heads, head_dim, d_ff;
+    float rope_theta, rms_eps;
+    uint32_t tie_embeddings; /* 1: the head is tok.weight (quantized), else lm_head.weight */
+    uint32_t qk_norm;        /* 1: per-head RMSNorm of q and k before RoPE */
+} bh_qwen3_config;
+
+/* Engine for up to max_batch sequences of max_seq positions each; prefill
+ * chunks hold at most max_rows token rows (batch * positions). Allocates every
+ * device buffer once; weights start unset (zero). */
+int bh_qwen3_create(const bh_qwen3_config* cfg, uint32_t max_batch, uint32_t max_seq, uint32_t max_rows,
+                    int device, bh_qwen3** out);
+void bh_qwen3_destroy(bh_qwen3* e);
+
+/* Upload one f32 parameter by its reference name (`decoder_param_list`,
+ * serve.rs:320-340: tok.weight, norm.weight, lm_head.weight,
+ * blocks.{l}.{ln1,ln2}.weight, blocks.{l}.attn.{wq,wk,wv,wo,q_norm,k_norm}.weight,
+ * blocks.{l}.mlp.{gate,up,down}.weight). Linear weights are quantized on the
+ * device per output row (crates/model/src/int8.rs:33-59); with tied
+ * embeddings tok.weight also becomes the int8 head. numel must match. */
+int bh_qwen3_set_weight(bh_qwen3* e, const char* name, const float* host, uint64_t numel);
+/* Upload an already-quantized linear (packed [n, k/4] u32 + scales [n], the
+ * int8 on-disk layout of crates/model/src/int8.rs:112-187). */
+int bh_qwen3_set_weight_i8(bh_qwen3* e, const char* name, const uint32_t* packed, const float* scale,
+                           uint32_t n, uint32_t k);
+/* Random init on the device with the reference's distributions
+ * (crates/qwen3/src/init.rs:30-59): norm gains 1, wo/down N(0, 0.02/sqrt(2L)),
+ * other linears and the embedding N(0, 0.02). Counter-based generator, so a
+ * seed gives the same weights on every run (not the reference's stream). */
+int bh_qwen3_init_random(bh_qwen3* e, uint64_t seed);
+
+/* Start `batch` sequences from prompts tokens[batch][len] (row-major): runs
+ * the prompt rows through every layer (chunked to max_rows), fills the KV
+ * cache, and writes each sequence's greedy next token to next[batch]. */
+int bh_qwen3_prefill(bh_qwen3* e, const uint32_t* tokens, uint32_t batch, uint32_t len, uint32_t* next);
+/* `steps` greedy decode steps of every live sequence: each step feeds the
+ * previous token back on the device (no host round trip) and appends the new
+ * one. out[steps][batch] receives the generated tokens. The step is captured
+ * once in a HIP graph and replayed (flags & BH_QWEN3_EAGER: launch eagerly). */
+#define BH_QWEN3_EAGER 1u
+int bh_qwen3_decode(bh_qwen3* e, uint32_t steps, uint32_t flags, uint32_t* out);
+/* Logits [batch, vocab] f32 of the most recent head evaluation (prefill or
+ * the last decode step). */
+int bh_qwen3_logits(bh_qwen3* e, float* out, uint64_t n);
+/* Positions filled so far (prompt + decoded) of each sequence: len[batch]. */
+int bh_qwen3_lengths(bh_qwen3* e, uint32_t* len, uint32_t batch);
+void* bh_qwen3_stream(bh_qwen3* e);
+
 #ifdef __cplusplus
 }
 #endif

@@ -52,6 +52,9 @@ def lib():
             "or_f32_to_bf16_array": (None, [C.c_void_p, C.c_void_p, C.c_size_t]),
             "or_cpu_linear_gemv": (None, [vp, vp, vp, i64, i64, i64, i32, vp, vp, vp]),
             "or_cpu_gemv_packed": (None, [vp, vp, vp, vp, i64, i64, i64, i32, vp]),
+            "or_argmax_row": (u32, [vp, u32]),
+            "or_qwen3_param_count": (u64, [vp]),
+            "or_qwen3_generate": (i32, [vp, vp, i32, vp, u32, u32, u32, vp, vp]),
         }
         for n, (r, a) in sig.items():
             f = getattr(L, n)
@@ -259,3 +262,74 @@ def splitmix_u64(seed, count):
         z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
         z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
         return z ^ (z >> np.uint64(31))
+
+
+# ---------------------------------------------------------------- Qwen3 decoder
+class Qwen3Config(C.Structure):
+    """or_qwen3_config (qwen3_oracle.h), the QwenConfig fields the forward reads."""
+    _fields_ = [(n, C.c_uint32) for n in ("vocab", "n_layers", "d_model", "n_heads", "n_kv_heads", "head_dim", "d_ff")] + \
+               [("rope_theta", C.c_float), ("rms_eps", C.c_float), ("tie_embeddings", C.c_uint32), ("qk_norm", C.c_uint32)]
+
+
+def qwen3_param_list(cfg):
+    """(name, shape) in decoder_param_list order (crates/qwen3/src/serve.rs:320-340)."""
+    d, ff, hd = cfg["d_model"], cfg["d_ff"], cfg["head_dim"]
+    hq, hkv = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd
+    out = []
+    for l in range(cfg["n_layers"]):
+        p = f"blocks.{l}."
+        out += [(p + "ln1.weight", (d,)), (p + "attn.wq.weight", (hq, d)), (p + "attn.wk.weight", (hkv, d)),
+                (p + "attn.wv.weight", (hkv, d)), (p + "attn.q_norm.weight", (hd,)), (p + "attn.k_norm.weight", (hd,)),
+                (p + "attn.wo.weight", (d, hq)), (p + "ln2.weight", (d,)), (p + "mlp.gate.weight", (ff, d)),
+                (p + "mlp.up.weight", (ff, d)), (p + "mlp.down.weight", (d, ff))]
+    out += [("norm.weight", (d,)), ("tok.weight", (cfg["vocab"], d))]
+    if not cfg.get("tie_embeddings", 1):
+        out.append(("lm_head.weight", (cfg["vocab"], d)))
+    return out
+
+
+def qwen3_init(cfg, seed, gain_noise=0.0):
+    """Seeded weights with the reference's distributions (crates/qwen3/src/init.rs:30-59):
+    gains 1 (plus optional noise so they matter in a test), wo/down N(0, 0.02/sqrt(2L)),
+    everything else N(0, 0.02). numpy's generator, not the reference's stream."""
+    rng = np.random.default_rng(seed)
+    proj = 0.02 / np.sqrt(2.0 * cfg["n_layers"])
+    w = {}
+    for name, shape in qwen3_param_list(cfg):
+        if name.endswith(("ln1.weight", "ln2.weight", "norm.weight")):
+            v = 1.0 + gain_noise * rng.standard_normal(shape)
+        elif name.endswith(("attn.wo.weight", "mlp.down.weight")):
+            v = proj * rng.standard_normal(shape)
+        else:
+            v = 0.02 * rng.standard_normal(shape)
+        w[name] = v.astype(np.float32)
+    return w
+
+
+def _qcfg(cfg):
+    c = Qwen3Config()
+    for k in ("vocab", "n_layers", "d_model", "n_heads", "n_kv_heads", "head_dim", "d_ff"):
+        setattr(c, k, cfg[k])
+    c.rope_theta, c.rms_eps = cfg.get("rope_theta", 1e6), cfg.get("rms_eps", 1e-6)
+    c.tie_embeddings, c.qk_norm = cfg.get("tie_embeddings", 1), cfg.get("qk_norm", 1)
+    return c
+
+
+def qwen3_generate(cfg, weights, prompts, steps, int8=True):
+    """or_qwen3_generate: greedy tokens [(steps+1), batch] and logits [(steps+1), batch, vocab]."""
+    c = _qcfg(cfg)
+    blob = np.concatenate([weights[n].ravel() for n, _ in qwen3_param_list(cfg)]).astype(np.float32)
+    assert blob.size == lib().or_qwen3_param_count(C.byref(c))
+    prompts = _c(prompts, np.uint32)
+    batch, ln = prompts.shape
+    toks = np.zeros((steps + 1, batch), np.uint32)
+    logits = np.zeros((steps + 1, batch, cfg["vocab"]), np.float32)
+    rc = lib().or_qwen3_generate(C.byref(c), _p(blob), 1 if int8 else 0, _p(prompts), batch, ln, steps,
+                                 _p(toks), _p(logits))
+    assert rc == 0
+    return toks, logits
+
+
+def argmax_row(x):
+    x = _c(x, np.float32)
+    return lib().or_argmax_row(_p(x), x.size)

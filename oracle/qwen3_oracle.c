@@ -1,0 +1,265 @@
+/* CPU oracle of the int8 Qwen3 decoder -- TEST INFRASTRUCTURE ONLY.
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load this; the product path never does. A plain sequential restatement of
+ * qwen3::serve::Engine's step tape (crates/qwen3/src/serve.rs:1194-1310)
+ * for one token at a time per sequence (causal prefill == feeding the
+ * prompt token by token, because every op is row-wise except attention,
+ * which reads only earlier positions):
+ *
+ *   x = tok[t]                                   embed.wgsl
+ *   per layer:
+ *     xn = rmsnorm(x, ln1)                       rmsnorm_rows.wgsl:24-44
+ *     q,k,v = lin(xn, wq|wk|wv)                  serve.rs:1242-1247
+ *     q,k = rmsnorm per head (q_norm/k_norm)     serve.rs:1253-1254
+ *     q,k = rope(pos)                            rope_paged.wgsl:27-38
+ *     K[pos],V[pos] = k,v                        paged_kv_append_batched.wgsl
+ *     s_j = (q . K_j) * hd^-1/2, j <= pos        paged_decode_scores_wg.wgsl
+ *     p = softmax(s)                             decode_softmax_batched.wgsl
+ *     ctx = sum_j p_j V_j                        paged_decode_apply_batched.wgsl
+ *     x = x + lin(ctx, wo)                       add2.wgsl
+ *     xn = rmsnorm(x, ln2)
+ *     h = silu(lin(xn, gate)) * lin(xn, up)      silu_mul.wgsl
+ *     x = x + lin(h, down)
+ *   logits = lin(rmsnorm(x, norm), head)          serve.rs:1297, 1358-1367
+ *   next = argmax(logits)                         argmax_row.wgsl
+ *
+ * lin() is the int8 path when int8 != 0: per-token activation quant
+ * (or_max_abs_row / or_quant_pack), weights quantized per output row
+ * (or_quantize_weight), exact integer accumulation and the (f32(acc)*sx)*sw
+ * epilogue, all from brain_oracle.c. With int8 == 0 it is an f32 linear
+ * (double accumulation, rounded once): the fp32 model the int8 path is
+ * bounded against (crates/qwen3/src/model.rs:2638-2661, rel-L2 < 0.10).
+ *
+ * Parameters arrive as one f32 blob in decoder_param_list order
+ * (crates/qwen3/src/serve.rs:320-340), then lm_head.weight when untied.
+ *
+ * Pinned by tests/test_qwen3_oracle.py: an independent numpy float64 forward
+ * of the fp32 model, the int8-vs-fp32 bound, and argmax tie/NaN cases.
+ */
+#include <float.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "brain_oracle.h"
+#include "qwen3_oracle.h"
+
+typedef struct {
+    const float *ln1, *wq, *wk, *wv, *qn, *kn, *wo, *ln2, *gate, *up, *down;
+} layer_t;
+
+typedef struct {
+    uint32_t *packed; /* NULL in fp32 mode */
+    float *scale;
+    const float *w;
+    uint32_t n, k;
+} lin_t;
+
+static void lin_init(lin_t *l, const float *w, uint32_t n, uint32_t k, int int8) {
+    l->w = w;
+    l->n = n;
+    l->k = k;
+    l->packed = NULL;
+    l->scale = NULL;
+    if (int8) {
+        l->packed = (uint32_t *)malloc((size_t)n * k);
+        l->scale = (float *)malloc((size_t)n * 4);
+        or_quantize_weight(w, n, k, l->packed, l->scale);
+    }
+}
+
+static void lin_free(lin_t *l) {
+    free(l->packed);
+    free(l->scale);
+}
+
+/* out[n] = lin(x[k]) for one token row. */
+static void lin_apply(const lin_t *l, const float *x, float *out) {
+    const uint32_t n = l->n, k = l->k;
+    if (l->packed) {
+        float sx;
+        uint32_t *xq = (uint32_t *)malloc((size_t)k);
+        or_max_abs_row(x, 1, k, &sx);
+        or_quant_pack(x, &sx, 1, k, xq);
+        const int8_t *a = (const int8_t *)xq;
+        for (uint32_t j = 0; j < n; ++j) {
+            const int8_t *b = (const int8_t *)(l->packed + (size_t)j * (k / 4));
+            int64_t acc = 0;
+            for (uint32_t c = 0; c < k; ++c) acc += (int32_t)a[c] * (int32_t)b[c];
+            const float v = (float)(int32_t)acc * sx;
+            out[j] = v * l->scale[j];
+        }
+        free(xq);
+    } else {
+        for (uint32_t j = 0; j < n; ++j) {
+            const float *w = l->w + (size_t)j * k;
+            double acc = 0.0;
+            for (uint32_t c = 0; c < k; ++c) acc += (double)x[c] * (double)w[c];
+            out[j] = (float)acc;
+        }
+    }
+}
+
+static void rmsnorm(const float *x, const float *w, uint32_t d, float eps, float *out) {
+    float ss = 0.0f;
+    for (uint32_t c = 0; c < d; ++c) ss += x[c] * x[c];
+    const float inv = 1.0f / sqrtf(ss / (float)d + eps);
+    for (uint32_t c = 0; c < d; ++c) out[c] = x[c] * inv * w[c];
+}
+
+static void rope(float *h, uint32_t hd, uint32_t pos, float theta) {
+    const uint32_t half = hd / 2;
+    for (uint32_t m = 0; m < half; ++m) {
+        const float angle = (float)pos * powf(theta, -(float)(2 * m) / (float)hd);
+        const float c = cosf(angle), s = sinf(angle);
+        const float x0 = h[m], x1 = h[m + half];
+        h[m] = x0 * c - x1 * s;
+        h[m + half] = x1 * c + x0 * s;
+    }
+}
+
+uint32_t or_argmax_row(const float *x, uint32_t n) {
+    uint32_t best = 0;
+    float bv = -FLT_MAX;
+    for (uint32_t j = 0; j < n; ++j)
+        if (x[j] > bv) {
+            bv = x[j];
+            best = j;
+        }
+    return best;
+}
+
+uint64_t or_qwen3_param_count(const or_qwen3_config *c) {
+    const uint64_t d = c->d_model, ff = c->d_ff, hd = c->head_dim;
+    const uint64_t hq = (uint64_t)c->n_heads * hd, hkv = (uint64_t)c->n_kv_heads * hd;
+    const uint64_t per = d + hq * d + 2 * hkv * d + 2 * hd + d * hq + d + 3 * ff * d;
+    uint64_t n = per * c->n_layers + d + (uint64_t)c->vocab * d;
+    if (!c->tie_embeddings) n += (uint64_t)c->vocab * d;
+    return n;
+}
+
+int or_qwen3_generate(const or_qwen3_config *c, const float *params, int int8, const uint32_t *prompts,
+                      uint32_t batch, uint32_t len, uint32_t steps, uint32_t *out_tokens, float *out_logits) {
+    const uint32_t d = c->d_model, ff = c->d_ff, hd = c->head_dim, nh = c->n_heads, nkv = c->n_kv_heads;
+    const uint32_t hq = nh * hd, hkv = nkv * hd, G = nh / nkv, L = c->n_layers, V = c->vocab;
+    if (!len || nh % nkv || hd % 2) return -1;
+    const uint32_t T = len + steps;
+    const float *p = params;
+    layer_t *ly = (layer_t *)calloc(L, sizeof(layer_t));
+    for (uint32_t l = 0; l < L; ++l) {
+        ly[l].ln1 = p; p += d;
+        ly[l].wq = p; p += (size_t)hq * d;
+        ly[l].wk = p; p += (size_t)hkv * d;
+        ly[l].wv = p; p += (size_t)hkv * d;
+        ly[l].qn = p; p += hd;
+        ly[l].kn = p; p += hd;
+        ly[l].wo = p; p += (size_t)d * hq;
+        ly[l].ln2 = p; p += d;
+        ly[l].gate = p; p += (size_t)ff * d;
+        ly[l].up = p; p += (size_t)ff * d;
+        ly[l].down = p; p += (size_t)d * ff;
+    }
+    const float *norm = p; p += d;
+    const float *tok = p; p += (size_t)V * d;
+    const float *head_w = c->tie_embeddings ? tok : p;
+
+    lin_t *lq = (lin_t *)calloc(L * 7, sizeof(lin_t));
+    for (uint32_t l = 0; l < L; ++l) {
+        lin_init(&lq[7 * l + 0], ly[l].wq, hq, d, int8);
+        lin_init(&lq[7 * l + 1], ly[l].wk, hkv, d, int8);
+        lin_init(&lq[7 * l + 2], ly[l].wv, hkv, d, int8);
+        lin_init(&lq[7 * l + 3], ly[l].wo, d, hq, int8);
+        lin_init(&lq[7 * l + 4], ly[l].gate, ff, d, int8);
+        lin_init(&lq[7 * l + 5], ly[l].up, ff, d, int8);
+        lin_init(&lq[7 * l + 6], ly[l].down, d, ff, int8);
+    }
+    lin_t head;
+    lin_init(&head, head_w, V, d, int8);
+
+    float *K = (float *)malloc(sizeof(float) * L * T * hkv);
+    float *Vc = (float *)malloc(sizeof(float) * L * T * hkv);
+    float *x = (float *)malloc(sizeof(float) * d), *xn = (float *)malloc(sizeof(float) * d);
+    float *q = (float *)malloc(sizeof(float) * hq), *k = (float *)malloc(sizeof(float) * hkv);
+    float *v = (float *)malloc(sizeof(float) * hkv), *ctx = (float *)malloc(sizeof(float) * hq);
+    float *o = (float *)malloc(sizeof(float) * d), *g = (float *)malloc(sizeof(float) * ff);
+    float *u = (float *)malloc(sizeof(float) * ff), *s = (float *)malloc(sizeof(float) * T);
+    float *logits = (float *)malloc(sizeof(float) * V), *tmp = (float *)malloc(sizeof(float) * hd);
+    const float scale = 1.0f / sqrtf((float)hd);
+
+    for (uint32_t b = 0; b < batch; ++b) {
+        uint32_t cur = prompts[(size_t)b * len];
+        for (uint32_t pos = 0; pos < T; ++pos) {
+            memcpy(x, tok + (size_t)cur * d, sizeof(float) * d);
+            for (uint32_t l = 0; l < L; ++l) {
+                float *Kl = K + (size_t)l * T * hkv, *Vl = Vc + (size_t)l * T * hkv;
+                rmsnorm(x, ly[l].ln1, d, c->rms_eps, xn);
+                lin_apply(&lq[7 * l + 0], xn, q);
+                lin_apply(&lq[7 * l + 1], xn, k);
+                lin_apply(&lq[7 * l + 2], xn, v);
+                for (uint32_t h = 0; h < nh; ++h) {
+                    if (c->qk_norm) {
+                        rmsnorm(q + h * hd, ly[l].qn, hd, c->rms_eps, tmp);
+                        memcpy(q + h * hd, tmp, sizeof(float) * hd);
+                    }
+                    rope(q + h * hd, hd, pos, c->rope_theta);
+                }
+                for (uint32_t h = 0; h < nkv; ++h) {
+                    if (c->qk_norm) {
+                        rmsnorm(k + h * hd, ly[l].kn, hd, c->rms_eps, tmp);
+                        memcpy(k + h * hd, tmp, sizeof(float) * hd);
+                    }
+                    rope(k + h * hd, hd, pos, c->rope_theta);
+                }
+                memcpy(Kl + (size_t)pos * hkv, k, sizeof(float) * hkv);
+                memcpy(Vl + (size_t)pos * hkv, v, sizeof(float) * hkv);
+                for (uint32_t h = 0; h < nh; ++h) {
+                    const uint32_t kh = h / G;
+                    float mx = -3.4e38f;
+                    for (uint32_t j = 0; j <= pos; ++j) {
+                        float acc = 0.0f;
+                        const float *kr = Kl + (size_t)j * hkv + kh * hd;
+                        for (uint32_t e = 0; e < hd; ++e) acc += q[h * hd + e] * kr[e];
+                        s[j] = acc * scale;
+                        if (s[j] > mx) mx = s[j];
+                    }
+                    float sum = 0.0f;
+                    for (uint32_t j = 0; j <= pos; ++j) sum += expf(s[j] - mx);
+                    const float inv = 1.0f / sum;
+                    for (uint32_t j = 0; j <= pos; ++j) s[j] = expf(s[j] - mx) * inv;
+                    for (uint32_t e = 0; e < hd; ++e) {
+                        float acc = 0.0f;
+                        for (uint32_t j = 0; j <= pos; ++j) acc += s[j] * Vl[(size_t)j * hkv + kh * hd + e];
+                        ctx[h * hd + e] = acc;
+                    }
+                }
+                lin_apply(&lq[7 * l + 3], ctx, o);
+                for (uint32_t e = 0; e < d; ++e) x[e] = x[e] + o[e];
+                rmsnorm(x, ly[l].ln2, d, c->rms_eps, xn);
+                lin_apply(&lq[7 * l + 4], xn, g);
+                lin_apply(&lq[7 * l + 5], xn, u);
+                for (uint32_t e = 0; e < ff; ++e) g[e] = g[e] / (1.0f + expf(-g[e])) * u[e];
+                lin_apply(&lq[7 * l + 6], g, o);
+                for (uint32_t e = 0; e < d; ++e) x[e] = x[e] + o[e];
+            }
+            if (pos + 1 < len) {
+                cur = prompts[(size_t)b * len + pos + 1];
+                continue;
+            }
+            rmsnorm(x, norm, d, c->rms_eps, xn);
+            lin_apply(&head, xn, logits);
+            const uint32_t gen = pos + 1 - len; /* 0: the token after the prompt */
+            cur = or_argmax_row(logits, V);
+            if (out_tokens) out_tokens[(size_t)gen * batch + b] = cur;
+            if (out_logits) memcpy(out_logits + ((size_t)gen * batch + b) * V, logits, sizeof(float) * V);
+            if (pos + 1 == T) break;
+        }
+    }
+    free(K); free(Vc); free(x); free(xn); free(q); free(k); free(v); free(ctx); free(o);
+    free(g); free(u); free(s); free(logits); free(tmp);
+    for (uint32_t i = 0; i < 7 * L; ++i) lin_free(&lq[i]);
+    lin_free(&head);
+    free(lq);
+    free(ly);
+    return 0;
+}
