@@ -42,7 +42,8 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on CPU-baseline work")
-    ap.add_argument("--only", default="", help="profiling aid: 'decode', 'prefill' or 'copy' only")
+    ap.add_argument("--only", default="", help="profiling aid: 'decode', 'prefill', 'qwen3' or 'copy' only")
+    ap.add_argument("--no-qwen3", action="store_true")
     return ap.parse_args()
 
 
@@ -244,6 +245,48 @@ def mfma_roof(torch, lib, dev):
     return round(ops / (a.elapsed_time(b) * 1e-3) / 1e12, 1)
 
 
+def qwen3_weight_bytes(c):
+    """int8 weight + scale bytes one decode step streams (every linear + the head)."""
+    d, ff, hq, hkv = c["d_model"], c["d_ff"], c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
+    per_layer = (hq + 2 * hkv) * d + d * hq + 2 * ff * d + d * ff
+    rows = c["n_layers"] * (hq + 2 * hkv + d + 2 * ff + d) + c["vocab"]
+    return c["n_layers"] * per_layer + c["vocab"] * d + 4 * rows
+
+
+def bench_qwen3(prompt_len=128, gen=256, batches=(1, 8)):
+    """Qwen3-0.6B-architecture int8 decoder, random init, greedy.
+    Prefill of a random-id prompt, then `gen` decode steps (one HIP graph
+    replay each); tok/s = batch * gen / decode wall time."""
+    import numpy as np
+    from brain_amd.qwen3 import QWEN3_0_6B, Qwen3Engine
+    c = QWEN3_0_6B
+    wbytes = qwen3_weight_bytes(c)
+    out = {"model": "Qwen3-0.6B architecture (28 layers, d 1024, 16q/8kv heads, hd 128, ff 3072, vocab 151936, tied)",
+           "weights": "random init (device, seeded), int8 per-channel", "prompt_len": prompt_len, "decode_steps": gen,
+           "int8_weight_mb_per_step": round(wbytes / 1e6, 1)}
+    for b in batches:
+        e = Qwen3Engine(c, b, prompt_len + gen + 8, max_rows=b * prompt_len)
+        e.init_random(7)
+        prompts = np.random.default_rng(b).integers(0, c["vocab"], size=(b, prompt_len))
+        e.prefill(prompts)
+        e.decode(4)                      # graph capture + warm-up
+        t0 = time.perf_counter()
+        e.prefill(prompts)
+        t1 = time.perf_counter()
+        toks = e.decode(gen)
+        t2 = time.perf_counter()
+        assert toks.shape == (gen, b)
+        step_s = (t2 - t1) / gen
+        avg_ctx = prompt_len + (gen + 1) / 2.0
+        kv_bytes = 2 * c["n_layers"] * b * avg_ctx * c["n_kv_heads"] * c["head_dim"] * 4
+        out[f"batch{b}"] = {"decode_tok_s": round(b * gen / (t2 - t1), 1), "ms_per_step": round(step_s * 1e3, 4),
+                            "prefill_ms": round((t1 - t0) * 1e3, 2),
+                            "prefill_tok_s": round(b * prompt_len / (t1 - t0), 1),
+                            "step_hbm_gbs": round((wbytes + kv_bytes) / step_s / 1e9, 1)}
+        e.close()
+    return out
+
+
 def cpu_baseline(budget_s):
     """The restated backend-cpu decode path (max_abs_row -> quant_pack ->
     matmul_i8_gemv, OpenMP over output columns) on this host, on the same
@@ -311,6 +354,8 @@ def main():
         del sets
     if args.only in ("", "prefill") and not args.no_prefill:
         res["prefill"] = bench_prefill(torch, lib, dev, gen, args.prefill_reps)
+    if args.only in ("", "qwen3") and not args.no_qwen3:
+        res["qwen3"] = bench_qwen3()
     if args.only:
         print(json.dumps(res))
         return
@@ -356,6 +401,8 @@ def main():
     }
     if "prefill" in res:
         line["prefill"] = res["prefill"]
+    if "qwen3" in res:
+        line["qwen3_e2e"] = res["qwen3"]
     if cpu is not None:
         line["gpu_vs_cpu"] = round(value / cpu["value"], 1)
     print(json.dumps(line))

@@ -11,11 +11,13 @@
 //                   (the reference runs three; per-row weight scales make the
 //                   stacked product column-for-column identical)
 //   qk_rope_append  per head: QK-norm, RoPE (rope_paged.wgsl), K/V append
-//   attention       causal GQA over the f32 cache, one workgroup per
-//                   (row, kv head): scores, softmax, weighted V
+//   attention       causal GQA over the f32 cache split over key chunks
+//                   (flash-decoding): per (row, kv head, 32 keys) scores,
+//                   chunk softmax statistics and weighted V, then one
+//                   combine per row that also quantizes the context
 //                   (paged_decode_scores_wg / decode_softmax_batched /
-//                   paged_decode_apply_batched)
-//   quantize ctx    -> linear o
+//                   paged_decode_apply_batched + max_abs_row/quant_pack)
+//   linear o
 //   norm_quant      residual add + RMSNorm + quant
 //   linear gate|up  stacked like qkv
 //   swiglu_quant    silu(g)*u (silu_mul.wgsl) + quant
@@ -270,81 +272,137 @@ __global__ __launch_bounds__(64) void qk_rope_append_kernel(RopeArgs p) {
     }
 }
 
+constexpr int KCH = 32;  // keys per attention workgroup
+
 struct AttnArgs {
     const float* q;    // [rows, hq]
     const float* kc;   // this layer's caches
     const float* vc;
     const uint32_t* pos;
     const uint32_t* seq;
-    float* ctx;        // [rows, hq]
-    int nh, nkv, hd, hq, hkv, max_seq;
-    int sstride;  // LDS floats per query head's scores: max_seq rounded up to 4 (keeps qs 16-byte aligned)
+    float* part_o;     // [rows, nh, splits, hd]  sum_k exp(s_k - m) v_k over one chunk
+    float* part_ml;    // [rows, nh, splits, 2]   (m, sum_k exp(s_k - m))
+    int nh, nkv, hd, hq, hkv, max_seq, splits;
     float scale;
 };
 
-// Causal GQA for one (row, kv head): the row attends positions 0..pos of its
-// sequence. Scores q.k * scale for every query head of the group (16 lanes per
-// key, float4 loads along head_dim), softmax with the max subtracted, then
-// ctx = sum_j p_j v_j. LDS: scores [group][max_seq] + queries [group][hd].
-__global__ __launch_bounds__(RT) void attention_kernel(AttnArgs p) {
-    extern __shared__ float sm[];
-    __shared__ float red[RT / 64];
-    const int r = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x;
-    const int G = p.nh / p.nkv;
+// Causal GQA, split over the keys (flash-decoding): one workgroup per (row,
+// kv head, chunk of KCH keys); a row attends positions 0..pos of its sequence,
+// so chunks starting past pos exit at once. Scores q.k * scale for every
+// query head of the group (8 lanes per key, float4 along head_dim), then the
+// chunk's own softmax statistics and its unnormalized weighted sum of V.
+// attn_combine_quant_kernel merges the chunks: the same softmax as
+// paged_decode_scores_wg -> decode_softmax_batched -> paged_decode_apply_batched
+// up to f32 rounding order.
+__global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
+    __shared__ float qs[MAX_GROUP * 256];
+    __shared__ float es[MAX_GROUP * KCH];
+    __shared__ float ml[MAX_GROUP * 2];
+    const int r = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z, tid = threadIdx.x;
     const int t = (int)p.pos[r] + 1;
-    float* s = sm;
-    float* qs = sm + (size_t)G * p.sstride;
+    const int j0 = sp * KCH;
+    if (j0 >= t) return;
+    const int n = min(KCH, t - j0);
+    const int G = p.nh / p.nkv;
     for (int i = tid; i < G * p.hd; i += RT) qs[i] = p.q[(size_t)r * p.hq + (size_t)kh * G * p.hd + i];
     __syncthreads();
     const size_t base = (size_t)p.seq[r] * p.max_seq * p.hkv + (size_t)kh * p.hd;
-    const float* Kb = p.kc + base;
-    const float* Vb = p.vc + base;
-    const int li = tid & 15, slot = tid >> 4;
-    for (int j = slot; j < t; j += RT / 16) {
-        const float* kr = Kb + (size_t)j * p.hkv;
+    {
+        const int kk = tid >> 3, l8 = tid & 7;
         float acc[MAX_GROUP];
 #pragma unroll
         for (int g = 0; g < MAX_GROUP; ++g) acc[g] = 0.0f;
-        for (int c = li * 4; c < p.hd; c += 64) {
-            const float4 kv = *reinterpret_cast<const float4*>(kr + c);
+        if (kk < n) {
+            const float* kr = p.kc + base + (size_t)(j0 + kk) * p.hkv;
+            for (int c = l8 * 4; c < p.hd; c += 32) {
+                const float4 kv = *reinterpret_cast<const float4*>(kr + c);
 #pragma unroll
-            for (int g = 0; g < MAX_GROUP; ++g) {
-                if (g >= G) break;
-                const float4 qv = *reinterpret_cast<const float4*>(qs + g * p.hd + c);
-                acc[g] += qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+                for (int g = 0; g < MAX_GROUP; ++g) {
+                    if (g >= G) break;
+                    const float4 qv = *reinterpret_cast<const float4*>(qs + g * p.hd + c);
+                    acc[g] += qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+                }
             }
         }
 #pragma unroll
         for (int g = 0; g < MAX_GROUP; ++g) {
             if (g >= G) break;
             float v = acc[g];
-            v += __shfl_xor(v, 8, 64);
             v += __shfl_xor(v, 4, 64);
             v += __shfl_xor(v, 2, 64);
             v += __shfl_xor(v, 1, 64);
-            if (li == 0) s[(size_t)g * p.sstride + j] = v * p.scale;
+            if (l8 == 0) es[g * KCH + kk] = v * p.scale;
         }
     }
     __syncthreads();
-    for (int g = 0; g < G; ++g) {
-        float* sg = s + (size_t)g * p.sstride;
-        float mx = -3.4e38f;
-        for (int j = tid; j < t; j += RT) mx = fmaxf(mx, sg[j]);
-        mx = block_max(mx, red);
-        float sum = 0.0f;
-        for (int j = tid; j < t; j += RT) sum += expf(sg[j] - mx);
-        sum = block_sum(sum, red);
-        const float inv = 1.0f / sum;
-        for (int j = tid; j < t; j += RT) sg[j] = expf(sg[j] - mx) * inv;
+    {
+        // One 32-lane half-wave per query head: the chunk's max and sum of exp.
+        const int g = tid / KCH, k = tid % KCH;
+        const bool live = g < G && k < n;
+        const float s = live ? es[g * KCH + k] : -INFINITY;
+        float m = s;
+#pragma unroll
+        for (int off = KCH / 2; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        const float e = live ? expf(s - m) : 0.0f;
+        float l = e;
+#pragma unroll
+        for (int off = KCH / 2; off >= 1; off >>= 1) l += __shfl_xor(l, off, 64);
+        __syncthreads();
+        if (g < G) es[g * KCH + k] = e;
+        if (g < G && k == 0) {
+            ml[2 * g] = m;
+            ml[2 * g + 1] = l;
+        }
     }
     __syncthreads();
+    const float* vb = p.vc + base + (size_t)j0 * p.hkv;
     for (int i = tid; i < G * p.hd; i += RT) {
         const int g = i / p.hd, d = i - g * p.hd;
-        const float* pg = s + (size_t)g * p.sstride;
         float acc = 0.0f;
-        for (int j = 0; j < t; ++j) acc += pg[j] * Vb[(size_t)j * p.hkv + d];
-        p.ctx[(size_t)r * p.hq + (size_t)(kh * G + g) * p.hd + d] = acc;
+#pragma unroll 8
+        for (int k = 0; k < n; ++k) acc += es[g * KCH + k] * vb[(size_t)k * p.hkv + d];
+        const size_t slot = ((size_t)r * p.nh + kh * G + g) * p.splits + sp;
+        p.part_o[slot * p.hd + d] = acc;
+        if (d == 0) {
+            p.part_ml[2 * slot] = ml[2 * g];
+            p.part_ml[2 * slot + 1] = ml[2 * g + 1];
+        }
     }
+}
+
+// Merge the key chunks of every head of row r: M = max m_s,
+// L = sum l_s e^(m_s - M), ctx = sum o_s e^(m_s - M) / L; then quantize the
+// whole context row for the output projection (quant_pack semantics).
+template <int GQ>
+__global__ __launch_bounds__(RT) void attn_combine_quant_kernel(const float* part_o, const float* part_ml,
+                                                                const uint32_t* pos, int nh, int hd, int hq,
+                                                                int splits, float* sx, uint32_t* xq) {
+    __shared__ float red[RT / 64];
+    const int r = blockIdx.x;
+    const int ns = ((int)pos[r] + KCH) / KCH;  // chunks holding positions 0..pos
+    const int q4 = hq >> 2;
+    float4 y[GQ];
+#pragma unroll
+    for (int g = 0; g < GQ; ++g) {
+        const int i = threadIdx.x + g * RT;
+        y[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i >= q4) continue;
+        const int e = i * 4, h = e / hd, d = e - h * hd;
+        const size_t hs = ((size_t)r * nh + h) * splits;
+        float M = -INFINITY;
+        for (int s = 0; s < ns; ++s) M = fmaxf(M, part_ml[2 * (hs + s)]);
+        float L = 0.0f;
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s = 0; s < ns; ++s) {
+            const float w = expf(part_ml[2 * (hs + s)] - M);
+            L += part_ml[2 * (hs + s) + 1] * w;
+            const float4 v = *reinterpret_cast<const float4*>(part_o + (hs + s) * hd + d);
+            o = make_float4(o.x + v.x * w, o.y + v.y * w, o.z + v.z * w, o.w + v.w * w);
+        }
+        const float inv = 1.0f / L;
+        y[g] = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+    }
+    quant_row<GQ>(y, q4, red, sx + r, xq + (size_t)r * q4);
 }
 
 // Greedy argmax, stage 1: chunk c of row b -> (value, index) with the
@@ -468,7 +526,10 @@ struct bh_qwen3 {
     float *kc = nullptr, *vc = nullptr;
     size_t layer_kv = 0;  // floats per layer per cache
 
-    float *res = nullptr, *qkv = nullptr, *q = nullptr, *ctx = nullptr, *proj = nullptr, *gu = nullptr;
+    float *res = nullptr, *qkv = nullptr, *q = nullptr, *proj = nullptr, *gu = nullptr;
+    float *part_o = nullptr, *part_ml = nullptr;  // attention chunk partials
+    uint32_t max_splits = 0;
+    const uint32_t* cur_pos = nullptr;
     float *sx = nullptr, *logits = nullptr, *tmpw = nullptr, *am_v = nullptr;
     uint32_t *xq = nullptr, *am_i = nullptr;  // xq: every producer writes rows of width/4 words
     uint32_t *tok_rows = nullptr, *pos_rows = nullptr, *seq_rows = nullptr;
@@ -546,14 +607,26 @@ int launch_swiglu_quant(bh_qwen3* e, int rows) {
 // n_out > 0, the final norm of rows out_map[0..n_out) (null: rows 0..n_out),
 // the head and the argmax into tok_dec (advancing pos_dec and recording into
 // hist when `decode`).
+int launch_combine_quant(bh_qwen3* e, int rows, int splits) {
+    const int hq = (int)e->hq, groups = (hq / 4 + RT - 1) / RT;
+    const int nh = (int)e->c.n_heads, hd = (int)e->c.head_dim;
+    if (groups <= 1) attn_combine_quant_kernel<1><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, e->cur_pos, nh, hd, hq, splits, e->sx, e->xq);
+    else if (groups <= 2) attn_combine_quant_kernel<2><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, e->cur_pos, nh, hd, hq, splits, e->sx, e->xq);
+    else if (groups <= 4) attn_combine_quant_kernel<4><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, e->cur_pos, nh, hd, hq, splits, e->sx, e->xq);
+    else attn_combine_quant_kernel<8><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, e->cur_pos, nh, hd, hq, splits, e->sx, e->xq);
+    BH_HIP(hipGetLastError(), "attention combine launch");
+    return BH_OK;
+}
+
+// `splits`: key chunks of KCH covering the longest row of this launch (the
+// workspace stride; chunks past a row's position exit immediately).
 int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, const uint32_t* seq, int n_out,
-             const int* out_map, bool decode) {
+             const int* out_map, bool decode, int splits) {
+    e->cur_pos = pos;
     const bh_qwen3_config& c = e->c;
     const int d = (int)c.d_model, ff = (int)c.d_ff, hd = (int)c.head_dim;
-    const int nh = (int)c.n_heads, nkv = (int)c.n_kv_heads, G = nh / nkv;
+    const int nh = (int)c.n_heads, nkv = (int)c.n_kv_heads;
     const float scale = 1.0f / sqrtf((float)hd);
-    const int sstride = (int)((e->max_seq + 3) & ~3u);
-    const size_t attn_lds = ((size_t)G * sstride + (size_t)G * hd) * sizeof(float);
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         const bh_qwen3::Layer& Ly = e->L[l];
         float* kc = e->kc + l * e->layer_kv;
@@ -579,10 +652,11 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
                     (int)e->max_seq, (int)c.qk_norm, c.rms_eps, c.rope_theta};
         qk_rope_append_kernel<<<dim3(rows, nh + 2 * nkv), 64, 0, e->stream>>>(ra);
         BH_HIP(hipGetLastError(), "qk_rope_append launch");
-        AttnArgs aa{e->q, kc, vc, pos, seq, e->ctx, nh, nkv, hd, (int)e->hq, (int)e->hkv, (int)e->max_seq, sstride, scale};
-        attention_kernel<<<dim3(rows, nkv), RT, attn_lds, e->stream>>>(aa);
+        AttnArgs aa{e->q, kc, vc, pos, seq, e->part_o, e->part_ml, nh, nkv, hd, (int)e->hq, (int)e->hkv,
+                    (int)e->max_seq, splits, scale};
+        attn_split_kernel<<<dim3(rows, nkv, splits), RT, 0, e->stream>>>(aa);
         BH_HIP(hipGetLastError(), "attention launch");
-        BH_HIP(launch_quantize_rows(e->stream, e->ctx, rows, (int)e->hq, e->sx, e->xq), "quantize ctx");
+        BH_TRY(launch_combine_quant(e, rows, splits));
         BH_TRY(launch_linear(e, Ly.wo, Ly.so, e->proj, rows, (int)e->hq, d));
         NormQuantArgs nb{};
         nb.a = e->res;
@@ -740,9 +814,7 @@ int bh_qwen3_create(const bh_qwen3_config* cfg, uint32_t max_batch, uint32_t max
         return fail(BH_ERR_INVALID, "bh_qwen3_create: widths must be multiples of 4 and <= 8192");
     if (!max_batch || !max_seq || max_rows < max_batch)
         return fail(BH_ERR_INVALID, "bh_qwen3_create: max_batch %u max_seq %u max_rows %u", max_batch, max_seq, max_rows);
-    const uint64_t G = c.n_heads / c.n_kv_heads;
-    if ((G * ((max_seq + 3) & ~3u) + G * c.head_dim) * 4 > 64 * 1024)
-        return fail(BH_ERR_INVALID, "bh_qwen3_create: max_seq %u too long for the attention kernel's LDS", max_seq);
+    if (max_seq > 65536) return fail(BH_ERR_INVALID, "bh_qwen3_create: max_seq %u above 65536", max_seq);
     if (hipSetDevice(device) != hipSuccess) return fail(BH_ERR_HIP, "bh_qwen3_create: hipSetDevice(%d)", device);
     bh_qwen3* e = new bh_qwen3();
     e->c = c;
@@ -754,6 +826,7 @@ int bh_qwen3_create(const bh_qwen3_config* cfg, uint32_t max_batch, uint32_t max
     e->hkv = c.n_kv_heads * c.head_dim;
     e->W = e->hq + 2 * e->hkv;
     e->xq_words = std::max(std::max(c.d_model, e->hq), c.d_ff) / 4;
+    e->max_splits = (max_seq + KCH - 1) / KCH;
     auto bail = [&](int rc) {
         delete e;
         return rc;
@@ -779,7 +852,7 @@ int bh_qwen3_create(const bh_qwen3_config* cfg, uint32_t max_batch, uint32_t max
         (rc = dalloc(e, &e->head, (uint64_t)c.vocab * d / 4)) || (rc = dalloc(e, &e->shead, c.vocab)) ||
         (rc = dalloc(e, &e->kc, e->layer_kv * c.n_layers)) || (rc = dalloc(e, &e->vc, e->layer_kv * c.n_layers)) ||
         (rc = dalloc(e, &e->res, R * d)) || (rc = dalloc(e, &e->qkv, R * e->W)) || (rc = dalloc(e, &e->q, R * hq)) ||
-        (rc = dalloc(e, &e->ctx, R * hq)) || (rc = dalloc(e, &e->proj, R * d)) || (rc = dalloc(e, &e->gu, R * 2 * ff)) ||
+        (rc = dalloc(e, &e->part_o, R * c.n_heads * e->max_splits * c.head_dim)) || (rc = dalloc(e, &e->part_ml, R * c.n_heads * e->max_splits * 2)) || (rc = dalloc(e, &e->proj, R * d)) || (rc = dalloc(e, &e->gu, R * 2 * ff)) ||
         (rc = dalloc(e, &e->sx, R)) || (rc = dalloc(e, &e->xq, R * e->xq_words)) ||
         (rc = dalloc(e, &e->logits, (uint64_t)max_batch * c.vocab)) || (rc = dalloc(e, &e->tmpw, e->tmpw_floats)) ||
         (rc = dalloc(e, &e->am_v, (uint64_t)max_batch * AM_CH)) || (rc = dalloc(e, &e->am_i, (uint64_t)max_batch * AM_CH)) ||
@@ -889,7 +962,8 @@ int bh_qwen3_prefill(bh_qwen3* e, const uint32_t* tokens, uint32_t batch, uint32
         BH_HIP(hipMemcpyAsync(e->pos_rows, pos.data(), rows * 4, hipMemcpyHostToDevice, e->stream), "upload");
         BH_HIP(hipMemcpyAsync(e->seq_rows, seq.data(), rows * 4, hipMemcpyHostToDevice, e->stream), "upload");
         if (last) BH_HIP(hipMemcpyAsync(e->row_map, map.data(), batch * 4, hipMemcpyHostToDevice, e->stream), "upload");
-        BH_TRY(run_rows(e, (int)rows, e->tok_rows, e->pos_rows, e->seq_rows, last ? (int)batch : 0, e->row_map, false));
+        BH_TRY(run_rows(e, (int)rows, e->tok_rows, e->pos_rows, e->seq_rows, last ? (int)batch : 0, e->row_map, false,
+                        (int)((p0 + cc + KCH - 1) / KCH)));
         BH_TRY(sync(e));  // the host vectors are reused by the next chunk
     }
     std::vector<uint32_t> pdec(batch, len);
@@ -913,7 +987,8 @@ int bh_qwen3_decode(bh_qwen3* e, uint32_t steps, uint32_t flags, uint32_t* out) 
     (void)hipSetDevice(e->device);
     const int b = (int)e->batch;
     if (flags & BH_QWEN3_EAGER) {
-        for (uint32_t s = 0; s < steps; ++s) BH_TRY(run_rows(e, b, e->tok_dec, e->pos_dec, e->seq_dec, b, nullptr, true));
+        for (uint32_t s = 0; s < steps; ++s)
+            BH_TRY(run_rows(e, b, e->tok_dec, e->pos_dec, e->seq_dec, b, nullptr, true, (int)e->max_splits));
     } else {
         if (!e->graph || e->graph_batch != e->batch) {
             if (e->graph) {
@@ -922,7 +997,7 @@ int bh_qwen3_decode(bh_qwen3* e, uint32_t steps, uint32_t flags, uint32_t* out) 
             }
             hipGraph_t g = nullptr;
             BH_HIP(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal), "begin capture");
-            const int rc = run_rows(e, b, e->tok_dec, e->pos_dec, e->seq_dec, b, nullptr, true);
+            const int rc = run_rows(e, b, e->tok_dec, e->pos_dec, e->seq_dec, b, nullptr, true, (int)e->max_splits);
             const hipError_t ce = hipStreamEndCapture(e->stream, &g);
             if (rc != BH_OK) {
                 if (g) (void)hipGraphDestroy(g);
