@@ -42,8 +42,9 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on CPU-baseline work")
-    ap.add_argument("--only", default="", help="profiling aid: 'decode', 'prefill', 'qwen3' or 'copy' only")
+    ap.add_argument("--only", default="", help="profiling aid: 'decode', 'prefill', 'qwen3', 'dit' or 'copy' only")
     ap.add_argument("--no-qwen3", action="store_true")
+    ap.add_argument("--no-dit", action="store_true")
     return ap.parse_args()
 
 
@@ -287,6 +288,31 @@ def bench_qwen3(prompt_len=128, gen=256, batches=(1, 8)):
     return out
 
 
+def bench_dit(reps=5):
+    """the DiT int8 linear stack (brain_amd.dit), 30 layers at
+    M=1152, one HIP graph per step; TOPS over the 4 linears of every layer."""
+    import torch
+    from brain_amd import dit
+    st = dit.DitInt8Stack(device="cuda")
+    st.capture()
+    st.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        st.replay()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    ops_step = dit.linear_ops() * st.layers
+    out = {"workload": "configs[4]: 30 layers x (quant 3840 -> QKV 3840x11520, out 3840x3840, quant -> FFN up "
+                       "3840x10240, quant 10240 -> down 10240x3840), M=1152, bf16 activations",
+           "ms_per_step": round(dt * 1e3, 3), "tops": round(ops_step / dt / 1e12, 1),
+           "frac_of_int8_peak": round(ops_step / dt / 1e12 / INT8_PEAK_TOPS, 4)}
+    assert torch.isfinite(st.x.float()).all()
+    del st
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(budget_s):
     """The restated backend-cpu decode path (max_abs_row -> quant_pack ->
     matmul_i8_gemv, OpenMP over output columns) on this host, on the same
@@ -356,6 +382,8 @@ def main():
         res["prefill"] = bench_prefill(torch, lib, dev, gen, args.prefill_reps)
     if args.only in ("", "qwen3") and not args.no_qwen3:
         res["qwen3"] = bench_qwen3()
+    if args.only in ("", "dit") and not args.no_dit:
+        res["dit"] = bench_dit()
     if args.only:
         print(json.dumps(res))
         return
@@ -403,6 +431,8 @@ def main():
         line["prefill"] = res["prefill"]
     if "qwen3" in res:
         line["qwen3_e2e"] = res["qwen3"]
+    if "dit" in res:
+        line["dit_stack"] = res["dit"]
     if cpu is not None:
         line["gpu_vs_cpu"] = round(value / cpu["value"], 1)
     print(json.dumps(line))

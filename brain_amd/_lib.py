@@ -62,6 +62,7 @@ SIGNATURES = {
     "bh_max_abs_rows": (i32, [vp, vp, u32, u32, vp]),
     "bh_quant_pack": (i32, [vp, vp, vp, u32, u32, vp]),
     "bh_quantize_rows": (i32, [vp, vp, u32, u32, vp, vp]),
+    "bh_quantize_rows_bf16": (i32, [vp, vp, u32, u32, vp, vp]),
     "bh_matmul_i8": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
     "bh_matmul_i8_gemv": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
     "bh_matmul_i8_dyn": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),

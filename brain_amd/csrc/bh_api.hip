@@ -25,6 +25,7 @@ namespace bh {
 hipError_t launch_max_abs_rows(hipStream_t s, const float* x, int m, int k, float* sx);
 hipError_t launch_quant_pack(hipStream_t s, const float* x, const float* sx, int m, int k, uint32_t* xq);
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, float* sx, uint32_t* xq);
+hipError_t launch_quantize_rows_bf16(hipStream_t s, const uint16_t* x, int m, int k, float* sx, uint32_t* xq);
 hipError_t launch_quantize_weight(hipStream_t s, const float* w, int n, int k, uint32_t* packed, float* sw);
 hipError_t launch_gemv_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n);
@@ -206,6 +207,14 @@ int bh_quantize_rows(void* stream, const float* x, uint32_t m, uint32_t k, float
     if (m == 0) return BH_OK;
     if (!sx || (k > 0 && (!x || !xq))) return fail(BH_ERR_INVALID, "bh_quantize_rows: null buffer");
     return hip_status(launch_quantize_rows((hipStream_t)stream, x, (int)m, (int)k, sx, xq), "quantize_rows launch");
+}
+
+int bh_quantize_rows_bf16(void* stream, const uint16_t* x, uint32_t m, uint32_t k, float* sx, uint32_t* xq) {
+    if (k % 4 != 0) return fail(BH_ERR_INVALID, "bh_quantize_rows_bf16: k=%u is not a multiple of 4", k);
+    if (m > I32MAX || k > I32MAX) return fail(BH_ERR_INVALID, "bh_quantize_rows_bf16: m=%u k=%u", m, k);
+    if (m == 0) return BH_OK;
+    if (!sx || (k > 0 && (!x || !xq))) return fail(BH_ERR_INVALID, "bh_quantize_rows_bf16: null buffer");
+    return hip_status(launch_quantize_rows_bf16((hipStream_t)stream, x, (int)m, (int)k, sx, xq), "quantize_rows_bf16 launch");
 }
 
 int bh_matmul_i8_gemv(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,

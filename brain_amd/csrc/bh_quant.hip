@@ -134,6 +134,80 @@ __global__ __launch_bounds__(QT) void quantize_rows_kernel(const float* __restri
     }
 }
 
+// Per-token quantization of bf16 activations: widening bf16 to f32 is exact
+// (the bits shifted up by 16), so this is quantize_rows on f32(x), bit for
+// bit. Register version: each thread keeps NV 16-byte groups (8 values) of the
+// row; k % 8 == 0, x 16-byte aligned, k <= 8 * QT * NV.
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+template <int NV>
+__global__ __launch_bounds__(QT) void quantize_rows_bf16_kernel(const uint16_t* __restrict__ x, int m, int k,
+                                                                float* __restrict__ sx, uint32_t* __restrict__ xq) {
+    const int row = blockIdx.x;
+    if (row >= m) return;
+    const int k8 = k >> 3;
+    const uint4* xr = reinterpret_cast<const uint4*>(x + (int64_t)row * k);
+    uint4 v[NV];
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int g = threadIdx.x + i * QT;
+        v[i] = g < k8 ? xr[g] : make_uint4(0u, 0u, 0u, 0u);
+        const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a = fmaxf(a, fmaxf(fabsf(bf16_lo(w[j])), fabsf(bf16_hi(w[j]))));
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
+    __shared__ float red[QT / 64];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = a;
+    __syncthreads();
+    float mx = red[0];
+#pragma unroll
+    for (int w = 1; w < QT / 64; ++w) mx = fmaxf(mx, red[w]);
+    const float s = fmaxf(mx, 1e-8f) / 127.0f;
+    if (threadIdx.x == 0) sx[row] = s;
+    const float inv = 1.0f / s;
+    uint2* q = reinterpret_cast<uint2*>(xq + (int64_t)row * (k >> 2));
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int g = threadIdx.x + i * QT;
+        if (g >= k8) continue;
+        const uint32_t lo = quant_word(make_float4(bf16_lo(v[i].x), bf16_hi(v[i].x), bf16_lo(v[i].y), bf16_hi(v[i].y)), inv);
+        const uint32_t hi = quant_word(make_float4(bf16_lo(v[i].z), bf16_hi(v[i].z), bf16_lo(v[i].w), bf16_hi(v[i].w)), inv);
+        q[g] = make_uint2(lo, hi);
+    }
+}
+
+// Any k % 4 == 0 and alignment: two passes of scalar loads.
+__global__ __launch_bounds__(QT) void quantize_rows_bf16_any_kernel(const uint16_t* __restrict__ x, int m, int k,
+                                                                    float* __restrict__ sx,
+                                                                    uint32_t* __restrict__ xq) {
+    const int row = blockIdx.x;
+    if (row >= m) return;
+    const uint16_t* xr = x + (int64_t)row * k;
+    float a = 0.0f;
+    for (int i = threadIdx.x; i < k; i += QT) a = fmaxf(a, fabsf(__uint_as_float((uint32_t)xr[i] << 16)));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
+    __shared__ float red[QT / 64];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = a;
+    __syncthreads();
+    float mx = red[0];
+#pragma unroll
+    for (int w = 1; w < QT / 64; ++w) mx = fmaxf(mx, red[w]);
+    const float s = fmaxf(mx, 1e-8f) / 127.0f;
+    if (threadIdx.x == 0) sx[row] = s;
+    const float inv = 1.0f / s;
+    uint32_t* q = xq + (int64_t)row * (k >> 2);
+    for (int g = threadIdx.x; g < (k >> 2); g += QT) {
+        const float4 v = make_float4(__uint_as_float((uint32_t)xr[4 * g] << 16), __uint_as_float((uint32_t)xr[4 * g + 1] << 16),
+                                     __uint_as_float((uint32_t)xr[4 * g + 2] << 16), __uint_as_float((uint32_t)xr[4 * g + 3] << 16));
+        q[g] = quant_word(v, inv);
+    }
+}
+
 // Per-output-row weight quantization (crates/model/src/int8.rs:33-59):
 // sw = max(max|w|, 1e-8)/127, q = clamp(round_half_away(w*(1/sw)), +-127),
 // NaN -> 0 (Rust's saturating `as i32`).
@@ -183,6 +257,20 @@ hipError_t launch_quant_pack(hipStream_t s, const float* x, const float* sx, int
     if (blocks > 65536) blocks = 65536;
     if (al16(x)) quant_pack_kernel<true><<<(unsigned)blocks, QT, 0, s>>>(x, sx, m, k, xq);
     else quant_pack_kernel<false><<<(unsigned)blocks, QT, 0, s>>>(x, sx, m, k, xq);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_rows_bf16(hipStream_t s, const uint16_t* x, int m, int k, float* sx, uint32_t* xq) {
+    if (m <= 0) return hipSuccess;
+    const int k8 = k / 8;
+    if (k % 8 == 0 && al16(x) && k8 <= 8 * QT) {
+        if (k8 <= QT) quantize_rows_bf16_kernel<1><<<m, QT, 0, s>>>(x, m, k, sx, xq);
+        else if (k8 <= 2 * QT) quantize_rows_bf16_kernel<2><<<m, QT, 0, s>>>(x, m, k, sx, xq);
+        else if (k8 <= 4 * QT) quantize_rows_bf16_kernel<4><<<m, QT, 0, s>>>(x, m, k, sx, xq);
+        else quantize_rows_bf16_kernel<8><<<m, QT, 0, s>>>(x, m, k, sx, xq);
+    } else {
+        quantize_rows_bf16_any_kernel<<<m, QT, 0, s>>>(x, m, k, sx, xq);
+    }
     return hipGetLastError();
 }
 

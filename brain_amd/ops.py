@@ -68,6 +68,17 @@ def quantize_rows(x, sx=None, xq=None):
     return sx, xq
 
 
+def quantize_rows_bf16(x, sx=None, xq=None):
+    """Per-token quantization of bf16 activations (exactly quantize_rows of x.float())."""
+    m, k = x.shape
+    _dev(x)
+    _need(x, torch.bfloat16, m * k, "x")
+    sx = torch.empty(m, device=x.device, dtype=torch.float32) if sx is None else sx
+    xq = torch.empty(m, k // 4, device=x.device, dtype=torch.int32) if xq is None else xq
+    check(load().bh_quantize_rows_bf16(_stream(), _ptr(x), m, k, _ptr(sx), _ptr(xq)))
+    return sx, xq
+
+
 _VARIANTS = {"auto": "bh_matmul_i8", "gemv": "bh_matmul_i8_gemv", "dyn": "bh_matmul_i8_dyn"}
 
 

@@ -74,6 +74,13 @@ int bh_quant_pack(void* stream, const float* x, const float* sx, uint32_t m, uin
  * (crates/model/src/int8.rs:221-235). */
 int bh_quantize_rows(void* stream, const float* x, uint32_t m, uint32_t k, float* sx, uint32_t* xq);
 
+/* bf16 activations (raw bf16 bits [m,k]): quantize_rows of the exactly
+ * widened f32 values. The DiT-style stacks keep activations in bf16 between
+ * linears; the reference's quant_pack reads f32 (quant_pack.wgsl:26-45), and
+ * bf16 -> f32 is exact, so the bytes and scales equal bh_quantize_rows on
+ * f32(x). */
+int bh_quantize_rows_bf16(void* stream, const uint16_t* x, uint32_t m, uint32_t k, float* sx, uint32_t* xq);
+
 /* W8A8 matmul, variant chosen by bh_select_i8 (GEMV for m <= 32, MFMA tile
  * otherwise). Replaces the `matmul_i8_dyn` / `matmul_i8_gemv` dispatches,
  * bindings [xq, wq, sx, sw, out], params [m, kg, n]
