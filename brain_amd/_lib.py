@@ -82,6 +82,15 @@ SIGNATURES = {
     "bh_qwen3_logits": (i32, [vp, vp, u64]),
     "bh_qwen3_lengths": (i32, [vp, vp, u32]),
     "bh_qwen3_stream": (vp, [vp]),
+    "bh_qwen3_load": (i32, [vp, C.c_char_p]),
+    "bh_qwen3_autotune": (i32, [vp, u32]),
+    "bh_tune_i8": (i32, [vp, u32, u32, u32, u32, vp, vp]),
+    "bh_tune_set": (i32, [u32, u32, u32, i32]),
+    "bh_tune_get": (i32, [u32, u32, u32]),
+    "bh_tune_clear": (None, []),
+    "bh_tune_save": (i32, [C.c_char_p]),
+    "bh_tune_load": (i32, [C.c_char_p]),
+    "bh_st_describe": (i32, [C.c_char_p, C.c_char_p, vp, vp, u32, vp]),
     "bh_backend_create": (i32, [P(C.c_char_p), P(C.c_char_p), u32, i32, u32, P(vp)]),
     "bh_backend_destroy": (None, [vp]),
     "bh_backend_kind": (C.c_char_p, [vp]),

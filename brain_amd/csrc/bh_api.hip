@@ -13,6 +13,8 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <map>
+#include <tuple>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -177,6 +179,26 @@ static int check_matmul(const void* xq, const void* wq, const void* sx, const vo
 
 static const int GEMV_MAX_ROWS = 32;
 
+// Measured GEMV-vs-tile choices, keyed by (row bucket, n, k): the bucket is m
+// rounded up to a power of two (m <= 32), as Engine::mm8 keys its tuned map
+// (crates/qwen3/src/serve.rs:1088-1097).
+static std::mutex g_tune_mu;
+static std::map<std::tuple<uint32_t, uint32_t, uint32_t>, int> g_tune;
+
+static uint32_t row_bucket(uint32_t m) {
+    uint32_t b = 1;
+    while (b < m) b <<= 1;
+    return std::min<uint32_t>(b, GEMV_MAX_ROWS);
+}
+
+// The tuned variant for this shape, or 0 when none was measured.
+int tuned_variant(uint32_t m, uint32_t n, uint32_t k) {
+    if (m == 0 || m > (uint32_t)GEMV_MAX_ROWS) return 0;
+    std::lock_guard<std::mutex> g(g_tune_mu);
+    auto it = g_tune.find({row_bucket(m), n, k});
+    return it == g_tune.end() ? 0 : it->second;
+}
+
 }  // namespace bh
 
 using namespace bh;
@@ -289,6 +311,7 @@ int bh_matmul_i8(void* stream, const uint32_t* xq, const uint32_t* wq, const flo
                  const float* bias, void* out, int out_dtype, uint32_t m, uint32_t kg, uint32_t n) {
     int v[2];
     bh_select_i8(m, n, kg * 4, 1, 1, v);
+    if (const int t = tuned_variant(m, n, kg * 4)) v[0] = t;
     if (v[0] == BH_VARIANT_WORKGROUP_PER_OUTPUT)
         return bh_matmul_i8_gemv(stream, xq, wq, sx, sw, bias, out, out_dtype, m, kg, n);
     return bh_matmul_i8_dyn(stream, xq, wq, sx, sw, bias, out, out_dtype, m, kg, n);
@@ -332,6 +355,133 @@ int bh_roof_mfma_i8(void* stream, uint32_t blocks, uint32_t iters, int32_t* out)
     if (blocks == 0 || blocks > I32MAX || !out) return fail(BH_ERR_INVALID, "bh_roof_mfma_i8: blocks=%u", blocks);
     roof_mfma_i8_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(iters, out);
     return hip_status(hipGetLastError(), "roof_mfma_i8 launch");
+}
+
+// ---------------------------------------------------------------- autotune
+// Engine::measure_i8 (crates/qwen3/src/serve.rs:1133-1158): both candidates on
+// the same buffers, `reps` dispatches back to back after one warm-up, mean ms
+// per dispatch; the faster is recorded for the shape's row bucket.
+int bh_tune_i8(void* stream, uint32_t m, uint32_t k, uint32_t n, uint32_t reps, int* variant, float ms[2]) {
+    if (!variant || m == 0 || m > (uint32_t)GEMV_MAX_ROWS || n == 0 || k == 0 || k % 4 || reps == 0 ||
+        (uint64_t)n * k > I32MAX)
+        return fail(BH_ERR_INVALID, "bh_tune_i8: m=%u k=%u n=%u reps=%u (m must be 1..32)", m, k, n, reps);
+    hipStream_t st = (hipStream_t)stream;
+    void *xq = nullptr, *wq = nullptr, *sx = nullptr, *sw = nullptr, *out = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int rc = BH_OK;
+    float t[2] = {0.f, 0.f};
+    auto cleanup = [&]() {
+        if (e0) (void)hipEventDestroy(e0);
+        if (e1) (void)hipEventDestroy(e1);
+        for (void* p : {xq, wq, sx, sw, out})
+            if (p) (void)hipFree(p);
+    };
+    if (hipMalloc(&xq, (size_t)m * k) != hipSuccess || hipMalloc(&wq, (size_t)n * k) != hipSuccess ||
+        hipMalloc(&sx, (size_t)m * 4) != hipSuccess || hipMalloc(&sw, (size_t)n * 4) != hipSuccess ||
+        hipMalloc(&out, (size_t)m * n * 4) != hipSuccess) {
+        cleanup();
+        return fail(BH_ERR_NOMEM, "bh_tune_i8: scratch allocation failed");
+    }
+    (void)hipMemsetAsync(xq, 1, (size_t)m * k, st);
+    (void)hipMemsetAsync(wq, 1, (size_t)n * k, st);
+    (void)hipMemsetAsync(sx, 0, (size_t)m * 4, st);
+    (void)hipMemsetAsync(sw, 0, (size_t)n * 4, st);
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+        cleanup();
+        return fail(BH_ERR_HIP, "bh_tune_i8: event creation failed");
+    }
+    const int cand[2] = {BH_VARIANT_WORKGROUP_PER_OUTPUT, BH_VARIANT_PACKED_INT8};
+    for (int c = 0; c < 2 && rc == BH_OK; ++c) {
+        auto run = [&]() {
+            return cand[c] == BH_VARIANT_WORKGROUP_PER_OUTPUT
+                       ? bh_matmul_i8_gemv(stream, (const uint32_t*)xq, (const uint32_t*)wq, (const float*)sx,
+                                           (const float*)sw, nullptr, out, OUT_F32, m, k / 4, n)
+                       : bh_matmul_i8_dyn(stream, (const uint32_t*)xq, (const uint32_t*)wq, (const float*)sx,
+                                          (const float*)sw, nullptr, out, OUT_F32, m, k / 4, n);
+        };
+        if ((rc = run()) != BH_OK) break;
+        (void)hipEventRecord(e0, st);
+        for (uint32_t i = 0; i < reps && rc == BH_OK; ++i) rc = run();
+        (void)hipEventRecord(e1, st);
+        if (rc == BH_OK && hipEventSynchronize(e1) == hipSuccess) {
+            (void)hipEventElapsedTime(&t[c], e0, e1);
+            t[c] /= (float)reps;
+        }
+    }
+    cleanup();
+    if (rc != BH_OK) return rc;
+    const int best = t[0] <= t[1] ? cand[0] : cand[1];
+    {
+        std::lock_guard<std::mutex> g(g_tune_mu);
+        g_tune[{row_bucket(m), n, k}] = best;
+    }
+    *variant = best;
+    if (ms) {
+        ms[0] = t[0];
+        ms[1] = t[1];
+    }
+    return BH_OK;
+}
+
+int bh_tune_set(uint32_t m, uint32_t n, uint32_t k, int variant) {
+    if (m == 0 || m > (uint32_t)GEMV_MAX_ROWS ||
+        (variant != BH_VARIANT_WORKGROUP_PER_OUTPUT && variant != BH_VARIANT_PACKED_INT8 && variant != 0))
+        return fail(BH_ERR_INVALID, "bh_tune_set: m=%u variant=%d", m, variant);
+    std::lock_guard<std::mutex> g(g_tune_mu);
+    if (variant == 0) g_tune.erase({row_bucket(m), n, k});
+    else g_tune[{row_bucket(m), n, k}] = variant;
+    return BH_OK;
+}
+
+void bh_tune_clear(void) {
+    std::lock_guard<std::mutex> g(g_tune_mu);
+    g_tune.clear();
+}
+
+int bh_tune_get(uint32_t m, uint32_t n, uint32_t k) { return tuned_variant(m, n, k); }
+
+// Text store (gpu_core::tune::FileTuneStore's role): a header naming the
+// format, the ABI version and the gfx target, then "m n k variant" lines.
+static const char* TUNE_HEADER = "brain-hip-tune 1 gfx950";
+
+int bh_tune_save(const char* path) {
+    if (!path) return fail(BH_ERR_INVALID, "bh_tune_save: null path");
+    FILE* f = fopen(path, "w");
+    if (!f) return fail(BH_ERR_INVALID, "bh_tune_save: cannot write %s", path);
+    std::lock_guard<std::mutex> g(g_tune_mu);
+    fprintf(f, "%s abi %d\n", TUNE_HEADER, BH_ABI_VERSION);
+    for (const auto& kv : g_tune)
+        fprintf(f, "%u %u %u %d\n", std::get<0>(kv.first), std::get<1>(kv.first), std::get<2>(kv.first), kv.second);
+    fclose(f);
+    return BH_OK;
+}
+
+int bh_tune_load(const char* path) {
+    if (!path) return fail(BH_ERR_INVALID, "bh_tune_load: null path");
+    FILE* f = fopen(path, "r");
+    if (!f) return fail(BH_ERR_INVALID, "bh_tune_load: cannot read %s", path);
+    char line[256];
+    char want[128];
+    snprintf(want, sizeof want, "%s abi %d", TUNE_HEADER, BH_ABI_VERSION);
+    if (!fgets(line, sizeof line, f) || strncmp(line, want, strlen(want)) != 0) {
+        fclose(f);
+        return fail(BH_ERR_INVALID, "bh_tune_load: %s was not written by this library build", path);
+    }
+    std::map<std::tuple<uint32_t, uint32_t, uint32_t>, int> t;
+    unsigned m, n, k;
+    int v;
+    while (fgets(line, sizeof line, f)) {
+        if (sscanf(line, "%u %u %u %d", &m, &n, &k, &v) != 4 || m == 0 || m > (unsigned)GEMV_MAX_ROWS ||
+            (v != BH_VARIANT_WORKGROUP_PER_OUTPUT && v != BH_VARIANT_PACKED_INT8)) {
+            fclose(f);
+            return fail(BH_ERR_INVALID, "bh_tune_load: bad line in %s: %s", path, line);
+        }
+        t[{row_bucket(m), n, k}] = v;
+    }
+    fclose(f);
+    std::lock_guard<std::mutex> g(g_tune_mu);
+    for (const auto& kv : t) g_tune[kv.first] = kv.second;
+    return (int)t.size();
 }
 
 // ---------------------------------------------------------------- host quantizer

@@ -42,6 +42,7 @@
 
 #include "../../include/brain_hip.h"
 #include "bh_common.h"
+#include "bh_st.h"
 
 namespace bh {
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, float* sx, uint32_t* xq);
@@ -50,6 +51,8 @@ hipError_t launch_gemv_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n);
 hipError_t launch_gemm_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n);
+
+int tuned_variant(uint32_t m, uint32_t n, uint32_t k);
 
 namespace {
 
@@ -576,7 +579,9 @@ int dalloc(bh_qwen3* e, T** p, size_t count) {
     } while (0)
 
 int launch_linear(bh_qwen3* e, const uint32_t* w, const float* sw, float* out, int m, int k, int n) {
-    hipError_t err = m <= 32 ? launch_gemv_i8(e->stream, e->xq, w, e->sx, sw, nullptr, out, OUT_F32, m, k / 4, n)
+    const int tuned = tuned_variant((uint32_t)m, (uint32_t)n, (uint32_t)k);
+    const bool gemv = tuned ? tuned == BH_VARIANT_WORKGROUP_PER_OUTPUT : m <= 32;
+    hipError_t err = gemv ? launch_gemv_i8(e->stream, e->xq, w, e->sx, sw, nullptr, out, OUT_F32, m, k / 4, n)
                              : launch_gemm_i8(e->stream, e->xq, w, e->sx, sw, nullptr, out, OUT_F32, m, k / 4, n);
     BH_HIP(err, "int8 linear launch");
     return BH_OK;
@@ -905,6 +910,84 @@ int bh_qwen3_set_weight_i8(bh_qwen3* e, const char* name, const uint32_t* packed
     BH_HIP(hipMemcpyAsync(t.packed, packed, (size_t)n * k, hipMemcpyHostToDevice, e->stream), "upload");
     BH_HIP(hipMemcpyAsync(t.scale, scale, (size_t)n * 4, hipMemcpyHostToDevice, e->stream), "upload");
     return sync(e);
+}
+
+static int upload_chunked(bh_qwen3* e, void* dst, const uint8_t* src, size_t bytes) {
+    constexpr size_t CH = 64u << 20;
+    for (size_t off = 0; off < bytes; off += CH) {
+        const size_t len = std::min(CH, bytes - off);
+        BH_HIP(hipMemcpyAsync(static_cast<uint8_t*>(dst) + off, src + off, len, hipMemcpyHostToDevice, e->stream),
+               "checkpoint upload");
+        BH_TRY(sync(e));
+    }
+    return BH_OK;
+}
+
+int bh_qwen3_load(bh_qwen3* e, const char* path) {
+    if (!e || !path) return fail(BH_ERR_INVALID, "bh_qwen3_load: null argument");
+    (void)hipSetDevice(e->device);
+    bh::StFile f;
+    std::string err;
+    if (!f.open(path, &err)) return fail(BH_ERR_INVALID, "bh_qwen3_load: %s", err.c_str());
+    for (const std::string& name : param_names(e->c)) {
+        Target t;
+        BH_TRY(resolve(e, name, &t));
+        const bh::StTensor* st = f.find(name);
+        if (!st) return fail(BH_ERR_INVALID, "bh_qwen3_load: %s has no tensor '%s'", path, name.c_str());
+        uint64_t elems = 1;
+        for (uint64_t d : st->shape) elems *= d;
+        if (t.f32) {
+            if (st->dtype != bh::ST_F32 || elems != t.n)
+                return fail(BH_ERR_INVALID, "bh_qwen3_load: '%s' must be F32 with %llu elements", name.c_str(),
+                            (unsigned long long)t.n);
+            BH_TRY(upload_chunked(e, t.f32, f.bytes(*st), elems * 4));
+            if (t.is_emb && e->c.tie_embeddings)
+                BH_TRY(quantize_into(e, e->emb, e->c.vocab, e->c.d_model, e->head, e->shead));
+            continue;
+        }
+        if (st->dtype == bh::ST_U32) {
+            const bh::StTensor* sc = f.find(name + ".scale");
+            if (st->shape.size() != 2 || st->shape[0] != t.n || st->shape[1] * 4 != t.k)
+                return fail(BH_ERR_INVALID, "bh_qwen3_load: packed '%s' must be U32 [%llu, %llu]", name.c_str(),
+                            (unsigned long long)t.n, (unsigned long long)(t.k / 4));
+            if (!sc || sc->dtype != bh::ST_F32 || sc->shape.size() != 1 || sc->shape[0] != t.n)
+                return fail(BH_ERR_INVALID, "bh_qwen3_load: '%s.scale' must be F32 [%llu]", name.c_str(),
+                            (unsigned long long)t.n);
+            BH_TRY(upload_chunked(e, t.packed, f.bytes(*st), t.n * t.k));
+            BH_TRY(upload_chunked(e, t.scale, f.bytes(*sc), t.n * 4));
+        } else if (st->dtype == bh::ST_F32) {
+            if (st->shape.size() != 2 || st->shape[0] != t.n || st->shape[1] != t.k)
+                return fail(BH_ERR_INVALID, "bh_qwen3_load: '%s' must be [%llu, %llu]", name.c_str(),
+                            (unsigned long long)t.n, (unsigned long long)t.k);
+            BH_TRY(upload_chunked(e, e->tmpw, f.bytes(*st), elems * 4));
+            BH_TRY(quantize_into(e, e->tmpw, (uint32_t)t.n, (uint32_t)t.k, t.packed, t.scale));
+        } else {
+            return fail(BH_ERR_INVALID, "bh_qwen3_load: '%s' has an unsupported dtype", name.c_str());
+        }
+    }
+    return sync(e);
+}
+
+int bh_qwen3_autotune(bh_qwen3* e, uint32_t reps) {
+    if (!e) return fail(BH_ERR_INVALID, "bh_qwen3_autotune: null engine");
+    const char* off = getenv("BRAIN_NO_AUTOTUNE");
+    if (off && strcmp(off, "1") == 0) return 0;
+    (void)hipSetDevice(e->device);
+    const uint32_t d = e->c.d_model, ff = e->c.d_ff;
+    const uint32_t shapes[5][2] = {{e->W, d}, {d, e->hq}, {2 * ff, d}, {d, ff}, {e->c.vocab, d}};  // (n, k)
+    int measured = 0;
+    for (uint32_t m = 1; m <= 32 && m <= std::max<uint32_t>(1, e->max_batch); m <<= 1)
+        for (const auto& sh : shapes) {
+            int v = 0;
+            float ms[2];
+            BH_TRY(bh_tune_i8(e->stream, m, sh[1], sh[0], reps ? reps : 8, &v, ms));
+            ++measured;
+        }
+    if (e->graph) {  // the captured step baked in the old choices
+        (void)hipGraphExecDestroy(e->graph);
+        e->graph = nullptr;
+    }
+    return measured;
 }
 
 int bh_qwen3_init_random(bh_qwen3* e, uint64_t seed) {

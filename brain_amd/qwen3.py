@@ -62,6 +62,14 @@ class Qwen3Engine:
         for name, w in weights.items():
             self.set_weight(name, w)
 
+    def load(self, path):
+        """Every parameter from an int8 safetensors checkpoint (brain_amd.int8_format)."""
+        check(load().bh_qwen3_load(self._h, path.encode()))
+
+    def autotune(self, reps=8):
+        """Measure GEMV vs tile for every linear shape at row buckets up to max_batch."""
+        return check(load().bh_qwen3_autotune(self._h, reps))
+
     def init_random(self, seed):
         check(load().bh_qwen3_init_random(self._h, seed))
 

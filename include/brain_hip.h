@@ -274,12 +274,33 @@ int bh_select_i8(uint32_t m, uint32_t n, uint32_t k, int int8_dot, int workgroup
 /* The kernel name a variant binds to (`Ops::bind`, crates/model/src/ops.rs:603-625). */
 const char* bh_variant_kernel(int variant);
 
+/* GEMV-vs-tile autotune (`Engine::tune_i8` / `measure_i8`,
+ * crates/qwen3/src/serve.rs:1117-1158; `AutoTuner`, crates/backend-api/src/select.rs:466-540).
+ * bh_tune_i8 times both candidates for [m,k] x [n,k] (m <= 32) on scratch
+ * buffers, `reps` dispatches each, records the faster for m's power-of-two
+ * row bucket and returns it (ms[0] GEMV, ms[1] tile, mean per dispatch).
+ * bh_matmul_i8 and the Qwen3 engine consult the recorded choices; without
+ * one the static selector applies. The store is a text file: a header naming
+ * this library build, then "m n k variant" lines. */
+int bh_tune_i8(void* stream, uint32_t m, uint32_t k, uint32_t n, uint32_t reps, int* variant, float ms[2]);
+int bh_tune_set(uint32_t m, uint32_t n, uint32_t k, int variant); /* variant 0 removes the entry */
+int bh_tune_get(uint32_t m, uint32_t n, uint32_t k);               /* 0: none recorded */
+void bh_tune_clear(void);
+int bh_tune_save(const char* path);
+int bh_tune_load(const char* path);                                /* returns the entries read */
+
 /* `gpu_core::cost` (crates/gpu-core/src/cost.rs:267-275) for the int8 family:
  * flops, int_ops and bytes of one dispatch of `name` with `params`. */
 typedef struct {
     uint64_t flops, int_ops, bytes;
 } bh_cost_t;
 int bh_cost(const char* name, const uint32_t* params, uint32_t nparams, bh_cost_t* out);
+
+/* Inspect one tensor of a safetensors file (the int8 checkpoint container):
+ * dtype (1 F32, 2 U32, 3 I8, 4 U8, 5 F16, 6 BF16, 7 I32, 0 other), rank and up
+ * to max_rank dims. Host only. */
+int bh_st_describe(const char* path, const char* name, int* dtype, uint64_t* shape, uint32_t max_rank,
+                   uint32_t* rank);
 
 /* ======================================================================
  * D. The int8 Qwen3 decoder (the caller of sections A-C the reference runs
@@ -345,6 +366,19 @@ int bh_qwen3_logits(bh_qwen3* e, float* out, uint64_t n);
 /* Positions filled so far (prompt + decoded) of each sequence: len[batch]. */
 int bh_qwen3_lengths(bh_qwen3* e, uint32_t* len, uint32_t batch);
 void* bh_qwen3_stream(bh_qwen3* e);
+/* Measure the GEMV/tile choice for every distinct linear shape of the engine
+ * at row buckets 1..max_batch (bh_tune_i8); BRAIN_NO_AUTOTUNE=1 skips it, as
+ * in the reference. Returns the number of shapes measured. */
+int bh_qwen3_autotune(bh_qwen3* e, uint32_t reps);
+
+/* Load every parameter from an int8 checkpoint: a safetensors file in which a
+ * quantized linear `name` is U32 [n, k/4] (the packed layout above) with an
+ * F32 sibling `name.scale` [n], and any other tensor is F32
+ * (crates/model/src/int8.rs:112-187, crates/qwen3omnimoe/src/import.rs:420-425).
+ * An F32 linear is quantized on the device as bh_qwen3_set_weight does. The
+ * file is memory-mapped and uploaded in row-aligned chunks, so host memory
+ * stays bounded. Every parameter of the config must be present. */
+int bh_qwen3_load(bh_qwen3* e, const char* path);
 
 #ifdef __cplusplus
 }

@@ -154,3 +154,45 @@ def test_qwen3_0_6b_shape_runs(gpu):
     assert (e2.decode(8, eager=True) == g).all()
     e.close()
     e2.close()
+
+
+def test_int8_checkpoint_load_matches_f32_upload(gpu, tmp_path):
+    """bh_qwen3_load of the int8 safetensors format (packed linears + scales,
+    one linear left F32 to exercise the device-quantize branch) gives exactly
+    the engine that set_weight builds from the f32 weights."""
+    from brain_amd import int8_format as fmt
+    cfg = dict(SMALL, tie_embeddings=0)
+    w = scaled_weights(cfg, seed=21)
+    path = str(tmp_path / "q.safetensors")
+    fmt.write_int8_checkpoint(path, w, keep_f32=("blocks.1.mlp.up.weight",))
+    prompts = np.random.default_rng(8).integers(0, cfg["vocab"], size=(2, 7))
+    a = engine_for(cfg, w, 2, 16)
+    b = Qwen3Engine(cfg, 2, 16)
+    b.load(path)
+    assert (a.generate(prompts, 5) == b.generate(prompts, 5)).all()
+    assert np.array_equal(a.logits(), b.logits())
+    a.close()
+    b.close()
+
+
+def test_autotune_changes_no_result(gpu):
+    """Both candidates are bit-exact, so the measured choice changes speed only."""
+    from brain_amd._lib import load as L
+    cfg = SMALL
+    w = scaled_weights(cfg, seed=22)
+    prompts = np.random.default_rng(9).integers(0, cfg["vocab"], size=(4, 6))
+    a = engine_for(cfg, w, 4, 16)
+    ref = a.generate(prompts, 6)
+    ref_logits = a.logits()
+    assert a.autotune(reps=2) > 0
+    assert L().bh_tune_get(4, cfg["vocab"], cfg["d_model"]) in (1, 2)
+    for v in (1, 2):   # force every decode-regime linear onto one candidate
+        for m in (1, 2, 4):
+            for n, k in ((512, 256), (256, 256), (1024, 256), (256, 512), (1000, 256)):
+                L().bh_tune_set(m, n, k, v)
+        b = engine_for(cfg, w, 4, 16)
+        assert (b.generate(prompts, 6) == ref).all()
+        assert np.array_equal(b.logits(), ref_logits)
+        b.close()
+    L().bh_tune_clear()
+    a.close()
