@@ -679,20 +679,25 @@ struct TileChoice {
     int splits;  // split-K factor
 };
 
-// Pick a tile shape and split-K factor that fill the 256 CUs. Big problems use
-// 256x256 tiles (half the L2->LDS traffic per op of 128x128); when those give
-// too few workgroups, 128x128 tiles, then split K until ~2 workgroups per CU
-// while keeping >= 4 LDS stages (512 K-bytes) per split.
+// Pick the tile shape that finishes first on 256 CUs. A launch runs in rounds
+// of 256 workgroups, so its time is ~ rounds x (time of one tile). A 256x256
+// tile does 4x the work of a 128x128 one at ~1.25x its efficiency (half the
+// LDS-staging bytes per op), measured on MI355X. Hence the costs:
+//   256x256: 4 * ceil(tiles256 / 256)
+//   128x128: 1.25 * ceil(tiles128 / 256)
+// The smaller wins. On the measured configs[2] and configs[4] shapes this
+// picks the faster tile in every case; e.g. 8192x1024x3072 runs 384 big tiles
+// (2 rounds, one half-empty) but 1536 small ones (6 full rounds).
+// Split-K through i32 atomics measured slower than an under-filled grid
+// (2048x1024x3072: 457 us split vs ~60 us unsplit), so it stays off.
 static TileChoice choose_tiles(int m, int kg, int n) {
-    constexpr int CUS = 256;
-    const int kbytes = kg * 4;
-    const int nk = (kbytes + GM_BK - 1) / GM_BK;
+    (void)kg;
+    constexpr long CUS = 256;
     const long t256 = (long)((m + 255) / 256) * ((n + 255) / 256);
-    if (t256 >= CUS) return {0, 1};
-    // Split-K through i32 atomics measured slower than an under-filled grid
-    // (2048x1024x3072: 457 us split vs ~60 us unsplit), so it stays off.
-    (void)nk;
-    return {1, 1};
+    const long t128 = (long)((m + 127) / 128) * ((n + 127) / 128);
+    const double c256 = 4.0 * (double)((t256 + CUS - 1) / CUS);
+    const double c128 = 1.25 * (double)((t128 + CUS - 1) / CUS);
+    return {c256 <= c128 ? 0 : 1, 1};
 }
 
 template <int BM, int BN, int WM, int WN, int OUT, bool HAS_BIAS, bool STATIC, bool SPLITK>
