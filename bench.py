@@ -254,7 +254,22 @@ def qwen3_weight_bytes(c):
     return c["n_layers"] * per_layer + c["vocab"] * d + 4 * rows
 
 
-def bench_qwen3(prompt_len=128, gen=256, batches=(1, 8)):
+def qwen3_cpu_baseline(budget_s=8.0, ctx=128):
+    """The restated backend-cpu int8 decode of the same architecture (oracle
+    or_qwen3_cpu_decode: int8 GEMV per column over OpenMP threads, f32
+    norms/RoPE/attention), batch 1 after `ctx` cached positions; as many steps
+    as fit the budget after a 1-step estimate."""
+    from brain_amd.qwen3 import QWEN3_0_6B
+    from oracle import oracle as o
+    threads = min(16, os.cpu_count() or 1)
+    est = o.qwen3_cpu_decode_seconds(QWEN3_0_6B, threads, ctx, 1)
+    steps = max(2, min(64, int(budget_s / max(est, 1e-3))))
+    secs = o.qwen3_cpu_decode_seconds(QWEN3_0_6B, threads, ctx, steps)
+    return {"value": round(steps / secs, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} greedy int8 decode steps at batch 1 after {ctx} cached positions, random int8 weights"}
+
+
+def bench_qwen3(prompt_len=128, gen=256, batches=(1, 8), cpu=True):
     """Qwen3-0.6B-architecture int8 decoder, random init, greedy.
     Prefill of a random-id prompt, then `gen` decode steps (one HIP graph
     replay each); tok/s = batch * gen / decode wall time."""
@@ -285,6 +300,9 @@ def bench_qwen3(prompt_len=128, gen=256, batches=(1, 8)):
                             "prefill_tok_s": round(b * prompt_len / (t1 - t0), 1),
                             "step_hbm_gbs": round((wbytes + kv_bytes) / step_s / 1e9, 1)}
         e.close()
+    if cpu:
+        out["cpu_baseline"] = qwen3_cpu_baseline()
+        out["batch1_gpu_vs_cpu"] = round(out["batch1"]["decode_tok_s"] / out["cpu_baseline"]["value"], 1)
     return out
 
 
@@ -381,7 +399,7 @@ def main():
     if args.only in ("", "prefill") and not args.no_prefill:
         res["prefill"] = bench_prefill(torch, lib, dev, gen, args.prefill_reps)
     if args.only in ("", "qwen3") and not args.no_qwen3:
-        res["qwen3"] = bench_qwen3()
+        res["qwen3"] = bench_qwen3(cpu=not args.no_cpu)
     if args.only in ("", "dit") and not args.no_dit:
         res["dit"] = bench_dit()
     if args.only:

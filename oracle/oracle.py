@@ -55,6 +55,7 @@ def lib():
             "or_argmax_row": (u32, [vp, u32]),
             "or_qwen3_param_count": (u64, [vp]),
             "or_qwen3_generate": (i32, [vp, vp, i32, vp, u32, u32, u32, vp, vp]),
+            "or_qwen3_cpu_decode": (C.c_double, [vp, u64, i32, u32, u32]),
         }
         for n, (r, a) in sig.items():
             f = getattr(L, n)
@@ -333,3 +334,9 @@ def qwen3_generate(cfg, weights, prompts, steps, int8=True):
 def argmax_row(x):
     x = _c(x, np.float32)
     return lib().or_argmax_row(_p(x), x.size)
+
+
+def qwen3_cpu_decode_seconds(cfg, threads, ctx, steps, seed=1):
+    """or_qwen3_cpu_decode: seconds for `steps` batch-1 int8 decode steps on the CPU."""
+    c = _qcfg(cfg)
+    return lib().or_qwen3_cpu_decode(C.byref(c), seed, threads, ctx, steps)

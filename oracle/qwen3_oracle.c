@@ -263,3 +263,164 @@ int or_qwen3_generate(const or_qwen3_config *c, const float *params, int int8, c
     free(ly);
     return 0;
 }
+
+/* ---------------------------------------------------------------------------
+ * CPU baseline of one int8 decode step at the real shape (bench only).
+ * The linears run backend-cpu's restated int8 GEMV (or_cpu_gemv_packed: one
+ * workgroup per output column, OpenMP over columns, as rayon over
+ * available_parallelism), each activation quantized once per distinct input
+ * (crates/qwen3/src/serve.rs:1059-1066). RMSNorm, RoPE and attention are f32
+ * loops, attention parallel over heads. Weights are random int8 with small
+ * scales, since only time is measured. The KV cache holds `ctx` random
+ * positions, then `steps` greedy steps are timed at batch 1. Returns the
+ * seconds of the timed steps. */
+#include <omp.h>
+
+static uint64_t xs_next(uint64_t *s) {
+    uint64_t x = *s;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    return *s = x;
+}
+
+static void fill_i8(uint32_t *p, size_t words, uint64_t seed) {
+#pragma omp parallel
+    {
+        uint64_t s = seed * 0x9E3779B97F4A7C15ull + (uint64_t)omp_get_thread_num() * 0xBF58476D1CE4E5B9ull + 1;
+#pragma omp for schedule(static)
+        for (long long i = 0; i < (long long)words; ++i) {
+            s ^= (uint64_t)i;
+            p[i] = (uint32_t)xs_next(&s) & 0x7f7f7f7fu;  /* bytes in [0,127]: no -128 */
+        }
+    }
+}
+
+typedef struct {
+    uint32_t *w;
+    float *s;
+    uint32_t n, k;
+} plin_t;
+
+static void plin_make(plin_t *l, uint32_t n, uint32_t k, uint64_t seed) {
+    l->n = n;
+    l->k = k;
+    l->w = (uint32_t *)malloc((size_t)n * k);
+    l->s = (float *)malloc((size_t)n * 4);
+    fill_i8(l->w, (size_t)n * k / 4, seed);
+    for (uint32_t i = 0; i < n; ++i) l->s[i] = 1.0f / (64.0f * sqrtf((float)k));
+}
+
+static void plin_run(const plin_t *l, const uint32_t *xq, const float *sx, int threads, float *out) {
+    or_cpu_gemv_packed(xq, l->w, sx, l->s, 1, l->k / 4, l->n, threads, out);
+}
+
+static void quant1(const float *x, uint32_t k, float *sx, uint32_t *xq) {
+    or_max_abs_row(x, 1, k, sx);
+    or_quant_pack(x, sx, 1, k, xq);
+}
+
+double or_qwen3_cpu_decode(const or_qwen3_config *c, uint64_t seed, int threads, uint32_t ctx, uint32_t steps) {
+    const uint32_t d = c->d_model, ff = c->d_ff, hd = c->head_dim, nh = c->n_heads, nkv = c->n_kv_heads;
+    const uint32_t hq = nh * hd, hkv = nkv * hd, G = nh / nkv, L = c->n_layers, V = c->vocab;
+    const uint32_t T = ctx + steps;
+    omp_set_num_threads(threads);
+    plin_t *q = (plin_t *)calloc(L * 7, sizeof(plin_t)), head;
+    for (uint32_t l = 0; l < L; ++l) {
+        plin_make(&q[7 * l + 0], hq, d, seed + 7 * l + 0);
+        plin_make(&q[7 * l + 1], hkv, d, seed + 7 * l + 1);
+        plin_make(&q[7 * l + 2], hkv, d, seed + 7 * l + 2);
+        plin_make(&q[7 * l + 3], d, hq, seed + 7 * l + 3);
+        plin_make(&q[7 * l + 4], ff, d, seed + 7 * l + 4);
+        plin_make(&q[7 * l + 5], ff, d, seed + 7 * l + 5);
+        plin_make(&q[7 * l + 6], d, ff, seed + 7 * l + 6);
+    }
+    plin_make(&head, V, d, seed + 7 * L);
+    float *K = (float *)malloc(sizeof(float) * (size_t)L * T * hkv);
+    float *Vc = (float *)malloc(sizeof(float) * (size_t)L * T * hkv);
+    uint64_t rs = seed | 1;
+    for (size_t i = 0; i < (size_t)L * T * hkv; ++i) {
+        K[i] = (float)(int32_t)(xs_next(&rs) & 0xffff) / 65536.0f - 0.5f;
+        Vc[i] = (float)(int32_t)(xs_next(&rs) & 0xffff) / 65536.0f - 0.5f;
+    }
+    float *gain = (float *)malloc(sizeof(float) * (d > hd ? d : hd));
+    for (uint32_t i = 0; i < (d > hd ? d : hd); ++i) gain[i] = 1.0f;
+    float *x = (float *)malloc(4 * d), *xn = (float *)malloc(4 * d), *qv = (float *)malloc(4 * hq);
+    float *kv = (float *)malloc(4 * hkv), *vv = (float *)malloc(4 * hkv), *cx = (float *)malloc(4 * hq);
+    float *o = (float *)malloc(4 * d), *g = (float *)malloc(4 * ff), *u = (float *)malloc(4 * ff);
+    float *lg = (float *)malloc(4 * (size_t)V), *tmp = (float *)malloc(4 * hd);
+    uint32_t *xq = (uint32_t *)malloc(ff > d ? ff : (hq > d ? hq : d));
+    float sx;
+    const float scale = 1.0f / sqrtf((float)hd);
+    uint32_t cur = 1;
+    const double t0 = omp_get_wtime();
+    for (uint32_t pos = ctx; pos < T; ++pos) {
+        for (uint32_t e = 0; e < d; ++e) x[e] = (float)((cur * 2654435761u + e * 40503u) & 1023) / 1024.0f - 0.5f;
+        for (uint32_t l = 0; l < L; ++l) {
+            float *Kl = K + (size_t)l * T * hkv, *Vl = Vc + (size_t)l * T * hkv;
+            rmsnorm(x, gain, d, c->rms_eps, xn);
+            quant1(xn, d, &sx, xq);
+            plin_run(&q[7 * l + 0], xq, &sx, threads, qv);
+            plin_run(&q[7 * l + 1], xq, &sx, threads, kv);
+            plin_run(&q[7 * l + 2], xq, &sx, threads, vv);
+            for (uint32_t h = 0; h < nh; ++h) {
+                rmsnorm(qv + h * hd, gain, hd, c->rms_eps, tmp);
+                memcpy(qv + h * hd, tmp, 4 * hd);
+                rope(qv + h * hd, hd, pos, c->rope_theta);
+            }
+            for (uint32_t h = 0; h < nkv; ++h) {
+                rmsnorm(kv + h * hd, gain, hd, c->rms_eps, tmp);
+                memcpy(kv + h * hd, tmp, 4 * hd);
+                rope(kv + h * hd, hd, pos, c->rope_theta);
+            }
+            memcpy(Kl + (size_t)pos * hkv, kv, 4 * hkv);
+            memcpy(Vl + (size_t)pos * hkv, vv, 4 * hkv);
+#pragma omp parallel for schedule(static)
+            for (int h = 0; h < (int)nh; ++h) {
+                const uint32_t kh = (uint32_t)h / G;
+                float *s = (float *)malloc(4 * (size_t)(pos + 1));
+                float mx = -3.4e38f;
+                for (uint32_t j = 0; j <= pos; ++j) {
+                    float acc = 0.0f;
+                    for (uint32_t e = 0; e < hd; ++e) acc += qv[h * hd + e] * Kl[(size_t)j * hkv + kh * hd + e];
+                    s[j] = acc * scale;
+                    if (s[j] > mx) mx = s[j];
+                }
+                float sum = 0.0f;
+                for (uint32_t j = 0; j <= pos; ++j) sum += (s[j] = expf(s[j] - mx));
+                const float inv = 1.0f / sum;
+                for (uint32_t e = 0; e < hd; ++e) {
+                    float acc = 0.0f;
+                    for (uint32_t j = 0; j <= pos; ++j) acc += s[j] * inv * Vl[(size_t)j * hkv + kh * hd + e];
+                    cx[h * hd + e] = acc;
+                }
+                free(s);
+            }
+            quant1(cx, hq, &sx, xq);
+            plin_run(&q[7 * l + 3], xq, &sx, threads, o);
+            for (uint32_t e = 0; e < d; ++e) x[e] += o[e];
+            rmsnorm(x, gain, d, c->rms_eps, xn);
+            quant1(xn, d, &sx, xq);
+            plin_run(&q[7 * l + 4], xq, &sx, threads, g);
+            plin_run(&q[7 * l + 5], xq, &sx, threads, u);
+            for (uint32_t e = 0; e < ff; ++e) g[e] = g[e] / (1.0f + expf(-g[e])) * u[e];
+            quant1(g, ff, &sx, xq);
+            plin_run(&q[7 * l + 6], xq, &sx, threads, o);
+            for (uint32_t e = 0; e < d; ++e) x[e] += o[e];
+        }
+        rmsnorm(x, gain, d, c->rms_eps, xn);
+        quant1(xn, d, &sx, xq);
+        plin_run(&head, xq, &sx, threads, lg);
+        cur = or_argmax_row(lg, V);
+    }
+    const double secs = omp_get_wtime() - t0;
+    for (uint32_t i = 0; i < 7 * L; ++i) {
+        free(q[i].w);
+        free(q[i].s);
+    }
+    free(q);
+    free(head.w); free(head.s);
+    free(K); free(Vc); free(gain); free(x); free(xn); free(qv); free(kv); free(vv); free(cx);
+    free(o); free(g); free(u); free(lg); free(tmp); free(xq);
+    return secs;
+}

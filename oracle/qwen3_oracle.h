@@ -18,4 +18,8 @@ uint64_t or_qwen3_param_count(const or_qwen3_config *c);
  * (either may be NULL). int8: 1 = int8 linears, 0 = f32 linears. */
 int or_qwen3_generate(const or_qwen3_config *c, const float *params, int int8, const uint32_t *prompts,
                       uint32_t batch, uint32_t len, uint32_t steps, uint32_t *out_tokens, float *out_logits);
+/* CPU baseline (bench only): seconds for `steps` int8 decode steps at batch 1
+ * after `ctx` cached positions, backend-cpu's restated int8 GEMV on `threads`
+ * OpenMP threads, random int8 weights at the config's shapes. */
+double or_qwen3_cpu_decode(const or_qwen3_config *c, uint64_t seed, int threads, uint32_t ctx, uint32_t steps);
 #endif
