@@ -42,9 +42,10 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on CPU-baseline work")
-    ap.add_argument("--only", default="", help="profiling aid: 'decode', 'prefill', 'qwen3', 'dit' or 'copy' only")
+    ap.add_argument("--only", default="", help="profiling aid: 'decode', 'prefill', 'qwen3', 'dit', 'w4a8' or 'copy' only")
     ap.add_argument("--no-qwen3", action="store_true")
     ap.add_argument("--no-dit", action="store_true")
+    ap.add_argument("--no-w4a8", action="store_true")
     return ap.parse_args()
 
 
@@ -246,6 +247,51 @@ def mfma_roof(torch, lib, dev):
     return round(ops / (a.elapsed_time(b) * 1e-3) / 1e12, 1)
 
 
+def bench_w4a8(reps=20):
+    """W4A8 (matmul_q4_gemv / matmul_q4_dyn): the configs[1] decode shapes and
+    two prefill shapes with int4 weights, one HIP graph of `reps` launches
+    per shape (weights re-read from the Infinity Cache, so these are warm
+    numbers). Decode: GB/s over N*K/2 + 4N + M*K + 2*M*N; prefill: TOPS."""
+    import torch
+    from brain_amd import ops
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    out = {"decode": [], "prefill": []}
+
+    def timed(fn):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(reps):
+                fn()
+        gr.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        gr.replay()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / reps
+
+    for m, (k, n) in [(m, kn) for kn in DECODE_KN for m in (1, 16)] + [(512, (4096, 11008)), (2048, (4096, 4096))]:
+        xq = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=dev, generator=g).view(torch.int32)
+        w4 = torch.randint(-2**31, 2**31 - 1, (n, k // 8), dtype=torch.int32, device=dev, generator=g)
+        sx = torch.rand(m, device=dev, generator=g)
+        sw = torch.rand(n, device=dev, generator=g) * 0.01
+        o = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+        dt = timed(lambda: ops.matmul_q4(xq, w4, sx, sw, None, torch.bfloat16, "auto", out=o))
+        if m <= 32:
+            b = n * k // 2 + 4 * n + m * k + 2 * m * n
+            out["decode"].append({"m": m, "k": k, "n": n, "us": round(dt * 1e6, 2), "gbs": round(b / dt / 1e9, 1)})
+        else:
+            out["prefill"].append({"m": m, "k": k, "n": n, "us": round(dt * 1e6, 2),
+                                   "tops": round(2 * m * n * k / dt / 1e12, 1)})
+    return out
+
+
 def qwen3_weight_bytes(c):
     """int8 weight + scale bytes one decode step streams (every linear + the head)."""
     d, ff, hq, hkv = c["d_model"], c["d_ff"], c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
@@ -402,6 +448,8 @@ def main():
         res["qwen3"] = bench_qwen3(cpu=not args.no_cpu)
     if args.only in ("", "dit") and not args.no_dit:
         res["dit"] = bench_dit()
+    if args.only in ("", "w4a8") and not args.no_w4a8:
+        res["w4a8"] = bench_w4a8()
     if args.only:
         print(json.dumps(res))
         return
@@ -451,6 +499,8 @@ def main():
         line["qwen3_e2e"] = res["qwen3"]
     if "dit" in res:
         line["dit_stack"] = res["dit"]
+    if "w4a8" in res:
+        line["w4a8"] = res["w4a8"]
     if cpu is not None:
         line["gpu_vs_cpu"] = round(value / cpu["value"], 1)
     print(json.dumps(line))

@@ -37,6 +37,10 @@ hipError_t launch_gemm_i8_static(hipStream_t s, const uint32_t* xq, const uint32
                                  float* out, int m, int kg, int n);
 
 size_t gemm_workspace_ints(int m, int kg, int n, size_t* counters);
+hipError_t launch_gemv_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
+                          const float* bias, void* out, int out_dtype, int m, int k, int n);
+hipError_t launch_gemm_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
+                          const float* sw, const float* bias, void* out, int out_dtype, int m, int k, int n);
 
 // Split-K workspace, one per (device, stream): i32 sums plus per-tile arrival
 // counters. Zeroed once when (re)allocated; every kernel that uses it leaves
@@ -343,6 +347,37 @@ int bh_quantize_weight_device(void* stream, const float* w, uint32_t n, uint32_t
                       "quantize_weight launch");
 }
 
+static int check_q4(const void* xq, const void* wq, const void* sx, const void* sw, const void* out, int out_dtype,
+                    uint32_t m, uint32_t k, uint32_t n, const char* who) {
+    if (k % 8) return fail(BH_ERR_INVALID, "%s: k=%u is not a multiple of 8", who, k);
+    return check_matmul(xq, wq, sx, sw, out, out_dtype, m, k / 4, n, who);
+}
+
+int bh_matmul_q4_gemv(void* stream, const uint32_t* xq, const uint32_t* wq4, const float* sx, const float* sw,
+                      const float* bias, void* out, int out_dtype, uint32_t m, uint32_t k, uint32_t n) {
+    int rc = check_q4(xq, wq4, sx, sw, out, out_dtype, m, k, n, "bh_matmul_q4_gemv");
+    if (rc) return rc;
+    if (m > (uint32_t)GEMV_MAX_ROWS) return fail(BH_ERR_INVALID, "bh_matmul_q4_gemv: m=%u > %d", m, GEMV_MAX_ROWS);
+    if (m == 0 || n == 0) return BH_OK;
+    return hip_status(launch_gemv_q4((hipStream_t)stream, xq, wq4, sx, sw, bias, out, out_dtype, (int)m, (int)k, (int)n),
+                      "gemv_q4 launch");
+}
+
+int bh_matmul_q4_dyn(void* stream, const uint32_t* xq, const uint32_t* wq4, const float* sx, const float* sw,
+                     const float* bias, void* out, int out_dtype, uint32_t m, uint32_t k, uint32_t n) {
+    int rc = check_q4(xq, wq4, sx, sw, out, out_dtype, m, k, n, "bh_matmul_q4_dyn");
+    if (rc) return rc;
+    if (m == 0 || n == 0) return BH_OK;
+    return hip_status(launch_gemm_q4((hipStream_t)stream, xq, wq4, sx, sw, bias, out, out_dtype, (int)m, (int)k, (int)n),
+                      "gemm_q4 launch");
+}
+
+int bh_matmul_q4(void* stream, const uint32_t* xq, const uint32_t* wq4, const float* sx, const float* sw,
+                 const float* bias, void* out, int out_dtype, uint32_t m, uint32_t k, uint32_t n) {
+    if (m <= (uint32_t)GEMV_MAX_ROWS) return bh_matmul_q4_gemv(stream, xq, wq4, sx, sw, bias, out, out_dtype, m, k, n);
+    return bh_matmul_q4_dyn(stream, xq, wq4, sx, sw, bias, out, out_dtype, m, k, n);
+}
+
 int bh_f32_to_bf16(void* stream, const float* x, uint16_t* out, uint64_t n) {
     if (n == 0) return BH_OK;
     if (!x || !out) return fail(BH_ERR_INVALID, "bh_f32_to_bf16: null buffer");
@@ -530,6 +565,35 @@ int bh_quantize_weight(const float* w, uint64_t n, uint64_t k, uint32_t* packed,
     return BH_OK;
 }
 
+// crates/model/src/int4.rs:46-67: sw = max(max|w|, 1e-8)/7, q = clamp(round_half_away(w*(1/sw)), +-7),
+// nibble b of word g = column 8g+b, two's complement.
+int bh_quantize_weight_q4(const float* w, uint64_t n, uint64_t k, uint32_t* packed, float* sw) {
+    if (k % 8) return fail(BH_ERR_INVALID, "bh_quantize_weight_q4: k=%llu is not a multiple of 8", (unsigned long long)k);
+    if (n && k && (!w || !packed || !sw)) return fail(BH_ERR_INVALID, "bh_quantize_weight_q4: null buffer");
+    const uint64_t kg = k / 8;
+    parallel_rows(n, [&](uint64_t r0, uint64_t r1) {
+        for (uint64_t r = r0; r < r1; ++r) {
+            const float* row = w + r * k;
+            float mx = 0.0f;
+            for (uint64_t c = 0; c < k; ++c) mx = std::max(mx, std::fabs(row[c]));
+            const float s = std::max(mx, 1e-8f) / 7.0f;
+            sw[r] = s;
+            const float inv = 1.0f / s;
+            for (uint64_t g = 0; g < kg; ++g) {
+                uint32_t word = 0;
+                for (int b = 0; b < 8; ++b) {
+                    float q = std::round(row[g * 8 + b] * inv);
+                    q = std::min(std::max(q, -7.0f), 7.0f);
+                    const int qi = std::isnan(q) ? 0 : (int)q;
+                    word |= ((uint32_t)(uint8_t)qi & 0xFu) << (4 * b);
+                }
+                packed[r * kg + g] = word;
+            }
+        }
+    });
+    return BH_OK;
+}
+
 int bh_dequantize_weight(const uint32_t* packed, const float* sw, uint64_t n, uint64_t k, float* w) {
     if (k % 4 != 0) return fail(BH_ERR_INVALID, "bh_dequantize_weight: k=%llu is not a multiple of 4", (unsigned long long)k);
     if (n == 0 || k == 0) return BH_OK;
@@ -573,6 +637,8 @@ enum KernelId : int {
     K_MATMUL_I8,
     K_BIAS_ADD,
     K_ROOF_DP4A,
+    K_MATMUL_Q4_DYN,
+    K_MATMUL_Q4_GEMV,
 };
 
 struct KernelSpec {
@@ -587,6 +653,7 @@ static const KernelSpec kSpecs[] = {
     {"quant_pack", K_QUANT_PACK, 3, 2},        {"matmul_i8_dyn", K_MATMUL_I8_DYN, 5, 3},
     {"matmul_i8_gemv", K_MATMUL_I8_GEMV, 5, 3}, {"matmul_i8", K_MATMUL_I8, 3, 5},
     {"bias_add", K_BIAS_ADD, 2, 2},            {"roof_dp4a", K_ROOF_DP4A, 2, 4},
+    {"matmul_q4_dyn", K_MATMUL_Q4_DYN, 5, 3},   {"matmul_q4_gemv", K_MATMUL_Q4_GEMV, 5, 3},
 };
 
 static const KernelSpec* spec_of(const char* name) {
@@ -674,6 +741,14 @@ static int binding_needs(KernelId id, const std::vector<uint32_t>& p, std::vecto
             [[fallthrough]];
         case K_MATMUL_I8_DYN: need = {a * b, c * b, a, c, a * c}; return BH_OK;
         case K_MATMUL_I8: need = {a * b, c * b, a * c}; return BH_OK;
+        case K_MATMUL_Q4_GEMV:
+            if (a > (uint64_t)GEMV_MAX_ROWS)
+                return fail(BH_ERR_INVALID, "%s: m=%llu > %d", name, (unsigned long long)a, GEMV_MAX_ROWS);
+            [[fallthrough]];
+        case K_MATMUL_Q4_DYN:  // params [m, k, n] with the RAW k (crates/model/src/dispatch.rs:132-178)
+            if (b % 8) return fail(BH_ERR_INVALID, "%s: k=%llu is not a multiple of 8", name, (unsigned long long)b);
+            need = {a * b / 4, c * b / 8, a, c, a * c};
+            return BH_OK;
         case K_BIAS_ADD: need = {a * b, b}; return BH_OK;
         case K_ROOF_DP4A: need = {a, a}; return BH_OK;
         default: return fail(BH_ERR_UNSUPPORTED, "kernel '%s' is not provided by the hip backend", name);
@@ -687,7 +762,9 @@ static bool is_output(KernelId id, uint32_t i) {
         case K_MAX_ABS_ROWS: return i == 1;
         case K_QUANT_PACK: return i == 2;
         case K_MATMUL_I8_DYN:
-        case K_MATMUL_I8_GEMV: return i == 4;
+        case K_MATMUL_I8_GEMV:
+        case K_MATMUL_Q4_DYN:
+        case K_MATMUL_Q4_GEMV: return i == 4;
         case K_MATMUL_I8: return i == 2;
         case K_BIAS_ADD: return i == 0;
         case K_ROOF_DP4A: return i == 1;
@@ -771,6 +848,14 @@ static int launch_step(bh_backend* be, const bh_dispatch* s) {
                                     p[0], p[1], p[2]);
         case K_MATMUL_I8_GEMV:
             return bh_matmul_i8_gemv(st, (const uint32_t*)wptr(s, 0), (const uint32_t*)wptr(s, 1),
+                                     (const float*)wptr(s, 2), (const float*)wptr(s, 3), nullptr, wptr(s, 4), OUT_F32,
+                                     p[0], p[1], p[2]);
+        case K_MATMUL_Q4_DYN:
+            return bh_matmul_q4_dyn(st, (const uint32_t*)wptr(s, 0), (const uint32_t*)wptr(s, 1),
+                                    (const float*)wptr(s, 2), (const float*)wptr(s, 3), nullptr, wptr(s, 4), OUT_F32,
+                                    p[0], p[1], p[2]);
+        case K_MATMUL_Q4_GEMV:
+            return bh_matmul_q4_gemv(st, (const uint32_t*)wptr(s, 0), (const uint32_t*)wptr(s, 1),
                                      (const float*)wptr(s, 2), (const float*)wptr(s, 3), nullptr, wptr(s, 4), OUT_F32,
                                      p[0], p[1], p[2]);
         case K_MATMUL_I8: {

@@ -42,6 +42,30 @@ __device__ __forceinline__ uint32_t quant_word(float4 v, float inv) {
            (quant_byte(v.w, inv) << 24);
 }
 
+// W4A8: one u32 of 8 int4 nibbles (nibble b = K index 8g+b, two's complement,
+// crates/model/src/int4.rs:46-67) -> 8 sign-extended int8 in K order, bytes
+// 0..3 in lo and 4..7 in hi. The even and odd nibbles are masked into bytes;
+// bit 3 is copied to bits 4..7 (x * 0x1E, no carry between bytes); then
+// v_perm_b32 interleaves the two halves back into K order.
+__device__ __forceinline__ void unpack_q4(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    uint32_t t0 = w & 0x0F0F0F0Fu;         // nibbles 0,2,4,6
+    uint32_t t1 = (w >> 4) & 0x0F0F0F0Fu;  // nibbles 1,3,5,7
+    t0 |= (t0 & 0x08080808u) * 0x1Eu;
+    t1 |= (t1 & 0x08080808u) * 0x1Eu;
+    lo = __builtin_amdgcn_perm(t1, t0, 0x05010400u);  // t0.b0 t1.b0 t0.b1 t1.b1
+    hi = __builtin_amdgcn_perm(t1, t0, 0x07030602u);  // t0.b2 t1.b2 t0.b3 t1.b3
+}
+// 16 bytes of int4 (32 K values) -> two 16-byte int8 fragments (K 0..15, 16..31).
+__device__ __forceinline__ void unpack_q4x4(v4i w, v4i& a, v4i& b) {
+    uint32_t l0, h0, l1, h1, l2, h2, l3, h3;
+    unpack_q4((uint32_t)w[0], l0, h0);
+    unpack_q4((uint32_t)w[1], l1, h1);
+    unpack_q4((uint32_t)w[2], l2, h2);
+    unpack_q4((uint32_t)w[3], l3, h3);
+    a = v4i{(int)l0, (int)h0, (int)l1, (int)h1};
+    b = v4i{(int)l2, (int)h2, (int)l3, (int)h3};
+}
+
 // The dequant epilogue of matmul_i8_dyn / matmul_i8_gemv: (f32(acc)*sx)*sw,
 // evaluated left to right with no fused multiply-add (the library is built
 // with -ffp-contract=off), then the optional bias add.

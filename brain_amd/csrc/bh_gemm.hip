@@ -93,7 +93,11 @@ __device__ __forceinline__ void emit(const GemmArgs& a, int row, int col, int ac
     }
 }
 
-template <int BM, int BN, int WM, int WN, int OUT, bool HAS_BIAS, bool ALIGNED, bool STATIC, bool SPLITK>
+// Q4: the weight operand is int4 (W4A8, [N, K/8] u32, crates/model/src/int4.rs:46-67).
+// Each thread loads half as many 16-byte pieces of B and unpacks every piece
+// into the two int8 chunks the int8 layout holds at that K, so the LDS image,
+// the MFMA loop and the epilogue are the int8 kernel's.
+template <int BM, int BN, int WM, int WN, int OUT, bool HAS_BIAS, bool ALIGNED, bool STATIC, bool SPLITK, bool Q4 = false>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_kernel(GemmArgs a) {
     using C = GemmCfg<BM, BN, WM, WN>;
     __shared__ __attribute__((aligned(16))) uint8_t lds[2 * C::STAGE];
@@ -130,16 +134,21 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_kernel(GemmArgs a) {
         a_cb[i] = cb * 16;
         a_lds[i] = swz(r, cb);
     }
-    const uint8_t* bg[C::B_CHUNKS];
-    int b_lds[C::B_CHUNKS], b_cb[C::B_CHUNKS];
+    // int8 B: chunk q -> (row q/8, chunk q%8). int4 B: piece q -> (row q/4,
+    // piece q%4) of the row's 64 int4 bytes per stage, landing in int8 chunks
+    // 2*(q%4) and 2*(q%4)+1.
+    constexpr int BL = Q4 ? C::B_CHUNKS / 2 : C::B_CHUNKS;  // global loads of B per thread
+    const int bbytes = Q4 ? kbytes / 2 : kbytes;
+    const uint8_t* bg[BL];
+    int b_lds[BL], b_cb[BL];
 #pragma unroll
-    for (int i = 0; i < C::B_CHUNKS; ++i) {
+    for (int i = 0; i < BL; ++i) {
         const int q = t + C::NT * i;
-        const int r = q >> 3, cb = q & 7;
+        const int r = Q4 ? q >> 2 : q >> 3, cb = Q4 ? q & 3 : q & 7;
         const int gr = min(col0 + r, n - 1);
-        bg[i] = reinterpret_cast<const uint8_t*>(a.wq) + (int64_t)gr * kbytes;
+        bg[i] = reinterpret_cast<const uint8_t*>(a.wq) + (int64_t)gr * bbytes;
         b_cb[i] = cb * 16;
-        b_lds[i] = C::LDS_A + swz(r, cb);
+        b_lds[i] = C::LDS_A + swz(r, Q4 ? 2 * cb : cb);
     }
 
     v16i acc[C::FM][C::FN];
@@ -150,20 +159,33 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_kernel(GemmArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
 
-    v4i ra[C::A_CHUNKS], rb[C::B_CHUNKS];
+    v4i ra[C::A_CHUNKS], rb[BL];
     auto gload = [&](int kt) {
         const int k0 = kt * GM_BK;
 #pragma unroll
         for (int i = 0; i < C::A_CHUNKS; ++i) ra[i] = load_k16<ALIGNED>(ag[i], k0 + a_cb[i], kbytes);
 #pragma unroll
-        for (int i = 0; i < C::B_CHUNKS; ++i) rb[i] = load_k16<ALIGNED>(bg[i], k0 + b_cb[i], kbytes);
+        for (int i = 0; i < BL; ++i) rb[i] = load_k16<ALIGNED>(bg[i], (Q4 ? k0 / 2 : k0) + b_cb[i], bbytes);
     };
     auto sstore = [&](int buf) {
         uint8_t* base = lds + buf * C::STAGE;
 #pragma unroll
         for (int i = 0; i < C::A_CHUNKS; ++i) *reinterpret_cast<v4i*>(base + a_lds[i]) = ra[i];
 #pragma unroll
-        for (int i = 0; i < C::B_CHUNKS; ++i) *reinterpret_cast<v4i*>(base + b_lds[i]) = rb[i];
+        for (int i = 0; i < BL; ++i) {
+            if constexpr (Q4) {
+                // chunk 2c and 2c+1 of a row are adjacent before the swizzle
+                // (c ^ s and (c ^ s) ^ 1 for even c): recompute the second slot.
+                const int q = t + C::NT * i;
+                const int r = q >> 2, cb = q & 3;
+                v4i lo, hi;
+                unpack_q4x4(rb[i], lo, hi);
+                *reinterpret_cast<v4i*>(base + b_lds[i]) = lo;
+                *reinterpret_cast<v4i*>(base + C::LDS_A + swz(r, 2 * cb + 1)) = hi;
+            } else {
+                *reinterpret_cast<v4i*>(base + b_lds[i]) = rb[i];
+            }
+        }
     };
 
     if (nk > 0) {
@@ -700,15 +722,15 @@ static TileChoice choose_tiles(int m, int kg, int n) {
     return {c256 <= c128 ? 0 : 1, 1};
 }
 
-template <int BM, int BN, int WM, int WN, int OUT, bool HAS_BIAS, bool STATIC, bool SPLITK>
+template <int BM, int BN, int WM, int WN, int OUT, bool HAS_BIAS, bool STATIC, bool SPLITK, bool Q4 = false>
 static hipError_t go(hipStream_t s, bool aligned, const GemmArgs& a) {
     const long tiles = (long)((a.m + BM - 1) / BM) * ((a.n + BN - 1) / BN);
     const unsigned grid = (unsigned)(tiles * (SPLITK ? a.splits : 1));
     constexpr int NT = WM * WN * 64;
     if (aligned)
-        gemm_i8_kernel<BM, BN, WM, WN, OUT, HAS_BIAS, true, STATIC, SPLITK><<<grid, NT, 0, s>>>(a);
+        gemm_i8_kernel<BM, BN, WM, WN, OUT, HAS_BIAS, true, STATIC, SPLITK, Q4><<<grid, NT, 0, s>>>(a);
     else
-        gemm_i8_kernel<BM, BN, WM, WN, OUT, HAS_BIAS, false, STATIC, SPLITK><<<grid, NT, 0, s>>>(a);
+        gemm_i8_kernel<BM, BN, WM, WN, OUT, HAS_BIAS, false, STATIC, SPLITK, Q4><<<grid, NT, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -802,6 +824,28 @@ hipError_t launch_gemm_i8_static(hipStream_t s, const uint32_t* xq, const uint32
     tc.splits = 1;  // the static variant stays on plain tiles
     const bool al = gemm_aligned(xq, wq, kg);
     return go_cfg<OUT_F32, false, true>(s, al, al && ((kg * 4) % 128 == 0), tc, a);
+}
+
+// W4A8 prefill GEMM (matmul_q4_dyn, crates/kernels/wgsl/matmul_q4_dyn.wgsl):
+// the register-staged kernel with int4 B unpacked on the way into LDS. k is
+// the raw K (k % 8 == 0); the activation keeps its int8 [M, K/4] layout.
+template <int OUT, bool HAS_BIAS>
+static hipError_t go_q4(hipStream_t s, bool aligned, const GemmArgs& a) {
+    TileChoice tc = choose_tiles(a.m, a.kg, a.n);
+    if (tc.cfg == 0) return go<256, 256, 2, 2, OUT, HAS_BIAS, false, false, true>(s, aligned, a);
+    return go<128, 128, 2, 2, OUT, HAS_BIAS, false, false, true>(s, aligned, a);
+}
+
+hipError_t launch_gemm_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
+                          const float* sw, const float* bias, void* out, int out_dtype, int m, int k, int n) {
+    GemmArgs a{xq, wq, sx, sw, bias, out, m, k / 4, n, 0.f, 0.f, 1, nullptr, nullptr};
+    // Aligned 16-byte loads need 16-byte rows in both operands: K % 32 == 0.
+    const bool al = (k % 32) == 0 && ((reinterpret_cast<uintptr_t>(xq) | reinterpret_cast<uintptr_t>(wq)) & 15u) == 0;
+    switch (out_dtype) {
+        case OUT_I32: return go_q4<OUT_I32, false>(s, al, a);
+        case OUT_F32: return bias ? go_q4<OUT_F32, true>(s, al, a) : go_q4<OUT_F32, false>(s, al, a);
+        default: return bias ? go_q4<OUT_BF16, true>(s, al, a) : go_q4<OUT_BF16, false>(s, al, a);
+    }
 }
 
 }  // namespace bh

@@ -41,11 +41,11 @@ struct GemvArgs {
     int m, kg, n;
 };
 
-template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int KSPLIT, bool XLDS, int U, int CG>
-__global__ __launch_bounds__(GV_THREADS) void gemv_i8_kernel(GemvArgs a) {
-    constexpr int SLOTS = GV_WAVES / KSPLIT;  // wave slots per workgroup, each CG column groups
+template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int KSPLIT, bool XLDS, int U, int CG, int NW = GV_WAVES>
+__global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
+    constexpr int SLOTS = NW / KSPLIT;  // wave slots per workgroup, each CG column groups
     extern __shared__ __attribute__((aligned(16))) uint8_t xs[];  // [MT*16][kbytes+16] when XLDS
-    __shared__ int red[KSPLIT > 1 ? GV_WAVES : 1][CG * MT * 4][64];
+    __shared__ int red[KSPLIT > 1 ? NW : 1][CG * MT * 4][64];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -79,7 +79,7 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_i8_kernel(GemvArgs a) {
     if constexpr (XLDS) {
         const int pieces = kbytes >> 4;
         const int total = MT * 16 * pieces;
-        for (int p = threadIdx.x; p < total; p += GV_THREADS) {
+        for (int p = threadIdx.x; p < total; p += NW * 64) {
             const int r = p / pieces, c = p - r * pieces;
             v4i v = {0, 0, 0, 0};
             if (r < m) v = *reinterpret_cast<const v4i*>(reinterpret_cast<const uint8_t*>(a.xq) + (int64_t)r * kbytes + c * 16);
@@ -179,13 +179,13 @@ static int gv_cfg() {
     return v;
 }
 
-template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int U, int CG>
+template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int U, int CG, int KSPLIT = 4>
 static hipError_t gv_go(hipStream_t s, const GemvArgs& a) {
-    constexpr int KSPLIT = 4;
-    constexpr int per_wg = (GV_WAVES / KSPLIT) * CG;
+    constexpr int NW = KSPLIT > GV_WAVES ? KSPLIT : GV_WAVES;  // waves per workgroup
+    constexpr int per_wg = (NW / KSPLIT) * CG;
     const int ngroups = (a.n + 15) / 16;
     const int grid = (ngroups + per_wg - 1) / per_wg;
-    gemv_i8_kernel<MT, OUT, HAS_BIAS, ALIGNED, KSPLIT, false, U, CG><<<grid, GV_THREADS, 0, s>>>(a);
+    gemv_i8_kernel<MT, OUT, HAS_BIAS, ALIGNED, KSPLIT, false, U, CG, NW><<<grid, NW * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -205,9 +205,15 @@ static hipError_t gv_split(hipStream_t s, const GemvArgs& a) {
         case 1: return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 1>(s, a);
         case 2: return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 2>(s, a);
         case 3: return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 16, 1>(s, a);
+        case 4: return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 1, 4>(s, a);
         default: break;
     }
     if (ngroups >= 1024) return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 2>(s, a);
+    // Narrow N: split K 8 or 16 ways inside one workgroup (512 / 1024 threads)
+    // so the grid holds ~1000+ waves instead of N/16 x 4.
+    const int nchunks = (a.kg * 4 + 63) / 64;
+    if (nchunks >= 32) return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 1, 16>(s, a);
+    if (nchunks >= 16) return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 1, 8>(s, a);
     if (wave_chunks > 4) return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 16, 1>(s, a);
     return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 1>(s, a);
 }

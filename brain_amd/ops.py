@@ -149,3 +149,25 @@ def reserve_workspace(m, k, n, stream=None):
     [m,k] x [n,k] GEMM; required before capturing such a GEMM in a graph."""
     sp = (stream or torch.cuda.current_stream()).cuda_stream
     check(load().bh_reserve_workspace(sp, m, k // 4, n))
+
+
+_Q4_VARIANTS = {"auto": "bh_matmul_q4", "gemv": "bh_matmul_q4_gemv", "dyn": "bh_matmul_q4_dyn"}
+
+
+def matmul_q4(xq, wq4, sx, sw, bias=None, out_dtype=torch.float32, variant="auto", out=None):
+    """W4A8: xq [m, k/4] int8 activation words, wq4 [n, k/8] int4 weight words
+    (crates/model/src/int4.rs), (f32(acc)*sx)*sw (+bias) -> out [m, n]."""
+    m, kg = xq.shape
+    n, kw = wq4.shape
+    k = kg * 4
+    if kw * 8 != k:
+        raise ValueError(f"matmul_q4: xq has K={k}, wq4 has K={kw * 8}")
+    _dev(xq, wq4, sx, sw, bias, out)
+    _need(xq, torch.int32, m * kg, "xq")
+    _need(wq4, torch.int32, n * kw, "wq4")
+    code = _CODES[out_dtype]
+    out = torch.empty(m, n, device=xq.device, dtype=out_dtype) if out is None else out
+    _need(out, out_dtype, m * n, "out")
+    check(getattr(load(), _Q4_VARIANTS[variant])(
+        _stream(), _ptr(xq), _ptr(wq4), _ptr(sx), _ptr(sw), _ptr(bias), _ptr(out), code, m, k, n))
+    return out

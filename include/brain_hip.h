@@ -127,6 +127,19 @@ int bh_linear_i8(void* stream, const float* x, const uint32_t* wq, const float* 
  * packed [n,k/4] u32, sw [n] f32. */
 int bh_quantize_weight_device(void* stream, const float* w, uint32_t n, uint32_t k, uint32_t* packed, float* sw);
 
+/* W4A8 (crates/model/src/int4.rs, crates/kernels/wgsl/matmul_q4_{gemv,dyn}.wgsl):
+ * int4 weights wq4 [n, k/8] u32 (8 nibbles per word, nibble b = K index 8g+b,
+ * two's complement, per-row scale), the int8 activation xq [m, k/4] of the
+ * int8 tier, the same (f32(acc)*sx)*sw epilogue. k is the RAW K, a multiple
+ * of 8 (the q4 family's param contract, crates/model/src/dispatch.rs:132-178).
+ * Step names "matmul_q4_gemv" / "matmul_q4_dyn" take params [m, k, n]. */
+int bh_matmul_q4_gemv(void* stream, const uint32_t* xq, const uint32_t* wq4, const float* sx, const float* sw,
+                      const float* bias, void* out, int out_dtype, uint32_t m, uint32_t k, uint32_t n);
+int bh_matmul_q4_dyn(void* stream, const uint32_t* xq, const uint32_t* wq4, const float* sx, const float* sw,
+                     const float* bias, void* out, int out_dtype, uint32_t m, uint32_t k, uint32_t n);
+int bh_matmul_q4(void* stream, const uint32_t* xq, const uint32_t* wq4, const float* sx, const float* sw,
+                 const float* bias, void* out, int out_dtype, uint32_t m, uint32_t k, uint32_t n);
+
 /* f32 -> bf16 bits, round to nearest even, NaN -> (bits >> 16) | 0x0040: the
  * conversion every bf16 output of this library goes through
  * (crates/model/src/half.rs:49-58, f32_to_bf16). x [n] f32 -> out [n] u16. */
@@ -251,6 +264,10 @@ int bh_stats(const bh_backend* be, bh_stats_t* st);
 
 /* crates/model/src/int8.rs:33-59 — row-parallel host quantizer (ties AWAY). */
 int bh_quantize_weight(const float* w, uint64_t n, uint64_t k, uint32_t* packed, float* sw);
+/* `model::int4::quantize_weight_q4` (crates/model/src/int4.rs:46-67): per-row
+ * sw = max(max|w|,1e-8)/7, q = clamp(round_half_away(w*(1/sw)), +-7) packed
+ * 8 per u32. k % 8 == 0. Host, row-parallel. */
+int bh_quantize_weight_q4(const float* w, uint64_t n, uint64_t k, uint32_t* packed, float* sw);
 /* crates/model/src/int8.rs:70-87 */
 int bh_dequantize_weight(const uint32_t* packed, const float* sw, uint64_t n, uint64_t k, float* w);
 

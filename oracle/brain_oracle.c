@@ -218,3 +218,50 @@ void or_cpu_linear_gemv(const float* x, const uint32_t* wq, const float* sw,
     }
     or_cpu_gemv_packed(xq, wq, sx, sw, m, kg, n, threads, out);
 }
+
+/* ---- W4A8 (crates/model/src/int4.rs:46-67, crates/kernels/wgsl/matmul_q4_gemv.wgsl) ---- */
+
+/* quantize_weight_q4: sw = max(max|w|,1e-8)/7; q = clamp(round_half_away(w*(1/sw)), -7, 7)
+ * (Rust f32::round, `as i32` maps NaN to 0); nibble b of word g holds column 8g+b. */
+void or_quantize_weight_q4(const float* w, int64_t n, int64_t k, uint32_t* packed, float* sw) {
+    const int64_t kg = k / 8;
+    for (int64_t r = 0; r < n; ++r) {
+        float m = 0.0f;
+        for (int64_t c = 0; c < k; ++c) m = mx(m, fabsf(w[r * k + c]));
+        const float s = mx(m, 1e-8f) / 7.0f;
+        sw[r] = s;
+        const float inv = 1.0f / s;
+        for (int64_t g = 0; g < kg; ++g) {
+            uint32_t word = 0;
+            for (int b = 0; b < 8; ++b) {
+                float q = roundf(w[r * k + g * 8 + b] * inv);
+                q = q < -7.0f ? -7.0f : (q > 7.0f ? 7.0f : q);
+                const int32_t qi = (q != q) ? 0 : (int32_t)q;
+                word |= ((uint32_t)(uint8_t)qi & 0xFu) << (4 * b);
+            }
+            packed[r * kg + g] = word;
+        }
+    }
+}
+
+/* The nibble of column c, sign-extended (int4.rs dequantize_weight_q4). */
+static int32_t q4_at(const uint32_t* row, int64_t c) {
+    const uint32_t raw = (row[c / 8] >> (4 * (c % 8))) & 0xFu;
+    return raw < 8 ? (int32_t)raw : (int32_t)raw - 16;
+}
+
+void or_dequantize_weight_q4(const uint32_t* packed, const float* sw, int64_t n, int64_t k, float* w) {
+    for (int64_t r = 0; r < n; ++r)
+        for (int64_t c = 0; c < k; ++c) w[r * k + c] = (float)q4_at(packed + r * (k / 8), c) * sw[r];
+}
+
+/* Exact i32 accumulators of the W4A8 product: xq [m, k/4] int8, w4 [n, k/8]. */
+void or_matmul_q4_acc(const uint32_t* xq, const uint32_t* w4, int64_t m, int64_t k, int64_t n, int32_t* acc) {
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            int64_t s = 0;
+            const int8_t* a = (const int8_t*)(xq + i * (k / 4));
+            for (int64_t c = 0; c < k; ++c) s += (int64_t)a[c] * q4_at(w4 + j * (k / 8), c);
+            acc[i * n + j] = (int32_t)s;
+        }
+}

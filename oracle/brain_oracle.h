@@ -79,6 +79,10 @@ void or_matmul_i8(const uint32_t* xq, const uint32_t* wq, const float* sx, const
 /* crates/model/src/half.rs:49-58 */
 uint16_t or_f32_to_bf16(float f);
 void or_f32_to_bf16_array(const float* x, uint16_t* out, size_t n);
+/* W4A8: int4 weight quantizer (int4.rs:46-67), its inverse, exact accumulators. */
+void or_quantize_weight_q4(const float* w, int64_t n, int64_t k, uint32_t* packed, float* sw);
+void or_dequantize_weight_q4(const uint32_t* packed, const float* sw, int64_t n, int64_t k, float* w);
+void or_matmul_q4_acc(const uint32_t* xq, const uint32_t* w4, int64_t m, int64_t k, int64_t n, int32_t* acc);
 
 /* CPU baseline: backend-cpu's execution of max_abs_row -> quant_pack ->
  * matmul_i8_gemv, restated (one workgroup per output column, 64 invocations

@@ -53,6 +53,9 @@ def lib():
             "or_cpu_linear_gemv": (None, [vp, vp, vp, i64, i64, i64, i32, vp, vp, vp]),
             "or_cpu_gemv_packed": (None, [vp, vp, vp, vp, i64, i64, i64, i32, vp]),
             "or_argmax_row": (u32, [vp, u32]),
+            "or_quantize_weight_q4": (None, [vp, i64, i64, vp, vp]),
+            "or_dequantize_weight_q4": (None, [vp, vp, i64, i64, vp]),
+            "or_matmul_q4_acc": (None, [vp, vp, i64, i64, i64, vp]),
             "or_qwen3_param_count": (u64, [vp]),
             "or_qwen3_generate": (i32, [vp, vp, i32, vp, u32, u32, u32, vp, vp]),
             "or_qwen3_cpu_decode": (C.c_double, [vp, u64, i32, u32, u32]),
@@ -340,3 +343,48 @@ def qwen3_cpu_decode_seconds(cfg, threads, ctx, steps, seed=1):
     """or_qwen3_cpu_decode: seconds for `steps` batch-1 int8 decode steps on the CPU."""
     c = _qcfg(cfg)
     return lib().or_qwen3_cpu_decode(C.byref(c), seed, threads, ctx, steps)
+
+
+# ---------------------------------------------------------------- W4A8
+def quantize_weight_q4(w):
+    """or_quantize_weight_q4 (crates/model/src/int4.rs:46-67) -> (packed u32 [n,k/8], sw f32 [n])."""
+    w = _c(w, np.float32)
+    n, k = w.shape
+    packed = np.zeros((n, k // 8), np.uint32)
+    sw = np.zeros(n, np.float32)
+    lib().or_quantize_weight_q4(_p(w), n, k, _p(packed), _p(sw))
+    return packed, sw
+
+
+def dequantize_weight_q4(packed, sw, k):
+    packed = _c(packed, np.uint32)
+    sw = _c(sw, np.float32)
+    out = np.zeros((packed.shape[0], k), np.float32)
+    lib().or_dequantize_weight_q4(_p(packed), _p(sw), packed.shape[0], k, _p(out))
+    return out
+
+
+def matmul_q4_acc(xq, w4, k):
+    """or_matmul_q4_acc: exact i32 [m, n] (scalar C; small shapes)."""
+    xq = _c(xq, np.uint32)
+    w4 = _c(w4, np.uint32)
+    m, n = xq.shape[0], w4.shape[0]
+    acc = np.zeros((m, n), np.int32)
+    lib().or_matmul_q4_acc(_p(xq), _p(w4), m, k, n, _p(acc))
+    return acc
+
+
+def unpack_q4(w4, k):
+    """Signed int4 values [n, k] of packed [n, k/8] (numpy, for float64-BLAS exact sums)."""
+    w4 = _c(w4, np.uint32)
+    shifts = (4 * np.arange(8, dtype=np.uint32))
+    nib = ((w4[:, :, None] >> shifts[None, None, :]) & 0xF).astype(np.int16)
+    nib = np.where(nib >= 8, nib - 16, nib)
+    return nib.reshape(w4.shape[0], -1)[:, :k].astype(np.int8)
+
+
+def acc_exact_q4(xq, w4, k, rows=None, cols=None):
+    """Exact i32 accumulators through float64 BLAS (|acc| < 127*7*k < 2**53)."""
+    a = unpack_i8(xq if rows is None else np.asarray(xq)[rows]).astype(np.float64)[:, :k]
+    b = unpack_q4(w4 if cols is None else np.asarray(w4)[cols], k).astype(np.float64)
+    return (a @ b.T).astype(np.int64).astype(np.int32)
