@@ -326,8 +326,8 @@ def bench_qwen3(prompt_len=128, gen=256, batches=(1, 8), cpu=True):
     out = {"model": "Qwen3-0.6B architecture (28 layers, d 1024, 16q/8kv heads, hd 128, ff 3072, vocab 151936, tied)",
            "weights": "random init (device, seeded), int8 per-channel", "prompt_len": prompt_len, "decode_steps": gen,
            "int8_weight_mb_per_step": round(wbytes / 1e6, 1)}
-    for b in batches:
-        e = Qwen3Engine(c, b, prompt_len + gen + 8, max_rows=b * prompt_len)
+    for b, kv8 in [(b, 0) for b in batches] + [(max(batches), 1)]:
+        e = Qwen3Engine(dict(c, kv_int8=kv8), b, prompt_len + gen + 8, max_rows=b * prompt_len)
         e.init_random(7)
         prompts = np.random.default_rng(b).integers(0, c["vocab"], size=(b, prompt_len))
         e.prefill(prompts)
@@ -340,8 +340,8 @@ def bench_qwen3(prompt_len=128, gen=256, batches=(1, 8), cpu=True):
         assert toks.shape == (gen, b)
         step_s = (t2 - t1) / gen
         avg_ctx = prompt_len + (gen + 1) / 2.0
-        kv_bytes = 2 * c["n_layers"] * b * avg_ctx * c["n_kv_heads"] * c["head_dim"] * 4
-        out[f"batch{b}"] = {"decode_tok_s": round(b * gen / (t2 - t1), 1), "ms_per_step": round(step_s * 1e3, 4),
+        kv_bytes = 2 * c["n_layers"] * b * avg_ctx * c["n_kv_heads"] * c["head_dim"] * (1 if kv8 else 4)
+        out[f"batch{b}" + ("_kv_int8" if kv8 else "")] = {"decode_tok_s": round(b * gen / (t2 - t1), 1), "ms_per_step": round(step_s * 1e3, 4),
                             "prefill_ms": round((t1 - t0) * 1e3, 2),
                             "prefill_tok_s": round(b * prompt_len / (t1 - t0), 1),
                             "step_hbm_gbs": round((wbytes + kv_bytes) / step_s / 1e9, 1)}

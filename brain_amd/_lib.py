@@ -46,7 +46,8 @@ class StatsT(C.Structure):
 
 class Qwen3ConfigT(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in ("vocab", "n_layers", "d_model", "n_heads", "n_kv_heads", "head_dim", "d_ff")] + \
-               [("rope_theta", C.c_float), ("rms_eps", C.c_float), ("tie_embeddings", C.c_uint32), ("qk_norm", C.c_uint32)]
+               [("rope_theta", C.c_float), ("rms_eps", C.c_float), ("tie_embeddings", C.c_uint32), ("qk_norm", C.c_uint32),
+                ("kv_int8", C.c_uint32)]
 
 
 class CostT(C.Structure):
@@ -83,6 +84,7 @@ SIGNATURES = {
     "bh_qwen3_lengths": (i32, [vp, vp, u32]),
     "bh_qwen3_stream": (vp, [vp]),
     "bh_qwen3_load": (i32, [vp, C.c_char_p]),
+    "bh_qwen3_set_kv_clip": (i32, [vp, u32, u32, vp]),
     "bh_qwen3_autotune": (i32, [vp, u32]),
     "bh_tune_i8": (i32, [vp, u32, u32, u32, u32, vp, vp]),
     "bh_tune_set": (i32, [u32, u32, u32, i32]),

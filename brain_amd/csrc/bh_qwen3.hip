@@ -203,8 +203,12 @@ __global__ __launch_bounds__(RT) void swiglu_quant_kernel(const float* gu, int f
 struct RopeArgs {
     const float* qkv;  // [rows, hq + 2 hkv]
     float* q;          // [rows, hq]
-    float* kc;         // this layer's K cache [max_batch, max_seq, hkv]
-    float* vc;
+    void* kc;          // this layer's K cache [max_batch, max_seq, hkv] (f32, or int8 with KV8)
+    void* vc;
+    float* ks;         // KV8: per (token slot, kv head) scales [max_batch, max_seq, nkv]
+    float* vs;
+    const float* kclip;  // KV8: per kv head ceilings (FLT_MAX: no clipping)
+    const float* vclip;
     const float* qn;   // q_norm / k_norm gains [hd]
     const float* kn;
     const uint32_t* pos;
@@ -213,74 +217,103 @@ struct RopeArgs {
     float eps, theta;
 };
 
+// One int8 KV code: clamp(round_even(v / scale), -127, 127)
+// (paged_kv_append_i8_clipped_batched.wgsl).
+__device__ __forceinline__ uint8_t kv8_code(float v, float scale) {
+    const float q = fminf(fmaxf(rintf(v / scale), -127.0f), 127.0f);
+    return (uint8_t)(int8_t)(int)q;
+}
+
 // One wave per (row, head): heads [0,nh) are queries, [nh, nh+nkv) keys,
 // [nh+nkv, nh+2nkv) values. Queries and keys get the per-head RMSNorm and the
 // rotate-half RoPE of rope_paged.wgsl:27-38 (pair (m, m+hd/2), angle
 // pos * theta^(-2m/hd)); keys and values land in the cache at (seq, pos)
-// (paged_kv_append_batched.wgsl with a contiguous slab per sequence).
+// (paged_kv_append_batched.wgsl with a contiguous slab per sequence). KV8
+// stores them as int8 with one scale per (token, kv head),
+// min(max|x|, clip[head]) / 127 (1 when that is 0), as
+// paged_kv_append_i8_clipped_batched.wgsl.
+template <bool KV8>
 __global__ __launch_bounds__(64) void qk_rope_append_kernel(RopeArgs p) {
     const int r = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const int W = p.hq + 2 * p.hkv, half = p.hd >> 1;
     const uint32_t pos = p.pos[r];
-    const size_t slot = ((size_t)p.seq[r] * p.max_seq + pos) * p.hkv;
-    const float* src;
-    float* dst;
-    const float* nw;
-    if (h < p.nh) {
-        src = p.qkv + (size_t)r * W + h * p.hd;
-        dst = p.q + (size_t)r * p.hq + h * p.hd;
-        nw = p.qn;
-    } else if (h < p.nh + p.nkv) {
-        const int kh = h - p.nh;
-        src = p.qkv + (size_t)r * W + p.hq + kh * p.hd;
-        dst = p.kc + slot + kh * p.hd;
-        nw = p.kn;
-    } else {
-        const int kh = h - p.nh - p.nkv;
-        src = p.qkv + (size_t)r * W + p.hq + p.hkv + kh * p.hd;
-        dst = p.vc + slot + kh * p.hd;
-        for (int i = lane; i < p.hd; i += 64) dst[i] = src[i];
-        return;
-    }
-    float x0[2], x1[2];
+    const size_t tok = (size_t)p.seq[r] * p.max_seq + pos;
+    const bool is_q = h < p.nh, is_k = !is_q && h < p.nh + p.nkv;
+    const int kh = is_q ? 0 : (is_k ? h - p.nh : h - p.nh - p.nkv);
+    const float* src = p.qkv + (size_t)r * W +
+                       (is_q ? h * p.hd : (is_k ? p.hq + kh * p.hd : p.hq + p.hkv + kh * p.hd));
+    float y0[2], y1[2];
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int m = lane + 64 * u;
-        x0[u] = x1[u] = 0.0f;
+        y0[u] = y1[u] = 0.0f;
         if (m < half) {
-            x0[u] = src[m];
-            x1[u] = src[m + half];
-            ss += x0[u] * x0[u] + x1[u] * x1[u];
+            y0[u] = src[m];
+            y1[u] = src[m + half];
+            ss += y0[u] * y0[u] + y1[u] * y1[u];
         }
     }
-    float inv = 1.0f;
-    if (p.qk_norm) {
-        ss = wave_sum(ss);
-        inv = 1.0f / sqrtf(ss / (float)p.hd + p.eps);
+    if (is_q || is_k) {
+        const float* nw = is_q ? p.qn : p.kn;
+        float inv = 1.0f;
+        if (p.qk_norm) {
+            ss = wave_sum(ss);
+            inv = 1.0f / sqrtf(ss / (float)p.hd + p.eps);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int m = lane + 64 * u;
+            if (m >= half) continue;
+            float a = y0[u], b = y1[u];
+            if (p.qk_norm) {
+                a = a * inv * nw[m];
+                b = b * inv * nw[m + half];
+            }
+            const float angle = (float)pos * powf(p.theta, -(float)(2 * m) / (float)p.hd);
+            const float c = cosf(angle), s = sinf(angle);
+            y0[u] = a * c - b * s;
+            y1[u] = b * c + a * s;
+        }
     }
+    if (is_q || !KV8) {
+        float* dst = is_q ? p.q + (size_t)r * p.hq + h * p.hd
+                          : static_cast<float*>(is_k ? p.kc : p.vc) + tok * p.hkv + kh * p.hd;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int m = lane + 64 * u;
+            if (m >= half) continue;
+            dst[m] = y0[u];
+            dst[m + half] = y1[u];
+        }
+        return;
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+        if (lane + 64 * u < half) mx = fmaxf(mx, fmaxf(fabsf(y0[u]), fabsf(y1[u])));
+    mx = wave_max(mx);
+    float scale = fminf(mx, (is_k ? p.kclip : p.vclip)[kh]) / 127.0f;
+    if (scale == 0.0f) scale = 1.0f;
+    uint8_t* d8 = static_cast<uint8_t*>(is_k ? p.kc : p.vc) + tok * p.hkv + kh * p.hd;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int m = lane + 64 * u;
         if (m >= half) continue;
-        float a = x0[u], b = x1[u];
-        if (p.qk_norm) {
-            a = a * inv * nw[m];
-            b = b * inv * nw[m + half];
-        }
-        const float angle = (float)pos * powf(p.theta, -(float)(2 * m) / (float)p.hd);
-        const float c = cosf(angle), s = sinf(angle);
-        dst[m] = a * c - b * s;
-        dst[m + half] = b * c + a * s;
+        d8[m] = kv8_code(y0[u], scale);
+        d8[m + half] = kv8_code(y1[u], scale);
     }
+    if (lane == 0) (is_k ? p.ks : p.vs)[tok * p.nkv + kh] = scale;
 }
 
 constexpr int KCH = 32;  // keys per attention workgroup
 
 struct AttnArgs {
     const float* q;    // [rows, hq]
-    const float* kc;   // this layer's caches
-    const float* vc;
+    const void* kc;    // this layer's caches (f32, or int8 with KV8)
+    const void* vc;
+    const float* ks;   // KV8 scales [max_batch, max_seq, nkv]
+    const float* vs;
     const uint32_t* pos;
     const uint32_t* seq;
     float* part_o;     // [rows, nh, splits, hd]  sum_k exp(s_k - m) v_k over one chunk
@@ -297,6 +330,15 @@ struct AttnArgs {
 // attn_combine_quant_kernel merges the chunks: the same softmax as
 // paged_decode_scores_wg -> decode_softmax_batched -> paged_decode_apply_batched
 // up to f32 rounding order.
+// KV8 (paged_decode_scores_i8_batched / paged_decode_apply_i8_batched): the
+// score is (q . f32(k8)) * kscale * scale, the weighted sum adds
+// (p * f32(v8)) * vscale.
+__device__ __forceinline__ float4 i8x4(uint32_t w) {
+    return make_float4((float)(int8_t)(w & 0xffu), (float)(int8_t)((w >> 8) & 0xffu),
+                       (float)(int8_t)((w >> 16) & 0xffu), (float)(int8_t)(w >> 24));
+}
+
+template <bool KV8>
 __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     __shared__ float qs[MAX_GROUP * 256];
     __shared__ float es[MAX_GROUP * KCH];
@@ -309,6 +351,7 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     const int G = p.nh / p.nkv;
     for (int i = tid; i < G * p.hd; i += RT) qs[i] = p.q[(size_t)r * p.hq + (size_t)kh * G * p.hd + i];
     __syncthreads();
+    const size_t tok0 = (size_t)p.seq[r] * p.max_seq + j0;  // cache slot of this chunk's first key
     const size_t base = (size_t)p.seq[r] * p.max_seq * p.hkv + (size_t)kh * p.hd;
     {
         const int kk = tid >> 3, l8 = tid & 7;
@@ -316,9 +359,10 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
 #pragma unroll
         for (int g = 0; g < MAX_GROUP; ++g) acc[g] = 0.0f;
         if (kk < n) {
-            const float* kr = p.kc + base + (size_t)(j0 + kk) * p.hkv;
+            const size_t kro = base + (size_t)(j0 + kk) * p.hkv;
             for (int c = l8 * 4; c < p.hd; c += 32) {
-                const float4 kv = *reinterpret_cast<const float4*>(kr + c);
+                const float4 kv = KV8 ? i8x4(*reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.kc) + kro + c))
+                                      : *reinterpret_cast<const float4*>(static_cast<const float*>(p.kc) + kro + c);
 #pragma unroll
                 for (int g = 0; g < MAX_GROUP; ++g) {
                     if (g >= G) break;
@@ -334,6 +378,7 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
             v += __shfl_xor(v, 4, 64);
             v += __shfl_xor(v, 2, 64);
             v += __shfl_xor(v, 1, 64);
+            if (KV8 && kk < n) v = v * p.ks[(tok0 + kk) * p.nkv + kh];
             if (l8 == 0) es[g * KCH + kk] = v * p.scale;
         }
     }
@@ -358,12 +403,20 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
         }
     }
     __syncthreads();
-    const float* vb = p.vc + base + (size_t)j0 * p.hkv;
+    const size_t vbo = base + (size_t)j0 * p.hkv;
     for (int i = tid; i < G * p.hd; i += RT) {
         const int g = i / p.hd, d = i - g * p.hd;
         float acc = 0.0f;
+        if constexpr (KV8) {
+            const int8_t* vb = reinterpret_cast<const int8_t*>(p.vc) + vbo;
 #pragma unroll 8
-        for (int k = 0; k < n; ++k) acc += es[g * KCH + k] * vb[(size_t)k * p.hkv + d];
+            for (int k = 0; k < n; ++k)
+                acc += es[g * KCH + k] * (float)vb[(size_t)k * p.hkv + d] * p.vs[(tok0 + k) * p.nkv + kh];
+        } else {
+            const float* vb = static_cast<const float*>(p.vc) + vbo;
+#pragma unroll 8
+            for (int k = 0; k < n; ++k) acc += es[g * KCH + k] * vb[(size_t)k * p.hkv + d];
+        }
         const size_t slot = ((size_t)r * p.nh + kh * G + g) * p.splits + sp;
         p.part_o[slot * p.hd + d] = acc;
         if (d == 0) {
@@ -526,8 +579,11 @@ struct bh_qwen3 {
     float* norm = nullptr;
     uint32_t* head = nullptr;
     float* shead = nullptr;
-    float *kc = nullptr, *vc = nullptr;
-    size_t layer_kv = 0;  // floats per layer per cache
+    void *kc = nullptr, *vc = nullptr;  // f32 or int8 elements
+    float *kscale = nullptr, *vscale = nullptr;  // KV8: [L][max_batch][max_seq][nkv]
+    float *kclip = nullptr, *vclip = nullptr;    // KV8: [L][nkv], FLT_MAX = no clipping
+    size_t layer_kv = 0;  // elements per layer per cache
+    size_t kv_elem = 4;   // bytes per cache element
 
     float *res = nullptr, *qkv = nullptr, *q = nullptr, *proj = nullptr, *gu = nullptr;
     float *part_o = nullptr, *part_ml = nullptr;  // attention chunk partials
@@ -634,8 +690,11 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
     const float scale = 1.0f / sqrtf((float)hd);
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         const bh_qwen3::Layer& Ly = e->L[l];
-        float* kc = e->kc + l * e->layer_kv;
-        float* vc = e->vc + l * e->layer_kv;
+        void* kc = static_cast<uint8_t*>(e->kc) + l * e->layer_kv * e->kv_elem;
+        void* vc = static_cast<uint8_t*>(e->vc) + l * e->layer_kv * e->kv_elem;
+        const size_t lsc = (size_t)l * e->max_batch * e->max_seq * nkv;
+        float* ksl = e->c.kv_int8 ? e->kscale + lsc : nullptr;
+        float* vsl = e->c.kv_int8 ? e->vscale + lsc : nullptr;
         NormQuantArgs na{};
         if (l == 0) {
             na.tok = tok;
@@ -653,13 +712,16 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
         na.xq_words = d / 4;
         BH_TRY(launch_norm_quant(e, na, rows));
         BH_TRY(launch_linear(e, Ly.wqkv, Ly.sqkv, e->qkv, rows, d, (int)e->W));
-        RopeArgs ra{e->qkv, e->q, kc, vc, Ly.qn, Ly.kn, pos, seq, nh, nkv, hd, (int)e->hq, (int)e->hkv,
-                    (int)e->max_seq, (int)c.qk_norm, c.rms_eps, c.rope_theta};
-        qk_rope_append_kernel<<<dim3(rows, nh + 2 * nkv), 64, 0, e->stream>>>(ra);
+        RopeArgs ra{e->qkv, e->q, kc, vc, ksl, vsl, e->kclip + (size_t)l * nkv, e->vclip + (size_t)l * nkv, Ly.qn,
+                    Ly.kn, pos, seq, nh, nkv, hd, (int)e->hq, (int)e->hkv, (int)e->max_seq, (int)c.qk_norm,
+                    c.rms_eps, c.rope_theta};
+        if (c.kv_int8) qk_rope_append_kernel<true><<<dim3(rows, nh + 2 * nkv), 64, 0, e->stream>>>(ra);
+        else qk_rope_append_kernel<false><<<dim3(rows, nh + 2 * nkv), 64, 0, e->stream>>>(ra);
         BH_HIP(hipGetLastError(), "qk_rope_append launch");
-        AttnArgs aa{e->q, kc, vc, pos, seq, e->part_o, e->part_ml, nh, nkv, hd, (int)e->hq, (int)e->hkv,
-                    (int)e->max_seq, splits, scale};
-        attn_split_kernel<<<dim3(rows, nkv, splits), RT, 0, e->stream>>>(aa);
+        AttnArgs aa{e->q, kc, vc, ksl, vsl, pos, seq, e->part_o, e->part_ml, nh, nkv, hd, (int)e->hq,
+                    (int)e->hkv, (int)e->max_seq, splits, scale};
+        if (c.kv_int8) attn_split_kernel<true><<<dim3(rows, nkv, splits), RT, 0, e->stream>>>(aa);
+        else attn_split_kernel<false><<<dim3(rows, nkv, splits), RT, 0, e->stream>>>(aa);
         BH_HIP(hipGetLastError(), "attention launch");
         BH_TRY(launch_combine_quant(e, rows, splits));
         BH_TRY(launch_linear(e, Ly.wo, Ly.so, e->proj, rows, (int)e->hq, d));
@@ -850,12 +912,18 @@ int bh_qwen3_create(const bh_qwen3_config* cfg, uint32_t max_batch, uint32_t max
             return bail(rc);
     }
     e->layer_kv = (size_t)max_batch * max_seq * e->hkv;
+    e->kv_elem = c.kv_int8 ? 1 : 4;
     e->tmpw_floats = std::max<uint64_t>(std::max<uint64_t>((uint64_t)e->W * d, 2 * ff * d), d * std::max<uint64_t>(hq, ff));
     if (!c.tie_embeddings) e->tmpw_floats = std::max<uint64_t>(e->tmpw_floats, (uint64_t)c.vocab * d);
     const uint64_t R = max_rows;
     if ((rc = dalloc(e, &e->emb, (uint64_t)c.vocab * d)) || (rc = dalloc(e, &e->norm, d)) ||
         (rc = dalloc(e, &e->head, (uint64_t)c.vocab * d / 4)) || (rc = dalloc(e, &e->shead, c.vocab)) ||
-        (rc = dalloc(e, &e->kc, e->layer_kv * c.n_layers)) || (rc = dalloc(e, &e->vc, e->layer_kv * c.n_layers)) ||
+        (rc = dalloc(e, (uint8_t**)&e->kc, e->layer_kv * c.n_layers * e->kv_elem)) ||
+        (rc = dalloc(e, (uint8_t**)&e->vc, e->layer_kv * c.n_layers * e->kv_elem)) ||
+        (rc = dalloc(e, &e->kscale, c.kv_int8 ? (uint64_t)c.n_layers * max_batch * max_seq * c.n_kv_heads : 1)) ||
+        (rc = dalloc(e, &e->vscale, c.kv_int8 ? (uint64_t)c.n_layers * max_batch * max_seq * c.n_kv_heads : 1)) ||
+        (rc = dalloc(e, &e->kclip, (uint64_t)c.n_layers * c.n_kv_heads)) ||
+        (rc = dalloc(e, &e->vclip, (uint64_t)c.n_layers * c.n_kv_heads)) ||
         (rc = dalloc(e, &e->res, R * d)) || (rc = dalloc(e, &e->qkv, R * e->W)) || (rc = dalloc(e, &e->q, R * hq)) ||
         (rc = dalloc(e, &e->part_o, R * c.n_heads * e->max_splits * c.head_dim)) || (rc = dalloc(e, &e->part_ml, R * c.n_heads * e->max_splits * 2)) || (rc = dalloc(e, &e->proj, R * d)) || (rc = dalloc(e, &e->gu, R * 2 * ff)) ||
         (rc = dalloc(e, &e->sx, R)) || (rc = dalloc(e, &e->xq, R * e->xq_words)) ||
@@ -866,6 +934,10 @@ int bh_qwen3_create(const bh_qwen3_config* cfg, uint32_t max_batch, uint32_t max
         (rc = dalloc(e, &e->pos_dec, max_batch)) || (rc = dalloc(e, &e->seq_dec, max_batch)) ||
         (rc = dalloc(e, &e->hist, (uint64_t)max_seq * max_batch)) || (rc = dalloc(e, &e->ctl, 2)))
         return bail(rc);
+    std::vector<float> clip((size_t)c.n_layers * c.n_kv_heads, FLT_MAX);
+    if (hipMemcpy(e->kclip, clip.data(), clip.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(e->vclip, clip.data(), clip.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+        return bail(fail(BH_ERR_HIP, "bh_qwen3_create: upload"));
     std::vector<uint32_t> seq(max_batch);
     for (uint32_t b = 0; b < max_batch; ++b) seq[b] = b;
     if (hipMemcpy(e->seq_dec, seq.data(), max_batch * 4, hipMemcpyHostToDevice) != hipSuccess)
@@ -988,6 +1060,15 @@ int bh_qwen3_autotune(bh_qwen3* e, uint32_t reps) {
         e->graph = nullptr;
     }
     return measured;
+}
+
+int bh_qwen3_set_kv_clip(bh_qwen3* e, uint32_t layer, uint32_t which, const float* clip) {
+    if (!e || !clip || layer >= e->c.n_layers || which > 1)
+        return fail(BH_ERR_INVALID, "bh_qwen3_set_kv_clip: bad argument");
+    (void)hipSetDevice(e->device);
+    float* dst = (which ? e->vclip : e->kclip) + (size_t)layer * e->c.n_kv_heads;
+    BH_HIP(hipMemcpyAsync(dst, clip, e->c.n_kv_heads * 4, hipMemcpyHostToDevice, e->stream), "upload");
+    return sync(e);
 }
 
 int bh_qwen3_init_random(bh_qwen3* e, uint64_t seed) {

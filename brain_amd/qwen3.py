@@ -14,7 +14,7 @@ import numpy as np
 from ._lib import Qwen3ConfigT, check, load
 
 QWEN3_0_6B = dict(vocab=151936, n_layers=28, d_model=1024, n_heads=16, n_kv_heads=8, head_dim=128,
-                  d_ff=3072, rope_theta=1.0e6, rms_eps=1e-6, tie_embeddings=1, qk_norm=1)
+                  d_ff=3072, rope_theta=1.0e6, rms_eps=1e-6, tie_embeddings=1, qk_norm=1, kv_int8=0)
 """QwenConfig::qwen3_0_6b (crates/qwen3/src/config.rs:100-118)."""
 
 EAGER = 1
@@ -24,7 +24,8 @@ class Qwen3Engine:
     def __init__(self, cfg, max_batch, max_seq, max_rows=None, device=0):
         self.cfg = dict(QWEN3_0_6B, **cfg) if cfg is not QWEN3_0_6B else dict(cfg)
         c = Qwen3ConfigT()
-        for k in ("vocab", "n_layers", "d_model", "n_heads", "n_kv_heads", "head_dim", "d_ff", "tie_embeddings", "qk_norm"):
+        for k in ("vocab", "n_layers", "d_model", "n_heads", "n_kv_heads", "head_dim", "d_ff", "tie_embeddings", "qk_norm",
+                  "kv_int8"):
             setattr(c, k, int(self.cfg[k]))
         c.rope_theta, c.rms_eps = float(self.cfg["rope_theta"]), float(self.cfg["rms_eps"])
         self._h = C.c_void_p()
@@ -65,6 +66,11 @@ class Qwen3Engine:
     def load(self, path):
         """Every parameter from an int8 safetensors checkpoint (brain_amd.int8_format)."""
         check(load().bh_qwen3_load(self._h, path.encode()))
+
+    def set_kv_clip(self, layer, which, clip):
+        """int8 KV ceilings per kv head for layer `layer`, K (which=0) or V (1)."""
+        clip = np.ascontiguousarray(clip, dtype=np.float32)
+        check(load().bh_qwen3_set_kv_clip(self._h, layer, which, clip.ctypes.data))
 
     def autotune(self, reps=8):
         """Measure GEMV vs tile for every linear shape at row buckets up to max_batch."""

@@ -341,6 +341,8 @@ typedef struct {
     float rope_theta, rms_eps;
     uint32_t tie_embeddings; /* 1: the head is tok.weight (quantized), else lm_head.weight */
     uint32_t qk_norm;        /* 1: per-head RMSNorm of q and k before RoPE */
+    uint32_t kv_int8;        /* engine option: 1 = int8 KV cache with per-(token, kv head) scales
+                                (paged_kv_append_i8_clipped_batched / paged_decode_{scores,apply}_i8_batched) */
 } bh_qwen3_config;
 
 /* Engine for up to max_batch sequences of max_seq positions each; prefill
@@ -382,6 +384,10 @@ int bh_qwen3_decode(bh_qwen3* e, uint32_t steps, uint32_t flags, uint32_t* out);
 int bh_qwen3_logits(bh_qwen3* e, float* out, uint64_t n);
 /* Positions filled so far (prompt + decoded) of each sequence: len[batch]. */
 int bh_qwen3_lengths(bh_qwen3* e, uint32_t* len, uint32_t batch);
+/* int8 KV: per-kv-head ceilings of layer `layer` for K (which 0) or V (1);
+ * the scale is min(max|x|, clip)/127. Default FLT_MAX (no clipping), the
+ * reference's uncalibrated sentinel. */
+int bh_qwen3_set_kv_clip(bh_qwen3* e, uint32_t layer, uint32_t which, const float* clip);
 void* bh_qwen3_stream(bh_qwen3* e);
 /* Measure the GEMV/tile choice for every distinct linear shape of the engine
  * at row buckets 1..max_batch (bh_tune_i8); BRAIN_NO_AUTOTUNE=1 skips it, as

@@ -272,7 +272,8 @@ def splitmix_u64(seed, count):
 class Qwen3Config(C.Structure):
     """or_qwen3_config (qwen3_oracle.h), the QwenConfig fields the forward reads."""
     _fields_ = [(n, C.c_uint32) for n in ("vocab", "n_layers", "d_model", "n_heads", "n_kv_heads", "head_dim", "d_ff")] + \
-               [("rope_theta", C.c_float), ("rms_eps", C.c_float), ("tie_embeddings", C.c_uint32), ("qk_norm", C.c_uint32)]
+               [("rope_theta", C.c_float), ("rms_eps", C.c_float), ("tie_embeddings", C.c_uint32), ("qk_norm", C.c_uint32),
+                ("kv_int8", C.c_uint32)]
 
 
 def qwen3_param_list(cfg):
@@ -316,6 +317,7 @@ def _qcfg(cfg):
         setattr(c, k, cfg[k])
     c.rope_theta, c.rms_eps = cfg.get("rope_theta", 1e6), cfg.get("rms_eps", 1e-6)
     c.tie_embeddings, c.qk_norm = cfg.get("tie_embeddings", 1), cfg.get("qk_norm", 1)
+    c.kv_int8 = cfg.get("kv_int8", 0)
     return c
 
 

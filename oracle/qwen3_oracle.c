@@ -7,6 +7,12 @@
  * prompt token by token, because every op is row-wise except attention,
  * which reads only earlier positions):
  *
+ * With kv_int8, K and V are stored as int8 codes with one scale per (token,
+ * kv head): scale = max|x|/127 (1 if 0), code = clamp(round_even(x/scale))
+ * (paged_kv_append_i8_clipped_batched.wgsl, FLT_MAX clip); scores use
+ * (q . f32(code)) * kscale * hd^-1/2 and the context (p * f32(code)) * vscale
+ * (paged_decode_{scores,apply}_i8_batched.wgsl).
+ *
  *   x = tok[t]                                   embed.wgsl
  *   per layer:
  *     xn = rmsnorm(x, ln1)                       rmsnorm_rows.wgsl:24-44
@@ -179,6 +185,8 @@ int or_qwen3_generate(const or_qwen3_config *c, const float *params, int int8, c
 
     float *K = (float *)malloc(sizeof(float) * L * T * hkv);
     float *Vc = (float *)malloc(sizeof(float) * L * T * hkv);
+    float *KS = (float *)malloc(sizeof(float) * L * T * nkv); /* kv_int8 scales; K/Vc then hold codes */
+    float *VS = (float *)malloc(sizeof(float) * L * T * nkv);
     float *x = (float *)malloc(sizeof(float) * d), *xn = (float *)malloc(sizeof(float) * d);
     float *q = (float *)malloc(sizeof(float) * hq), *k = (float *)malloc(sizeof(float) * hkv);
     float *v = (float *)malloc(sizeof(float) * hkv), *ctx = (float *)malloc(sizeof(float) * hq);
@@ -213,6 +221,22 @@ int or_qwen3_generate(const or_qwen3_config *c, const float *params, int int8, c
                 }
                 memcpy(Kl + (size_t)pos * hkv, k, sizeof(float) * hkv);
                 memcpy(Vl + (size_t)pos * hkv, v, sizeof(float) * hkv);
+                float *KSl = KS + (size_t)l * T * nkv, *VSl = VS + (size_t)l * T * nkv;
+                if (c->kv_int8) {
+                    for (uint32_t h = 0; h < nkv; ++h)
+                        for (int which = 0; which < 2; ++which) {
+                            float *xr = (which ? Vl : Kl) + (size_t)pos * hkv + h * hd;
+                            float mxa = 0.0f;
+                            for (uint32_t e = 0; e < hd; ++e) mxa = fmaxf(mxa, fabsf(xr[e]));
+                            float sc = fminf(mxa, FLT_MAX) / 127.0f;
+                            if (sc == 0.0f) sc = 1.0f;
+                            for (uint32_t e = 0; e < hd; ++e) {
+                                float qv = rintf(xr[e] / sc);
+                                xr[e] = qv < -127.0f ? -127.0f : (qv > 127.0f ? 127.0f : qv);
+                            }
+                            (which ? VSl : KSl)[(size_t)pos * nkv + h] = sc;
+                        }
+                }
                 for (uint32_t h = 0; h < nh; ++h) {
                     const uint32_t kh = h / G;
                     float mx = -3.4e38f;
@@ -220,6 +244,7 @@ int or_qwen3_generate(const or_qwen3_config *c, const float *params, int int8, c
                         float acc = 0.0f;
                         const float *kr = Kl + (size_t)j * hkv + kh * hd;
                         for (uint32_t e = 0; e < hd; ++e) acc += q[h * hd + e] * kr[e];
+                        if (c->kv_int8) acc = acc * KSl[(size_t)j * nkv + kh];
                         s[j] = acc * scale;
                         if (s[j] > mx) mx = s[j];
                     }
@@ -229,7 +254,10 @@ int or_qwen3_generate(const or_qwen3_config *c, const float *params, int int8, c
                     for (uint32_t j = 0; j <= pos; ++j) s[j] = expf(s[j] - mx) * inv;
                     for (uint32_t e = 0; e < hd; ++e) {
                         float acc = 0.0f;
-                        for (uint32_t j = 0; j <= pos; ++j) acc += s[j] * Vl[(size_t)j * hkv + kh * hd + e];
+                        for (uint32_t j = 0; j <= pos; ++j) {
+                            const float pv = s[j] * Vl[(size_t)j * hkv + kh * hd + e];
+                            acc += c->kv_int8 ? pv * VSl[(size_t)j * nkv + kh] : pv;
+                        }
                         ctx[h * hd + e] = acc;
                     }
                 }
@@ -255,7 +283,7 @@ int or_qwen3_generate(const or_qwen3_config *c, const float *params, int int8, c
             if (pos + 1 == T) break;
         }
     }
-    free(K); free(Vc); free(x); free(xn); free(q); free(k); free(v); free(ctx); free(o);
+    free(K); free(Vc); free(KS); free(VS); free(x); free(xn); free(q); free(k); free(v); free(ctx); free(o);
     free(g); free(u); free(s); free(logits); free(tmp);
     for (uint32_t i = 0; i < 7 * L; ++i) lin_free(&lq[i]);
     lin_free(&head);

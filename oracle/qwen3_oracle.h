@@ -7,6 +7,7 @@ typedef struct {
     uint32_t vocab, n_layers, d_model, n_heads, n_kv_heads, head_dim, d_ff;
     float rope_theta, rms_eps;
     uint32_t tie_embeddings, qk_norm;
+    uint32_t kv_int8; /* int8 KV cache (paged_kv_append_i8_clipped_batched with the FLT_MAX clip) */
 } or_qwen3_config;
 
 /* argmax_row.wgsl: first index of the largest value strictly above -FLT_MAX, else 0. */

@@ -83,8 +83,9 @@ def compare(cfg, w, prompts, steps, max_rows=None):
     e.close()
 
 
-@pytest.mark.parametrize("cfg_over", [{}, dict(tie_embeddings=0), dict(qk_norm=0, n_kv_heads=4)],
-                         ids=["tied", "untied", "mha_no_qknorm"])
+@pytest.mark.parametrize("cfg_over", [{}, dict(tie_embeddings=0), dict(qk_norm=0, n_kv_heads=4), dict(kv_int8=1),
+                                      dict(kv_int8=1, n_kv_heads=1, tie_embeddings=0)],
+                         ids=["tied", "untied", "mha_no_qknorm", "kv_int8", "kv_int8_mqa"])
 def test_engine_matches_oracle(gpu, cfg_over):
     cfg = dict(SMALL, **cfg_over)
     w = scaled_weights(cfg, seed=7)
@@ -196,3 +197,26 @@ def test_autotune_changes_no_result(gpu):
         b.close()
     L().bh_tune_clear()
     a.close()
+
+
+def test_kv_int8_chunking_graph_and_clip(gpu):
+    """int8 KV: chunked prefill and graph decode stay bit-identical; an explicit
+    FLT_MAX clip equals the default; a tight clip changes the result."""
+    cfg = dict(SMALL, kv_int8=1)
+    w = scaled_weights(cfg, seed=31)
+    prompts = np.random.default_rng(6).integers(0, cfg["vocab"], size=(2, 30))
+    a = engine_for(cfg, w, 2, 48)
+    b = engine_for(cfg, w, 2, 48, max_rows=6)
+    big = np.full(cfg["n_kv_heads"], np.finfo(np.float32).max, np.float32)
+    for l in range(cfg["n_layers"]):
+        b.set_kv_clip(l, 0, big)
+        b.set_kv_clip(l, 1, big)
+    assert (a.generate(prompts, 8) == b.generate(prompts, 8, eager=True)).all()
+    assert np.array_equal(a.logits(), b.logits())
+    c = engine_for(cfg, w, 2, 48)
+    for l in range(cfg["n_layers"]):
+        c.set_kv_clip(l, 0, np.full(cfg["n_kv_heads"], 0.05, np.float32))
+    c.generate(prompts, 8)
+    assert not np.array_equal(a.logits(), c.logits())
+    for e in (a, b, c):
+        e.close()

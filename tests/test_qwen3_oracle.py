@@ -122,3 +122,15 @@ def test_argmax_rule():
     assert o.argmax_row([-inf, -inf]) == 0
     assert o.argmax_row([-3.4028235e38, -inf]) == 0          # must be strictly above -FLT_MAX
     assert o.argmax_row([-inf, -1e30, 5.0, inf]) == 3
+
+
+def test_oracle_int8_kv_tracks_fp32_kv():
+    """crates/qwen3/src/model.rs:2638-2661 (int8_kv_decode_tracks_fp32): the
+    int8 KV cache stays within rel-L2 0.10 of the f32 cache."""
+    cfg = dict(TINY, d_model=64, d_ff=128)
+    w = o.qwen3_init(cfg, seed=13, gain_noise=0.1)
+    prompts = np.random.default_rng(4).integers(0, cfg["vocab"], size=(2, 6))
+    _, l32 = o.qwen3_generate(cfg, w, prompts, 3, int8=True)
+    _, l8 = o.qwen3_generate(dict(cfg, kv_int8=1), w, prompts, 3, int8=True)
+    r = rel_l2(l8[0], l32[0])
+    assert 0 < r < 0.10, r
