@@ -125,6 +125,7 @@ SIGNATURES = {
     "bh_matmul_q4_gemv": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
     "bh_matmul_q4_dyn": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
     "bh_matmul_q4": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
+    "bh_moe_linear_gated_i8": (i32, [vp, vp, vp, vp, vp, vp, u32, u32, vp, u32, u32, u32]),
     "bh_dequantize_weight": (i32, [vp, vp, u64, u64, vp]),
     "bh_quant_rows_steps": (i32, [vp, P(u32), vp, vp, vp, u32, u32, u32, P(vp)]),
     "bh_mm8_rows_off": (i32, [vp, u32, vp, vp, vp, vp, vp, u32, u64, u32, u32, u32, P(vp)]),

@@ -37,6 +37,12 @@ hipError_t launch_gemm_i8_static(hipStream_t s, const uint32_t* xq, const uint32
                                  float* out, int m, int kg, int n);
 
 size_t gemm_workspace_ints(int m, int kg, int n, size_t* counters);
+hipError_t launch_gemv_i8_gated(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
+                                const float* sw, const float* gate, int gate_stride, int gate_col, float* out, int m,
+                                int kg, int n);
+hipError_t launch_gemm_i8_gated(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
+                                const float* sw, const float* gate, int gate_stride, int gate_col, float* out, int m,
+                                int kg, int n);
 hipError_t launch_gemv_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
                           const float* bias, void* out, int out_dtype, int m, int k, int n);
 hipError_t launch_gemm_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
@@ -378,6 +384,22 @@ int bh_matmul_q4(void* stream, const uint32_t* xq, const uint32_t* wq4, const fl
     return bh_matmul_q4_dyn(stream, xq, wq4, sx, sw, bias, out, out_dtype, m, k, n);
 }
 
+int bh_moe_linear_gated_i8(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
+                           const float* gate, uint32_t n_experts, uint32_t e_idx, float* out, uint32_t m, uint32_t kg,
+                           uint32_t n) {
+    int rc = check_matmul(xq, wq, sx, sw, out, OUT_F32, m, kg, n, "bh_moe_linear_gated_i8");
+    if (rc) return rc;
+    if (m == 0 || n == 0) return BH_OK;
+    if (!gate || e_idx >= n_experts || n_experts > I32MAX)
+        return fail(BH_ERR_INVALID, "bh_moe_linear_gated_i8: gate null or e_idx %u >= n_experts %u", e_idx, n_experts);
+    const hipError_t e = m <= (uint32_t)GEMV_MAX_ROWS
+                             ? launch_gemv_i8_gated((hipStream_t)stream, xq, wq, sx, sw, gate, (int)n_experts, (int)e_idx,
+                                                    out, (int)m, (int)kg, (int)n)
+                             : launch_gemm_i8_gated((hipStream_t)stream, xq, wq, sx, sw, gate, (int)n_experts, (int)e_idx,
+                                                    out, (int)m, (int)kg, (int)n);
+    return hip_status(e, "moe_linear_gated_i8 launch");
+}
+
 int bh_f32_to_bf16(void* stream, const float* x, uint16_t* out, uint64_t n) {
     if (n == 0) return BH_OK;
     if (!x || !out) return fail(BH_ERR_INVALID, "bh_f32_to_bf16: null buffer");
@@ -639,6 +661,7 @@ enum KernelId : int {
     K_ROOF_DP4A,
     K_MATMUL_Q4_DYN,
     K_MATMUL_Q4_GEMV,
+    K_MOE_LINEAR_GATED_I8,
 };
 
 struct KernelSpec {
@@ -654,6 +677,7 @@ static const KernelSpec kSpecs[] = {
     {"matmul_i8_gemv", K_MATMUL_I8_GEMV, 5, 3}, {"matmul_i8", K_MATMUL_I8, 3, 5},
     {"bias_add", K_BIAS_ADD, 2, 2},            {"roof_dp4a", K_ROOF_DP4A, 2, 4},
     {"matmul_q4_dyn", K_MATMUL_Q4_DYN, 5, 3},   {"matmul_q4_gemv", K_MATMUL_Q4_GEMV, 5, 3},
+    {"moe_linear_gated_i8", K_MOE_LINEAR_GATED_I8, 6, 5},
 };
 
 static const KernelSpec* spec_of(const char* name) {
@@ -749,6 +773,12 @@ static int binding_needs(KernelId id, const std::vector<uint32_t>& p, std::vecto
             if (b % 8) return fail(BH_ERR_INVALID, "%s: k=%llu is not a multiple of 8", name, (unsigned long long)b);
             need = {a * b / 4, c * b / 8, a, c, a * c};
             return BH_OK;
+        case K_MOE_LINEAR_GATED_I8: {  // params [m, kg, n, n_experts, e_idx]
+            const uint64_t ne = p.size() > 3 ? p[3] : 0, ei = p.size() > 4 ? p[4] : 0;
+            if (ei >= ne) return fail(BH_ERR_INVALID, "%s: e_idx %llu >= n_experts %llu", name, (unsigned long long)ei, (unsigned long long)ne);
+            need = {a * b, c * b, a, c, a * ne, a * c};
+            return BH_OK;
+        }
         case K_BIAS_ADD: need = {a * b, b}; return BH_OK;
         case K_ROOF_DP4A: need = {a, a}; return BH_OK;
         default: return fail(BH_ERR_UNSUPPORTED, "kernel '%s' is not provided by the hip backend", name);
@@ -765,6 +795,7 @@ static bool is_output(KernelId id, uint32_t i) {
         case K_MATMUL_I8_GEMV:
         case K_MATMUL_Q4_DYN:
         case K_MATMUL_Q4_GEMV: return i == 4;
+        case K_MOE_LINEAR_GATED_I8: return i == 5;
         case K_MATMUL_I8: return i == 2;
         case K_BIAS_ADD: return i == 0;
         case K_ROOF_DP4A: return i == 1;
@@ -850,6 +881,10 @@ static int launch_step(bh_backend* be, const bh_dispatch* s) {
             return bh_matmul_i8_gemv(st, (const uint32_t*)wptr(s, 0), (const uint32_t*)wptr(s, 1),
                                      (const float*)wptr(s, 2), (const float*)wptr(s, 3), nullptr, wptr(s, 4), OUT_F32,
                                      p[0], p[1], p[2]);
+        case K_MOE_LINEAR_GATED_I8:
+            return bh_moe_linear_gated_i8(st, (const uint32_t*)wptr(s, 0), (const uint32_t*)wptr(s, 1),
+                                          (const float*)wptr(s, 2), (const float*)wptr(s, 3), (const float*)wptr(s, 4),
+                                          p[3], p[4], (float*)wptr(s, 5), p[0], p[1], p[2]);
         case K_MATMUL_Q4_DYN:
             return bh_matmul_q4_dyn(st, (const uint32_t*)wptr(s, 0), (const uint32_t*)wptr(s, 1),
                                     (const float*)wptr(s, 2), (const float*)wptr(s, 3), nullptr, wptr(s, 4), OUT_F32,

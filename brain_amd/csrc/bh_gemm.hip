@@ -76,7 +76,15 @@ struct GemmArgs {
     int splits;       // S (1 = no split)
     int* ws;          // [m*n] i32 split-K workspace (zero between calls)
     int* counters;    // [tiles] arrival counters (zero between calls)
+    // Row gate of moe_linear_gated_i8.wgsl (null: none): row r of the output
+    // is +0 when gate[r * gate_stride + gate_col] <= 0.
+    const float* gate;
+    int gate_stride, gate_col;
 };
+
+__device__ __forceinline__ bool gated_off(const GemmArgs& a, int row) {
+    return a.gate && a.gate[(int64_t)row * a.gate_stride + a.gate_col] <= 0.0f;
+}
 
 // One output element through the epilogue.
 template <int OUT, bool HAS_BIAS, bool STATIC>
@@ -89,6 +97,7 @@ __device__ __forceinline__ void emit(const GemmArgs& a, int row, int col, int ac
         if constexpr (STATIC) v = (float)acc * (a.ssx * a.ssw);
         else v = dequant(acc, sxm, swn);
         if constexpr (HAS_BIAS) v = v + bn;
+        if (gated_off(a, row)) v = 0.0f;
         store_out<OUT>(a.out, idx, v);
     }
 }
@@ -568,6 +577,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
                 const int row = wrow0 + i * 32 + lrow;
                 float sxm = 0.0f;
                 if constexpr (!STATIC && OUT != OUT_I32) sxm = row < m ? a.sx[row] : 0.0f;
+                const bool off = OUT != OUT_I32 && row < m && gated_off(a, row);
 #pragma unroll
                 for (int j = 0; j < C::FN; ++j)
 #pragma unroll
@@ -594,6 +604,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
                                 const float4 bv = live ? *reinterpret_cast<const float4*>(a.bias + col) : make_float4(0.f, 0.f, 0.f, 0.f);
                                 f0 = f0 + bv.x; f1 = f1 + bv.y; f2 = f2 + bv.z; f3 = f3 + bv.w;
                             }
+                            if (off) f0 = f1 = f2 = f3 = 0.0f;
                             if constexpr (OUT == OUT_F32) {
                                 *reinterpret_cast<float4*>(dst) = make_float4(f0, f1, f2, f3);
                             } else {
@@ -658,6 +669,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
                 if (row >= m || col >= n) continue;
                 float sxm = 0.0f;
                 if constexpr (!STATIC && OUT != OUT_I32) sxm = a.sx[row];
+                const bool off = OUT != OUT_I32 && gated_off(a, row);
                 const int v0 = acc[i][j][4 * g + 0], v1 = acc[i][j][4 * g + 1];
                 const int v2 = acc[i][j][4 * g + 2], v3 = acc[i][j][4 * g + 3];
                 const int64_t idx = (int64_t)row * n + col;
@@ -674,6 +686,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
                             f2 = dequant(v2, sxm, swv.z); f3 = dequant(v3, sxm, swv.w);
                         }
                         if constexpr (HAS_BIAS) { f0 = f0 + bv.x; f1 = f1 + bv.y; f2 = f2 + bv.z; f3 = f3 + bv.w; }
+                        if (off) f0 = f1 = f2 = f3 = 0.0f;
                         if constexpr (OUT == OUT_F32) {
                             *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + idx) = make_float4(f0, f1, f2, f3);
                         } else {
@@ -846,6 +859,15 @@ hipError_t launch_gemm_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
         case OUT_F32: return bias ? go_q4<OUT_F32, true>(s, al, a) : go_q4<OUT_F32, false>(s, al, a);
         default: return bias ? go_q4<OUT_BF16, true>(s, al, a) : go_q4<OUT_BF16, false>(s, al, a);
     }
+}
+
+hipError_t launch_gemm_i8_gated(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
+                                const float* sw, const float* gate, int gate_stride, int gate_col, float* out, int m,
+                                int kg, int n) {
+    GemmArgs a{xq, wq, sx, sw, nullptr, out, m, kg, n, 0.f, 0.f, 1, nullptr, nullptr, gate, gate_stride, gate_col};
+    const bool al = gemm_aligned(xq, wq, kg);
+    const bool dma = al && ((kg * 4) % 128 == 0);
+    return go_cfg<OUT_F32, false, false>(s, al, dma, choose_tiles(m, kg, n), a);
 }
 
 }  // namespace bh

@@ -39,6 +39,8 @@ struct GemvArgs {
     const float* bias;
     void* out;
     int m, kg, n;
+    const float* gate;  // moe_linear_gated_i8 row gate (null: none): row r is +0 when gate[r*stride+col] <= 0
+    int gate_stride, gate_col;
 };
 
 template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int KSPLIT, bool XLDS, int U, int CG, int NW = GV_WAVES>
@@ -140,6 +142,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
             } else {
                 float v = dequant(s, a.sx[row], a.sw[col]);
                 if constexpr (HAS_BIAS) v = v + a.bias[col];
+                if (a.gate && a.gate[(int64_t)row * a.gate_stride + a.gate_col] <= 0.0f) v = 0.0f;
                 store_out<OUT>(a.out, idx, v);
             }
         }
@@ -240,9 +243,19 @@ hipError_t launch_gemv_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n) {
     const bool aligned = ((kg * 4) % 16 == 0) && ((reinterpret_cast<uintptr_t>(xq) & 15u) == 0) &&
                          ((reinterpret_cast<uintptr_t>(wq) & 15u) == 0);
-    GemvArgs a{xq, wq, sx, sw, bias, out, m, kg, n};
+    GemvArgs a{xq, wq, sx, sw, bias, out, m, kg, n, nullptr, 0, 0};
     if (m <= 16) return gv_out<1>(s, aligned, out_dtype, a);
     return gv_out<2>(s, aligned, out_dtype, a);
+}
+
+hipError_t launch_gemv_i8_gated(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
+                                const float* sw, const float* gate, int gate_stride, int gate_col, float* out, int m,
+                                int kg, int n) {
+    const bool aligned = ((kg * 4) % 16 == 0) && ((reinterpret_cast<uintptr_t>(xq) & 15u) == 0) &&
+                         ((reinterpret_cast<uintptr_t>(wq) & 15u) == 0);
+    GemvArgs a{xq, wq, sx, sw, nullptr, out, m, kg, n, gate, gate_stride, gate_col};
+    if (m <= 16) return gv_out<1>(s, aligned, OUT_F32, a);
+    return gv_out<2>(s, aligned, OUT_F32, a);
 }
 
 }  // namespace bh

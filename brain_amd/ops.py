@@ -171,3 +171,17 @@ def matmul_q4(xq, wq4, sx, sw, bias=None, out_dtype=torch.float32, variant="auto
     check(getattr(load(), _Q4_VARIANTS[variant])(
         _stream(), _ptr(xq), _ptr(wq4), _ptr(sx), _ptr(sw), _ptr(bias), _ptr(out), code, m, k, n))
     return out
+
+
+
+def moe_linear_gated_i8(xq, wq, sx, sw, gate, e_idx, out=None):
+    """moe_linear_gated_i8.wgsl: f32 out [m, n], rows with gate[row, e_idx] <= 0 are +0."""
+    m, kg = xq.shape
+    n = wq.shape[0]
+    n_experts = gate.shape[1]
+    _dev(xq, wq, sx, sw, gate, out)
+    _need(gate, torch.float32, m * n_experts, "gate")
+    out = torch.empty(m, n, device=xq.device, dtype=torch.float32) if out is None else out
+    check(load().bh_moe_linear_gated_i8(_stream(), _ptr(xq), _ptr(wq), _ptr(sx), _ptr(sw), _ptr(gate), n_experts,
+                                        e_idx, _ptr(out), m, kg, n))
+    return out

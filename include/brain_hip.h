@@ -140,6 +140,16 @@ int bh_matmul_q4_dyn(void* stream, const uint32_t* xq, const uint32_t* wq4, cons
 int bh_matmul_q4(void* stream, const uint32_t* xq, const uint32_t* wq4, const float* sx, const float* sw,
                  const float* bias, void* out, int out_dtype, uint32_t m, uint32_t k, uint32_t n);
 
+/* Sparse-MoE expert linear, int8 (crates/kernels/wgsl/moe_linear_gated_i8.wgsl):
+ * out [m,n] f32 = (f32(xq.wq^T) * sx) * sw for rows routed to expert e_idx,
+ * +0 for rows with gate[row * n_experts + e_idx] <= 0. The GEMV (m <= 32) or
+ * MFMA GEMM computes every row and the epilogue zeroes the unrouted ones.
+ * Step name "moe_linear_gated_i8": bindings [xq, wq, sx, sw, gate, out],
+ * params [m, kg, n, n_experts, e_idx]. */
+int bh_moe_linear_gated_i8(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
+                           const float* gate, uint32_t n_experts, uint32_t e_idx, float* out, uint32_t m, uint32_t kg,
+                           uint32_t n);
+
 /* f32 -> bf16 bits, round to nearest even, NaN -> (bits >> 16) | 0x0040: the
  * conversion every bf16 output of this library goes through
  * (crates/model/src/half.rs:49-58, f32_to_bf16). x [n] f32 -> out [n] u16. */

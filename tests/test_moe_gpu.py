@@ -1,0 +1,59 @@
+"""moe_linear_gated_i8 (sparse-MoE expert linear, int8) against the oracle.
+
+Routed rows (gate[row, e_idx] > 0, and NaN, which the reference's `<= 0`
+test lets through) are the matmul_i8_dyn result bit for bit; other rows are
+exactly +0.0.
+"""
+import numpy as np
+import pytest
+import torch
+
+from brain_amd import ops
+from oracle import oracle as o
+
+pytestmark = pytest.mark.gpu
+
+
+def dev_u32(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(device)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1024, 768), (8, 1024, 768), (32, 2048, 512), (33, 512, 300), (512, 1024, 1536)])
+def test_moe_linear_gated_i8(gpu, m, k, n):
+    rng = np.random.default_rng(m + k + n)
+    n_experts, e_idx = 8, 3
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    sx = o.max_abs_row(x)
+    xq = o.quant_pack(x, sx)
+    wq, sw = o.quantize_weight(rng.standard_normal((n, k)).astype(np.float32))
+    gate = rng.standard_normal((m, n_experts)).astype(np.float32)
+    gate[::5, e_idx] = 0.0                   # exactly 0: not routed
+    if m > 2:
+        gate[2, e_idx] = np.nan              # NaN: `<= 0` is false, so computed
+    got = ops.moe_linear_gated_i8(dev_u32(xq, gpu), dev_u32(wq, gpu), torch.from_numpy(sx).to(gpu),
+                                  torch.from_numpy(sw).to(gpu), torch.from_numpy(gate).to(gpu), e_idx).cpu().numpy()
+    want = o.epilogue(o.acc_exact(xq, wq), sx, sw)
+    off = gate[:, e_idx] <= 0
+    want[off] = 0.0
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert (got[off].view(np.uint32) == 0).all()      # +0, not -0
+
+
+def test_moe_step_through_the_backend(gpu):
+    from brain_amd.backend import HipBackend
+    m, k, n, ne, ei = 4, 256, 64, 4, 1
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    sx = o.max_abs_row(x)
+    xq = o.quant_pack(x, sx)
+    wq, sw = o.quantize_weight(rng.standard_normal((n, k)).astype(np.float32))
+    gate = np.array([[0, 1, 0, 0], [0, -1, 0, 0], [0, 0.5, 0, 0], [0, 0, 0, 0]], np.float32)
+    be = HipBackend(["moe_linear_gated_i8"])
+    bufs = [be.storage_init("xq", xq.view(np.float32).ravel()), be.storage_init("wq", wq.view(np.float32).ravel()),
+            be.storage_init("sx", sx), be.storage_init("sw", sw), be.storage_init("gate", gate.ravel())]
+    out = be.storage(m * n)
+    be.submit([], [be.step(be.kernel_index("moe_linear_gated_i8"), bufs + [out], [m, k // 4, n, ne, ei], m * n)])
+    got = be.read(out, m * n).reshape(m, n)
+    want = o.epilogue(o.acc_exact(xq, wq), sx, sw)
+    want[[1, 3]] = 0.0
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
