@@ -367,7 +367,8 @@ __device__ __forceinline__ void wait_ahead(int ahead) {
     else wait_vmcnt<0>();
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int DK, int OUT, bool HAS_BIAS, bool STATIC, bool SPLITK>
+template <int BM, int BN, int WM, int WN, int STAGES, int DK, int OUT, bool HAS_BIAS, bool STATIC, bool SPLITK,
+          bool ILV_ENABLE = false>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the LDS-DMA builtins exist only in the device pass
     using C = DmaCfg<BM, BN, WM, WN, STAGES, DK>;
@@ -468,6 +469,33 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
         __builtin_amdgcn_sched_group_barrier(0x008, C::FM * C::FN - (C::FM + C::FN), 0);
     };
 
+    // DMA interleave: LOADS/KSTEPS loads per k-step, one between every
+    // ILV_MF of the MFMAs that follow the fragment-read ones.
+    constexpr int ILV_PER_STEP = C::LOADS / C::KSTEPS;
+    constexpr int ILV_TAIL = C::FM * C::FN - (C::FM + C::FN);
+    constexpr int ILV_MF = ILV_PER_STEP > 0 ? ILV_TAIL / ILV_PER_STEP : 0;
+    constexpr bool ILV = ILV_ENABLE && C::LOADS % C::KSTEPS == 0 && ILV_PER_STEP > 0 && ILV_MF > 0 &&
+                         ILV_MF * ILV_PER_STEP == ILV_TAIL;
+    auto dma_one = [&](int idx, uint32_t base, int64_t koff) {
+        if (idx < C::A_LOADS) dma(asrc[idx] + koff, base + idx * C::NT * 16);
+        else dma(bsrc[idx - C::A_LOADS] + koff, base + C::A_BYTES + (idx - C::A_LOADS) * C::NT * 16);
+    };
+    auto mfma_range = [&](const v4i* fa_, const v4i* fb_, int q0, int cnt) {
+#pragma unroll
+        for (int q = 0; q < C::FM * C::FN; ++q) {
+            if (q < q0 || q >= q0 + cnt) continue;
+            const int i = q / C::FN, j = q % C::FN;
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb_[j], fa_[i], acc[i][j], 0, 0, 0);
+        }
+    };
+    auto interleave_reads = [&]() {
+#pragma unroll
+        for (int q = 0; q < C::FM + C::FN; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        }
+    };
+
     v4i fa[2][C::FM], fb[2][C::FN];
     if (nk > 0) {
         wait_ahead<C::LOADS>(min(nk - 1, STAGES - 2));
@@ -480,7 +508,12 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
         wait_ahead<C::LOADS>(min(nk - 2 - it, STAGES - 3));
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
-        if (it + STAGES - 1 < nk) issue(kt0 + it + STAGES - 1, (it + STAGES - 1) % STAGES);
+        const bool do_issue = it + STAGES - 1 < nk;
+        if constexpr (!ILV) {
+            if (do_issue) issue(kt0 + it + STAGES - 1, (it + STAGES - 1) % STAGES);
+        }
+        const uint32_t ibase = lds_base + ((it + STAGES - 1) % STAGES) * C::STAGE;
+        const int64_t ikoff = (int64_t)(kt0 + it + STAGES - 1) * DK;
         const uint8_t* A = lds + (it % STAGES) * C::STAGE;
         const uint8_t* An = lds + ((it + 1) % STAGES) * C::STAGE;
 #pragma unroll
@@ -490,8 +523,23 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
             // The last k-step reads the next stage's first fragments (on the
             // final iteration that buffer holds stale data that is never used).
             read_frags(ks + 1 < C::KSTEPS ? A : An, ks + 1 < C::KSTEPS ? ks + 1 : 0, fa[nxt], fb[nxt]);
-            mfma_step(fa[cur], fb[cur]);
-            interleave();
+            if constexpr (ILV) {
+                // The first FM+FN MFMAs carry the fragment reads; each DMA of
+                // the stage being refilled sits between two of the rest, so
+                // the matrix pipe stays busy while it issues.
+                mfma_range(fa[cur], fb[cur], 0, C::FM + C::FN);
+                interleave_reads();
+#pragma unroll
+                for (int d = 0; d < ILV_PER_STEP; ++d) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (do_issue) dma_one(ks * ILV_PER_STEP + d, ibase, ikoff);
+                    __builtin_amdgcn_sched_barrier(0);
+                    mfma_range(fa[cur], fb[cur], C::FM + C::FN + d * ILV_MF, ILV_MF);
+                }
+            } else {
+                mfma_step(fa[cur], fb[cur]);
+                interleave();
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
         if constexpr (C::KSTEPS % 2 == 1) {
@@ -747,18 +795,21 @@ static hipError_t go(hipStream_t s, bool aligned, const GemmArgs& a) {
     return hipGetLastError();
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int DK, int OUT, bool HAS_BIAS, bool STATIC, bool SPLITK>
+template <int BM, int BN, int WM, int WN, int STAGES, int DK, int OUT, bool HAS_BIAS, bool STATIC, bool SPLITK,
+          bool ILV = false>
 static hipError_t go_dma(hipStream_t s, const GemmArgs& a) {
     const long tiles = (long)((a.m + BM - 1) / BM) * ((a.n + BN - 1) / BN);
     const unsigned grid = (unsigned)(tiles * (SPLITK ? a.splits : 1));
-    gemm_i8_dma_kernel<BM, BN, WM, WN, STAGES, DK, OUT, HAS_BIAS, STATIC, SPLITK><<<grid, WM * WN * 64, 0, s>>>(a);
+    gemm_i8_dma_kernel<BM, BN, WM, WN, STAGES, DK, OUT, HAS_BIAS, STATIC, SPLITK, ILV><<<grid, WM * WN * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
 // Tuning knob for the large-tile DMA configuration (read once):
-// BH_GEMM_BIG=0: 256x256, 4 waves, DK=64, 4 stages (default)
+// BH_GEMM_BIG=0: 256x256, 4 waves, DK=64, 4 stages, DMA issue interleaved with the MFMAs (default)
 // BH_GEMM_BIG=1: 256x128, 4 waves (128x64 each), DK=128, 3 stages
 // BH_GEMM_BIG=2: 256x256, 8 waves (128x64 each), DK=64, 4 stages
+// BH_GEMM_BIG=3: the default without the DMA interleave (all of a stage's
+//                DMA issued after the barrier)
 static int big_cfg() {
     static int v = [] {
         const char* e = getenv("BH_GEMM_BIG");
@@ -776,7 +827,8 @@ static hipError_t go_cfg(hipStream_t s, bool aligned, bool dma, const TileChoice
             switch (big_cfg()) {
                 case 1: return go_dma<256, 128, 2, 2, 3, 128, OUT, HAS_BIAS, STATIC, false>(s, a);
                 case 2: return go_dma<256, 256, 2, 4, 4, 64, OUT, HAS_BIAS, STATIC, false>(s, a);
-                default: return go_dma<256, 256, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, false>(s, a);
+                case 3: return go_dma<256, 256, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, false, false>(s, a);
+                default: return go_dma<256, 256, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, false, true>(s, a);
             }
         }
         if (tc.splits > 1) return go_dma<128, 128, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, true>(s, a);
