@@ -343,32 +343,48 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     __shared__ float qs[MAX_GROUP * 256];
     __shared__ float es[MAX_GROUP * KCH];
     __shared__ float ml[MAX_GROUP * 2];
+    __shared__ float ksc[KCH], vsc[KCH];  // KV8: this chunk's per-key scales
     const int r = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z, tid = threadIdx.x;
     const int t = (int)p.pos[r] + 1;
     const int j0 = sp * KCH;
     if (j0 >= t) return;
     const int n = min(KCH, t - j0);
     const int G = p.nh / p.nkv;
-    for (int i = tid; i < G * p.hd; i += RT) qs[i] = p.q[(size_t)r * p.hq + (size_t)kh * G * p.hd + i];
-    __syncthreads();
     const size_t tok0 = (size_t)p.seq[r] * p.max_seq + j0;  // cache slot of this chunk's first key
+    for (int i = tid; i < G * p.hd; i += RT) qs[i] = p.q[(size_t)r * p.hq + (size_t)kh * G * p.hd + i];
+    if constexpr (KV8) {
+        if (tid < KCH) ksc[tid] = tid < n ? p.ks[(tok0 + tid) * p.nkv + kh] : 0.0f;
+        else if (tid < 2 * KCH) vsc[tid - KCH] = tid - KCH < n ? p.vs[(tok0 + tid - KCH) * p.nkv + kh] : 0.0f;
+    }
+    __syncthreads();
     const size_t base = (size_t)p.seq[r] * p.max_seq * p.hkv + (size_t)kh * p.hd;
     {
         const int kk = tid >> 3, l8 = tid & 7;
         float acc[MAX_GROUP];
 #pragma unroll
         for (int g = 0; g < MAX_GROUP; ++g) acc[g] = 0.0f;
-        if (kk < n) {
-            const size_t kro = base + (size_t)(j0 + kk) * p.hkv;
-            for (int c = l8 * 4; c < p.hd; c += 32) {
-                const float4 kv = KV8 ? i8x4(*reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.kc) + kro + c))
-                                      : *reinterpret_cast<const float4*>(static_cast<const float*>(p.kc) + kro + c);
+        // All of this lane's K pieces (head_dim <= 256: at most 8) are loaded
+        // before the first product.
+        constexpr int KP = 256 / 32;
+        float4 kv[KP];
+        const size_t kro = base + (size_t)(j0 + kk) * p.hkv;
 #pragma unroll
-                for (int g = 0; g < MAX_GROUP; ++g) {
-                    if (g >= G) break;
-                    const float4 qv = *reinterpret_cast<const float4*>(qs + g * p.hd + c);
-                    acc[g] += qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
-                }
+        for (int u = 0; u < KP; ++u) {
+            const int c = l8 * 4 + 32 * u;
+            kv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (kk < n && c < p.hd)
+                kv[u] = KV8 ? i8x4(*reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.kc) + kro + c))
+                            : *reinterpret_cast<const float4*>(static_cast<const float*>(p.kc) + kro + c);
+        }
+#pragma unroll
+        for (int u = 0; u < KP; ++u) {
+            const int c = l8 * 4 + 32 * u;
+            if (c >= p.hd) break;
+#pragma unroll
+            for (int g = 0; g < MAX_GROUP; ++g) {
+                if (g >= G) break;
+                const float4 qv = *reinterpret_cast<const float4*>(qs + g * p.hd + c);
+                acc[g] += qv.x * kv[u].x + qv.y * kv[u].y + qv.z * kv[u].z + qv.w * kv[u].w;
             }
         }
 #pragma unroll
@@ -378,7 +394,7 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
             v += __shfl_xor(v, 4, 64);
             v += __shfl_xor(v, 2, 64);
             v += __shfl_xor(v, 1, 64);
-            if (KV8 && kk < n) v = v * p.ks[(tok0 + kk) * p.nkv + kh];
+            if (KV8 && kk < n) v = v * ksc[kk];
             if (l8 == 0) es[g * KCH + kk] = v * p.scale;
         }
     }
@@ -410,8 +426,7 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
         if constexpr (KV8) {
             const int8_t* vb = reinterpret_cast<const int8_t*>(p.vc) + vbo;
 #pragma unroll 8
-            for (int k = 0; k < n; ++k)
-                acc += es[g * KCH + k] * (float)vb[(size_t)k * p.hkv + d] * p.vs[(tok0 + k) * p.nkv + kh];
+            for (int k = 0; k < n; ++k) acc += es[g * KCH + k] * (float)vb[(size_t)k * p.hkv + d] * vsc[k];
         } else {
             const float* vb = static_cast<const float*>(p.vc) + vbo;
 #pragma unroll 8
@@ -445,15 +460,36 @@ __global__ __launch_bounds__(RT) void attn_combine_quant_kernel(const float* par
         if (i >= q4) continue;
         const int e = i * 4, h = e / hd, d = e - h * hd;
         const size_t hs = ((size_t)r * nh + h) * splits;
+        // Loads in batches of SB splits, all issued before use (one memory
+        // round trip per batch rather than per split).
+        constexpr int SB = 8;
         float M = -INFINITY;
-        for (int s = 0; s < ns; ++s) M = fmaxf(M, part_ml[2 * (hs + s)]);
+        for (int s0 = 0; s0 < ns; s0 += SB) {
+            float mv[SB];
+#pragma unroll
+            for (int j = 0; j < SB; ++j) mv[j] = s0 + j < ns ? part_ml[2 * (hs + s0 + j)] : -INFINITY;
+#pragma unroll
+            for (int j = 0; j < SB; ++j) M = fmaxf(M, mv[j]);
+        }
         float L = 0.0f;
         float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int s = 0; s < ns; ++s) {
-            const float w = expf(part_ml[2 * (hs + s)] - M);
-            L += part_ml[2 * (hs + s) + 1] * w;
-            const float4 v = *reinterpret_cast<const float4*>(part_o + (hs + s) * hd + d);
-            o = make_float4(o.x + v.x * w, o.y + v.y * w, o.z + v.z * w, o.w + v.w * w);
+        for (int s0 = 0; s0 < ns; s0 += SB) {
+            float mv[SB], lv[SB];
+            float4 ov[SB];
+#pragma unroll
+            for (int j = 0; j < SB; ++j) {
+                const bool live = s0 + j < ns;
+                mv[j] = live ? part_ml[2 * (hs + s0 + j)] : -INFINITY;
+                lv[j] = live ? part_ml[2 * (hs + s0 + j) + 1] : 0.0f;
+                ov[j] = live ? *reinterpret_cast<const float4*>(part_o + (hs + s0 + j) * hd + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int j = 0; j < SB; ++j) {
+                if (s0 + j >= ns) continue;
+                const float w = expf(mv[j] - M);
+                L += lv[j] * w;
+                o = make_float4(o.x + ov[j].x * w, o.y + ov[j].y * w, o.z + ov[j].z * w, o.w + ov[j].w * w);
+            }
         }
         const float inv = 1.0f / L;
         y[g] = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
