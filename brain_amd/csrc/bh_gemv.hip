@@ -100,6 +100,20 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
         }
     };
 
+    // Epilogue operands fetched up front, off the critical path: the scale
+    // of every row (MT*4 per lane) and of this lane's column in each group.
+    float sxr[MT * 4], swc[CG];
+#pragma unroll
+    for (int ri = 0; ri < MT * 4; ++ri) {
+        const int row = 16 * (ri >> 2) + 4 * (lane >> 4) + (ri & 3);
+        sxr[ri] = (OUT != OUT_I32 && row < m) ? a.sx[row] : 0.0f;
+    }
+#pragma unroll
+    for (int c = 0; c < CG; ++c) {
+        const int col = (g0 + c) * 16 + (lane & 15);
+        swc[c] = (OUT != OUT_I32 && col < n) ? a.sw[col] : 0.0f;
+    }
+
     v4i acc[CG][MT];
 #pragma unroll
     for (int c = 0; c < CG; ++c)
@@ -140,7 +154,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
             if constexpr (OUT == OUT_I32) {
                 reinterpret_cast<int*>(a.out)[idx] = s;
             } else {
-                float v = dequant(s, a.sx[row], a.sw[col]);
+                float v = dequant(s, sxr[ri], swc[c]);
                 if constexpr (HAS_BIAS) v = v + a.bias[col];
                 if (a.gate && a.gate[(int64_t)row * a.gate_stride + a.gate_col] <= 0.0f) v = 0.0f;
                 store_out<OUT>(a.out, idx, v);
