@@ -42,7 +42,7 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on CPU-baseline work")
-    ap.add_argument("--only", default="", help="profiling aid: 'decode', 'prefill', 'qwen3', 'dit', 'w4a8' or 'copy' only")
+    ap.add_argument("--only", default="", help="profiling aid: 'decode', 'gemv', 'prefill', 'qwen3', 'dit', 'w4a8' or 'copy' only")
     ap.add_argument("--no-qwen3", action="store_true")
     ap.add_argument("--no-dit", action="store_true")
     ap.add_argument("--no-w4a8", action="store_true")
@@ -88,12 +88,19 @@ def check_sample(torch, s, out_dtype):
     assert (got == want).all(), f"bench correctness gate failed at m={s['m']} k={s['k']} n={s['n']}"
 
 
-def bench_decode(torch, lib, sets, steps, warmup):
+def bench_decode(torch, lib, sets, steps, warmup, gemv_only=False):
+    """The decode step (16 linears) and, separately, the GEMV kernel alone.
+    gemv_only: just the GEMV measurement (the workload profiles/ summarizes
+    with rocprofv3, so its kernel average matches roofline.avg_launch_us)."""
     from brain_amd._lib import BH_OUT_BF16, check
 
     def linear(s):
+        # bh_linear_i8: quantization fused into the GEMV where that is faster
+        # (small m*K, narrow N), else quantize_rows + GEMV.
         sp = torch.cuda.current_stream().cuda_stream
-        check(lib.bh_quantize_rows(sp, s["x"].data_ptr(), s["m"], s["k"], s["sx"].data_ptr(), s["xq"].data_ptr()))
+        check(lib.bh_linear_i8(sp, s["x"].data_ptr(), s["wq"].data_ptr(), s["sw"].data_ptr(), None,
+                               s["sx"].data_ptr(), s["xq"].data_ptr(), s["out"].data_ptr(), BH_OUT_BF16,
+                               s["m"], s["k"], s["n"]))
 
     def gemv(s):
         sp = torch.cuda.current_stream().cuda_stream
@@ -104,15 +111,25 @@ def bench_decode(torch, lib, sets, steps, warmup):
     def step():
         for s in sets:
             linear(s)
-            gemv(s)
 
+    if gemv_only:
+        for s in sets:
+            sp = torch.cuda.current_stream().cuda_stream
+            check(lib.bh_quantize_rows(sp, s["x"].data_ptr(), s["m"], s["k"], s["sx"].data_ptr(), s["xq"].data_ptr()))
+        step_ms = wall = 0.0
+    else:
+        step_ms, wall = timed_step(torch, step, sets, steps, warmup)
+    return gemv_measure(torch, sets, gemv, steps, step_ms, wall)
+
+
+def timed_step(torch, step, sets, steps, warmup):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     for s in sets:
         check_sample(torch, s, "bf16")
 
-    # One step = 32 launches; the step is captured once as a HIP graph so the
+    # One step = 16 linears (16-32 launches); captured once as a HIP graph so the
     # timed loop measures the GPU, not Python's launch rate.
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
@@ -139,6 +156,11 @@ def bench_decode(torch, lib, sets, steps, warmup):
     step_ms = e0.elapsed_time(e1) / steps
     for s in sets:
         check_sample(torch, s, "bf16")
+    return step_ms, wall
+
+
+def gemv_measure(torch, sets, gemv, steps, step_ms, wall):
+    stream = torch.cuda.current_stream()
 
     # GEMV kernel duration: the step's 16 GEMV launches alone (activations
     # already quantized) captured as a second graph and replayed; events on the
@@ -438,9 +460,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes": src.numel() * 4}))
         return
-    if args.only in ("", "decode"):
+    if args.only in ("", "decode", "gemv"):
         sets = make_decode_set(torch, dev, gen)
-        res["decode"] = bench_decode(torch, lib, sets, args.steps, args.warmup)
+        res["decode"] = bench_decode(torch, lib, sets, args.steps, args.warmup, gemv_only=args.only == "gemv")
         del sets
     if args.only in ("", "prefill") and not args.no_prefill:
         res["prefill"] = bench_prefill(torch, lib, dev, gen, args.prefill_reps)

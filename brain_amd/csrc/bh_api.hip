@@ -43,6 +43,9 @@ hipError_t launch_gemv_i8_gated(hipStream_t s, const uint32_t* xq, const uint32_
 hipError_t launch_gemm_i8_gated(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                                 const float* sw, const float* gate, int gate_stride, int gate_col, float* out, int m,
                                 int kg, int n);
+hipError_t launch_linear_i8_fused(hipStream_t s, const float* x, const uint32_t* wq, const float* sw,
+                                  const float* bias, float* sx_out, uint32_t* xq_out, void* out, int out_dtype, int m,
+                                  int kg, int n);
 hipError_t launch_gemv_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
                           const float* bias, void* out, int out_dtype, int m, int k, int n);
 hipError_t launch_gemm_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
@@ -339,6 +342,15 @@ int bh_matmul_i8_static(void* stream, const uint32_t* xq, const uint32_t* wq, fl
 int bh_linear_i8(void* stream, const float* x, const uint32_t* wq, const float* sw, const float* bias,
                  float* sx_scratch, uint32_t* xq_scratch, void* out, int out_dtype, uint32_t m, uint32_t k,
                  uint32_t n) {
+    // Decode rows on the GEMV: one launch that quantizes in its prologue
+    // (bit-identical scratch contents and outputs), when its shape rules allow.
+    if (m >= 1 && m <= 16 && k % 4 == 0 && k > 0 && n > 0 && x && wq && sw && out && sx_scratch && xq_scratch &&
+        (out_dtype == OUT_F32 || out_dtype == OUT_BF16) && !tuned_variant(m, n, k) && m <= (uint32_t)GEMV_MAX_ROWS) {
+        const hipError_t e = launch_linear_i8_fused((hipStream_t)stream, x, wq, sw, bias, sx_scratch, xq_scratch, out,
+                                                    out_dtype, (int)m, (int)(k / 4), (int)n);
+        if (e == hipSuccess) return BH_OK;
+        if (e != hipErrorNotSupported) return hip_status(e, "linear_i8 fused launch");
+    }
     int rc = bh_quantize_rows(stream, x, m, k, sx_scratch, xq_scratch);
     if (rc) return rc;
     return bh_matmul_i8(stream, xq_scratch, wq, sx_scratch, sw, bias, out, out_dtype, m, k / 4, n);

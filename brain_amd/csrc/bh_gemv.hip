@@ -41,10 +41,21 @@ struct GemvArgs {
     int m, kg, n;
     const float* gate;  // moe_linear_gated_i8 row gate (null: none): row r is +0 when gate[r*stride+col] <= 0
     int gate_stride, gate_col;
+    // XMODE 2 (quantization fused into the prologue): the f32 activation
+    // [m, K] and the caller's scratch, which workgroup 0 fills with the same
+    // sx [m] and xq [m, K/4] that bh_quantize_rows writes.
+    const float* x;
+    float* sx_out;
+    uint32_t* xq_out;
 };
 
-template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int KSPLIT, bool XLDS, int U, int CG, int NW = GV_WAVES>
+// XMODE: 0 = packed activation read from global memory, 1 = staged into
+// LDS first, 2 = quantized from f32 into LDS by the workgroup itself (each
+// wave quantizes whole rows: exact row max, sx = max(max,1e-8)/127, codes
+// clamp(rne(x * (1/sx))) -- bit-identical to bh_quantize_rows).
+template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int KSPLIT, int XMODE, int U, int CG, int NW = GV_WAVES>
 __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
+    constexpr bool XLDS = XMODE != 0;
     constexpr int SLOTS = NW / KSPLIT;  // wave slots per workgroup, each CG column groups
     extern __shared__ __attribute__((aligned(16))) uint8_t xs[];  // [MT*16][kbytes+16] when XLDS
     __shared__ int red[KSPLIT > 1 ? NW : 1][CG * MT * 4][64];
@@ -78,7 +89,48 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
 #pragma unroll
             for (int c = 0; c < CG; ++c) wf[u][c] = load_k16<ALIGNED>(wp[c], (ks + KSPLIT * u) * 64 + ksub, kbytes);
 
-    if constexpr (XLDS) {
+    float* sxs = reinterpret_cast<float*>(xs + MT * 16 * xstride);  // XMODE 2: row scales
+    if constexpr (XMODE == 2) {
+        // Each row is split across wpr = NW/m waves (1 when m >= NW): partial
+        // maxima meet in LDS, then every wave quantizes its share of the row.
+        __shared__ float pmax[NW];
+        const int k4 = kbytes >> 2;
+        const int wpr = m < NW ? NW / m : 1;
+        const int rows_per_round = NW / wpr;
+        const bool first = blockIdx.x == 0;
+        for (int r0 = 0; r0 < m; r0 += rows_per_round) {
+            const int r = r0 + wave / wpr, part = wave % wpr;
+            const float4* xr = reinterpret_cast<const float4*>(a.x + (int64_t)(r < m ? r : 0) * kbytes);
+            float mx = 0.0f;
+            if (r < m)
+                for (int c = part * 64 + lane; c < k4; c += wpr * 64) {
+                    const float4 v = xr[c];
+                    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+                }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+            if (lane == 0) pmax[wave] = mx;
+            __syncthreads();
+            if (r < m) {
+                float rm = pmax[(wave / wpr) * wpr];
+                for (int j = 1; j < wpr; ++j) rm = fmaxf(rm, pmax[(wave / wpr) * wpr + j]);
+                const float sxv = fmaxf(rm, 1e-8f) / 127.0f;
+                const float inv = 1.0f / sxv;
+                uint8_t* xr8 = xs + r * xstride;
+                for (int c = part * 64 + lane; c < k4; c += wpr * 64) {
+                    const uint32_t w = quant_word(xr[c], inv);
+                    *reinterpret_cast<uint32_t*>(xr8 + 4 * c) = w;
+                    if (first) a.xq_out[(int64_t)r * k4 + c] = w;
+                }
+                if (part == 0 && lane < 4) *reinterpret_cast<uint32_t*>(xr8 + kbytes + 4 * lane) = 0u;  // pad past K
+                if (part == 0 && lane == 0) {
+                    sxs[r] = sxv;
+                    if (first) a.sx_out[r] = sxv;
+                }
+            }
+            __syncthreads();  // pmax is reused by the next round
+        }
+    } else if constexpr (XLDS) {
         const int pieces = kbytes >> 4;
         const int total = MT * 16 * pieces;
         for (int p = threadIdx.x; p < total; p += NW * 64) {
@@ -92,7 +144,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
     auto xfrag = [&](int t, int kb) -> v4i {
         const int r = (lane & 15) + 16 * t;
         if constexpr (XLDS) {
-            if (kb >= kbytes) return v4i{0, 0, 0, 0};
+            if (kb >= kbytes || (XMODE == 2 && r >= m)) return v4i{0, 0, 0, 0};
             return *reinterpret_cast<const v4i*>(xs + r * xstride + kb);
         } else {
             if (r >= m) return v4i{0, 0, 0, 0};
@@ -106,7 +158,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
 #pragma unroll
     for (int ri = 0; ri < MT * 4; ++ri) {
         const int row = 16 * (ri >> 2) + 4 * (lane >> 4) + (ri & 3);
-        sxr[ri] = (OUT != OUT_I32 && row < m) ? a.sx[row] : 0.0f;
+        sxr[ri] = (OUT != OUT_I32 && row < m) ? (XMODE == 2 ? sxs[row] : a.sx[row]) : 0.0f;
     }
 #pragma unroll
     for (int c = 0; c < CG; ++c) {
@@ -196,13 +248,14 @@ static int gv_cfg() {
     return v;
 }
 
-template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int U, int CG, int KSPLIT = 4>
+template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int U, int CG, int KSPLIT = 4, int XMODE = 0>
 static hipError_t gv_go(hipStream_t s, const GemvArgs& a) {
     constexpr int NW = KSPLIT > GV_WAVES ? KSPLIT : GV_WAVES;  // waves per workgroup
     constexpr int per_wg = (NW / KSPLIT) * CG;
     const int ngroups = (a.n + 15) / 16;
     const int grid = (ngroups + per_wg - 1) / per_wg;
-    gemv_i8_kernel<MT, OUT, HAS_BIAS, ALIGNED, KSPLIT, false, U, CG, NW><<<grid, NW * 64, 0, s>>>(a);
+    const size_t lds = XMODE ? (size_t)MT * 16 * (a.kg * 4 + 16) + MT * 16 * 4 : 0;
+    gemv_i8_kernel<MT, OUT, HAS_BIAS, ALIGNED, KSPLIT, XMODE, U, CG, NW><<<grid, NW * 64, lds, s>>>(a);
     return hipGetLastError();
 }
 
@@ -235,6 +288,17 @@ static hipError_t gv_split(hipStream_t s, const GemvArgs& a) {
     return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 1>(s, a);
 }
 
+// Quantization fused into the GEMV (XMODE 2), same launch policy as gv_split.
+template <int MT, int OUT, bool HAS_BIAS>
+static hipError_t gv_fused(hipStream_t s, const GemvArgs& a) {
+    const int ngroups = (a.n + 15) / 16;
+    const int nchunks = (a.kg * 4 + 63) / 64;
+    (void)ngroups;
+    if (nchunks >= 32) return gv_go<MT, OUT, HAS_BIAS, true, 4, 1, 16, 2>(s, a);
+    if (nchunks >= 16) return gv_go<MT, OUT, HAS_BIAS, true, 4, 1, 8, 2>(s, a);
+    return gv_go<MT, OUT, HAS_BIAS, true, 4, 1, 4, 2>(s, a);
+}
+
 template <int MT, int OUT, bool HAS_BIAS>
 static hipError_t gv_align(hipStream_t s, bool aligned, const GemvArgs& a) {
     if (aligned) return gv_split<MT, OUT, HAS_BIAS, true>(s, a);
@@ -257,7 +321,7 @@ hipError_t launch_gemv_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n) {
     const bool aligned = ((kg * 4) % 16 == 0) && ((reinterpret_cast<uintptr_t>(xq) & 15u) == 0) &&
                          ((reinterpret_cast<uintptr_t>(wq) & 15u) == 0);
-    GemvArgs a{xq, wq, sx, sw, bias, out, m, kg, n, nullptr, 0, 0};
+    GemvArgs a{xq, wq, sx, sw, bias, out, m, kg, n, nullptr, 0, 0, nullptr, nullptr, nullptr};
     if (m <= 16) return gv_out<1>(s, aligned, out_dtype, a);
     return gv_out<2>(s, aligned, out_dtype, a);
 }
@@ -267,9 +331,32 @@ hipError_t launch_gemv_i8_gated(hipStream_t s, const uint32_t* xq, const uint32_
                                 int kg, int n) {
     const bool aligned = ((kg * 4) % 16 == 0) && ((reinterpret_cast<uintptr_t>(xq) & 15u) == 0) &&
                          ((reinterpret_cast<uintptr_t>(wq) & 15u) == 0);
-    GemvArgs a{xq, wq, sx, sw, nullptr, out, m, kg, n, gate, gate_stride, gate_col};
+    GemvArgs a{xq, wq, sx, sw, nullptr, out, m, kg, n, gate, gate_stride, gate_col, nullptr, nullptr, nullptr};
     if (m <= 16) return gv_out<1>(s, aligned, OUT_F32, a);
     return gv_out<2>(s, aligned, OUT_F32, a);
+}
+
+// Quantize + GEMV in one launch for m <= 16 (bh_linear_i8's decode path).
+// Needs K % 16 == 0, 16-byte aligned x / wq / scratch, and the LDS image of
+// 16 rows (16 * (K + 16) bytes) within 64 KB; returns hipErrorNotSupported
+// otherwise so the caller falls back to the two-launch path.
+hipError_t launch_linear_i8_fused(hipStream_t s, const float* x, const uint32_t* wq, const float* sw,
+                                  const float* bias, float* sx_out, uint32_t* xq_out, void* out, int out_dtype, int m,
+                                  int kg, int n) {
+    const int kbytes = kg * 4;
+    const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(wq) |
+                         reinterpret_cast<uintptr_t>(xq_out);
+    // Wide N (the LM head) keeps the separate quantization: thousands of
+    // workgroups would each re-read the f32 activation. So do larger
+    // activations (m*K > 12288): every workgroup re-quantizes all rows, which
+    // measured slower than one quantize launch from m*K = 16384 up.
+    if (m > 16 || kbytes % 16 != 0 || (al & 15u) != 0 || (size_t)16 * (kbytes + 16) + 64 > 64 * 1024 ||
+        (n + 15) / 16 >= 1024 || (int64_t)m * kbytes > 12288)
+        return hipErrorNotSupported;
+    GemvArgs a{xq_out, wq, sx_out, sw, bias, out, m, kg, n, nullptr, 0, 0, x, sx_out, xq_out};
+    if (out_dtype == OUT_I32) return gv_fused<1, OUT_I32, false>(s, a);
+    if (out_dtype == OUT_F32) return bias ? gv_fused<1, OUT_F32, true>(s, a) : gv_fused<1, OUT_F32, false>(s, a);
+    return bias ? gv_fused<1, OUT_BF16, true>(s, a) : gv_fused<1, OUT_BF16, false>(s, a);
 }
 
 }  // namespace bh

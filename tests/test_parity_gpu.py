@@ -244,6 +244,33 @@ def test_linear_config0(gpu):
     assert (o.cpu_linear_gemv(x, wq, sw, 4).view(np.uint32) == want.view(np.uint32)).all()
 
 
+@pytest.mark.parametrize("m", [1, 4, 8, 16])
+@pytest.mark.parametrize("k,n", [(1024, 3072), (3072, 1024), (1024, 2048), (1024, 151936), (32, 7), (2032, 40)])
+def test_linear_fused_quant(gpu, m, k, n):
+    """bh_linear_i8 on the decode path quantizes inside the GEMV: outputs (f32
+    and bf16 with bias) and the sx / xq scratch it leaves must be exactly the
+    two-launch results."""
+    x = special_acts(m, k, m + k)
+    wq, sw = o.synth_weights(n, k, 3)
+    bias = np.random.default_rng(k).standard_normal(n).astype(np.float32)
+    sx_ref = o.max_abs_row(x)
+    xq_ref = o.quant_pack(x, sx_ref)
+    rows = np.arange(m)
+    cols = np.arange(n) if n < 20000 else np.unique(np.r_[0, n - 1, np.random.default_rng(1).integers(0, n, 500)])
+    acc = o.acc_exact(xq_ref, wq, rows, cols)
+    sx_s = torch.empty(m, device=gpu)
+    xq_s = torch.empty(m, k // 4, device=gpu, dtype=torch.int32)
+    xd, wd, swd = dev_f32(x, gpu), dev_u32(wq, gpu), dev_f32(sw, gpu)
+    got = ops.linear_i8(xd, wd, swd, sx=sx_s, xq=xq_s).cpu().numpy()
+    assert (sx_s.cpu().numpy().view(np.uint32) == sx_ref.view(np.uint32)).all()
+    assert (host_u32(xq_s) == xq_ref).all()
+    want = o.epilogue(acc, sx_ref, sw[cols])
+    assert (got[:, cols].view(np.uint32) == want.view(np.uint32)).all()
+    gotb = bf16_bits(ops.linear_i8(xd, wd, swd, dev_f32(bias, gpu), torch.bfloat16))
+    wantb = o.epilogue(acc, sx_ref, sw[cols], bias[cols], "bf16")
+    assert (gotb[:, cols] == wantb).all()
+
+
 @pytest.mark.parametrize("n,k", [(1, 64), (3, 8), (17, 24), (64, 4096), (129, 128), (300, 1000)])
 def test_device_weight_quantizer(gpu, n, k):
     rng = np.random.default_rng(n + k)
