@@ -805,11 +805,13 @@ static hipError_t go_dma(hipStream_t s, const GemmArgs& a) {
 }
 
 // Tuning knob for the large-tile DMA configuration (read once):
-// BH_GEMM_BIG=0: 256x256, 4 waves, DK=64, 4 stages, DMA issue interleaved with the MFMAs (default)
+// BH_GEMM_BIG=0: 256x256, 8 waves (128x64 each: 2 waves per SIMD, 196 VGPRs),
+//                DK=64, 4 stages, DMA issue interleaved with the MFMAs (default;
+//                measured 5-10% above the 4-wave form on the large shapes)
 // BH_GEMM_BIG=1: 256x128, 4 waves (128x64 each), DK=128, 3 stages
-// BH_GEMM_BIG=2: 256x256, 8 waves (128x64 each), DK=64, 4 stages
-// BH_GEMM_BIG=3: the default without the DMA interleave (all of a stage's
-//                DMA issued after the barrier)
+// BH_GEMM_BIG=2: the default without the DMA interleave
+// BH_GEMM_BIG=3: 256x256, 4 waves (128x128 each), no interleave
+// BH_GEMM_BIG=4: 256x256, 4 waves (128x128 each), DMA interleave
 static int big_cfg() {
     static int v = [] {
         const char* e = getenv("BH_GEMM_BIG");
@@ -828,7 +830,8 @@ static hipError_t go_cfg(hipStream_t s, bool aligned, bool dma, const TileChoice
                 case 1: return go_dma<256, 128, 2, 2, 3, 128, OUT, HAS_BIAS, STATIC, false>(s, a);
                 case 2: return go_dma<256, 256, 2, 4, 4, 64, OUT, HAS_BIAS, STATIC, false>(s, a);
                 case 3: return go_dma<256, 256, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, false, false>(s, a);
-                default: return go_dma<256, 256, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, false, true>(s, a);
+                case 4: return go_dma<256, 256, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, false, true>(s, a);
+                default: return go_dma<256, 256, 2, 4, 4, 64, OUT, HAS_BIAS, STATIC, false, true>(s, a);
             }
         }
         if (tc.splits > 1) return go_dma<128, 128, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, true>(s, a);
