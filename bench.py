@@ -337,7 +337,7 @@ def qwen3_cpu_baseline(budget_s=8.0, ctx=128):
             "sample": f"{steps} greedy int8 decode steps at batch 1 after {ctx} cached positions, random int8 weights"}
 
 
-def bench_qwen3(prompt_len=128, gen=256, batches=(1, 8), cpu=True):
+def bench_qwen3(prompt_len=128, gen=256, batches=(1, 4, 8), cpu=True):
     """Qwen3-0.6B-architecture int8 decoder, random init, greedy.
     Prefill of a random-id prompt, then `gen` decode steps (one HIP graph
     replay each); tok/s = batch * gen / decode wall time."""

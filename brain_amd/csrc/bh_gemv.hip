@@ -47,6 +47,17 @@ struct GemvArgs {
     const float* x;
     float* sx_out;
     uint32_t* xq_out;
+    // XMODE 3 / 4 (the decoder's producers fused into the prologue):
+    //   3: x = pre_emb[pre_tok[r]] or pre_a[r] (+ pre_b[r]); workgroup 0 stores
+    //      x to res_out[r]; y = RMSNorm(x) * pre_w (eps); quantize y;
+    //   4: y = silu(g) * u over pre_a = [m, 2K] (gate | up); quantize y.
+    const uint32_t* pre_tok;
+    const float* pre_emb;
+    const float* pre_a;
+    const float* pre_b;
+    const float* pre_w;
+    float* res_out;
+    float eps;
 };
 
 // XMODE: 0 = packed activation read from global memory, 1 = staged into
@@ -89,8 +100,92 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
 #pragma unroll
             for (int c = 0; c < CG; ++c) wf[u][c] = load_k16<ALIGNED>(wp[c], (ks + KSPLIT * u) * 64 + ksub, kbytes);
 
-    float* sxs = reinterpret_cast<float*>(xs + MT * 16 * xstride);  // XMODE 2: row scales
-    if constexpr (XMODE == 2) {
+    float* sxs = reinterpret_cast<float*>(xs + MT * 16 * xstride);  // XMODE 2-4: row scales
+    if constexpr (XMODE == 3 || XMODE == 4) {
+        // Rows in groups of 256 threads (NW/4 rows per round). The sum of
+        // squares uses exactly the reduction of the decoder's separate
+        // norm_quant kernel -- thread t accumulates float4 groups t, t+256, ...
+        // in order, a wave xor-tree, then the 4 wave sums in order -- so the
+        // quantized rows are bit-identical to that kernel's.
+        static_assert(NW % 4 == 0, "row groups of 4 waves");
+        constexpr int NG = NW / 4, GMAX = 4;  // rows per round, float4 per thread (K <= 4096)
+        __shared__ float gred[NW];
+        const int grp = wave >> 2, gt = threadIdx.x & 255;
+        const int d = kbytes, d4 = d >> 2;
+        const bool first = blockIdx.x == 0;
+        for (int r0 = 0; r0 < m; r0 += NG) {
+            const int r = r0 + grp;
+            const bool live = r < m;
+            float4 v[GMAX];
+            float ss = 0.0f;
+#pragma unroll
+            for (int g = 0; g < GMAX; ++g) {
+                const int i = gt + 256 * g;
+                v[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (!live || i >= d4) continue;
+                if constexpr (XMODE == 3) {
+                    const float4* src = a.pre_tok ? reinterpret_cast<const float4*>(a.pre_emb + (size_t)a.pre_tok[r] * d)
+                                                  : reinterpret_cast<const float4*>(a.pre_a + (size_t)r * d);
+                    float4 x = src[i];
+                    if (a.pre_b) {
+                        const float4 b = reinterpret_cast<const float4*>(a.pre_b + (size_t)r * d)[i];
+                        x = make_float4(x.x + b.x, x.y + b.y, x.z + b.z, x.w + b.w);
+                    }
+                    v[g] = x;
+                    ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+                    if (first) reinterpret_cast<float4*>(a.res_out + (size_t)r * d)[i] = x;
+                } else {
+                    const float4 gv = reinterpret_cast<const float4*>(a.pre_a + (size_t)r * 2 * d)[i];
+                    const float4 uv = reinterpret_cast<const float4*>(a.pre_a + (size_t)r * 2 * d + d)[i];
+                    v[g] = make_float4(gv.x / (1.0f + expf(-gv.x)) * uv.x, gv.y / (1.0f + expf(-gv.y)) * uv.y,
+                                       gv.z / (1.0f + expf(-gv.z)) * uv.z, gv.w / (1.0f + expf(-gv.w)) * uv.w);
+                }
+            }
+            if constexpr (XMODE == 3) {
+#pragma unroll
+                for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+                if (lane == 0) gred[wave] = ss;
+                __syncthreads();
+                float tot = gred[grp * 4];
+#pragma unroll
+                for (int w = 1; w < 4; ++w) tot += gred[grp * 4 + w];
+                const float inv = 1.0f / sqrtf(tot / (float)d + a.eps);
+                const float4* w4 = reinterpret_cast<const float4*>(a.pre_w);
+#pragma unroll
+                for (int g = 0; g < GMAX; ++g) {
+                    const int i = gt + 256 * g;
+                    if (!live || i >= d4) continue;
+                    const float4 wv = w4[i];
+                    v[g] = make_float4(v[g].x * inv * wv.x, v[g].y * inv * wv.y, v[g].z * inv * wv.z, v[g].w * inv * wv.w);
+                }
+                __syncthreads();  // gred is reused for the max
+            }
+            float am = 0.0f;
+#pragma unroll
+            for (int g = 0; g < GMAX; ++g)
+                am = fmaxf(am, fmaxf(fmaxf(fabsf(v[g].x), fabsf(v[g].y)), fmaxf(fabsf(v[g].z), fabsf(v[g].w))));
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+            if (lane == 0) gred[wave] = am;
+            __syncthreads();
+            if (live) {
+                float rm = gred[grp * 4];
+#pragma unroll
+                for (int w = 1; w < 4; ++w) rm = fmaxf(rm, gred[grp * 4 + w]);
+                const float sxv = fmaxf(rm, 1e-8f) / 127.0f;
+                const float invq = 1.0f / sxv;
+                uint8_t* xr8 = xs + r * xstride;
+#pragma unroll
+                for (int g = 0; g < GMAX; ++g) {
+                    const int i = gt + 256 * g;
+                    if (i < d4) *reinterpret_cast<uint32_t*>(xr8 + 4 * i) = quant_word(v[g], invq);
+                }
+                if (gt < 4) *reinterpret_cast<uint32_t*>(xr8 + d + 4 * gt) = 0u;  // pad past K
+                if (gt == 0) sxs[r] = sxv;
+            }
+            __syncthreads();  // gred is reused by the next round
+        }
+    } else if constexpr (XMODE == 2) {
         // Each row is split across wpr = NW/m waves (1 when m >= NW): partial
         // maxima meet in LDS, then every wave quantizes its share of the row.
         __shared__ float pmax[NW];
@@ -144,7 +239,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
     auto xfrag = [&](int t, int kb) -> v4i {
         const int r = (lane & 15) + 16 * t;
         if constexpr (XLDS) {
-            if (kb >= kbytes || (XMODE == 2 && r >= m)) return v4i{0, 0, 0, 0};
+            if (kb >= kbytes || (XMODE >= 2 && r >= m)) return v4i{0, 0, 0, 0};
             return *reinterpret_cast<const v4i*>(xs + r * xstride + kb);
         } else {
             if (r >= m) return v4i{0, 0, 0, 0};
@@ -158,7 +253,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
 #pragma unroll
     for (int ri = 0; ri < MT * 4; ++ri) {
         const int row = 16 * (ri >> 2) + 4 * (lane >> 4) + (ri & 3);
-        sxr[ri] = (OUT != OUT_I32 && row < m) ? (XMODE == 2 ? sxs[row] : a.sx[row]) : 0.0f;
+        sxr[ri] = (OUT != OUT_I32 && row < m) ? (XMODE >= 2 ? sxs[row] : a.sx[row]) : 0.0f;
     }
 #pragma unroll
     for (int c = 0; c < CG; ++c) {
@@ -321,7 +416,8 @@ hipError_t launch_gemv_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n) {
     const bool aligned = ((kg * 4) % 16 == 0) && ((reinterpret_cast<uintptr_t>(xq) & 15u) == 0) &&
                          ((reinterpret_cast<uintptr_t>(wq) & 15u) == 0);
-    GemvArgs a{xq, wq, sx, sw, bias, out, m, kg, n, nullptr, 0, 0, nullptr, nullptr, nullptr};
+    GemvArgs a{xq, wq, sx, sw, bias, out, m, kg, n, nullptr, 0, 0, nullptr, nullptr, nullptr,
+               nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0.0f};
     if (m <= 16) return gv_out<1>(s, aligned, out_dtype, a);
     return gv_out<2>(s, aligned, out_dtype, a);
 }
@@ -331,7 +427,8 @@ hipError_t launch_gemv_i8_gated(hipStream_t s, const uint32_t* xq, const uint32_
                                 int kg, int n) {
     const bool aligned = ((kg * 4) % 16 == 0) && ((reinterpret_cast<uintptr_t>(xq) & 15u) == 0) &&
                          ((reinterpret_cast<uintptr_t>(wq) & 15u) == 0);
-    GemvArgs a{xq, wq, sx, sw, nullptr, out, m, kg, n, gate, gate_stride, gate_col, nullptr, nullptr, nullptr};
+    GemvArgs a{xq, wq, sx, sw, nullptr, out, m, kg, n, gate, gate_stride, gate_col, nullptr, nullptr, nullptr,
+               nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0.0f};
     if (m <= 16) return gv_out<1>(s, aligned, OUT_F32, a);
     return gv_out<2>(s, aligned, OUT_F32, a);
 }
@@ -353,10 +450,32 @@ hipError_t launch_linear_i8_fused(hipStream_t s, const float* x, const uint32_t*
     if (m > 16 || kbytes % 16 != 0 || (al & 15u) != 0 || (size_t)16 * (kbytes + 16) + 64 > 64 * 1024 ||
         (n + 15) / 16 >= 1024 || (int64_t)m * kbytes > 12288)
         return hipErrorNotSupported;
-    GemvArgs a{xq_out, wq, sx_out, sw, bias, out, m, kg, n, nullptr, 0, 0, x, sx_out, xq_out};
+    GemvArgs a{xq_out, wq, sx_out, sw, bias, out, m, kg, n, nullptr, 0, 0, x, sx_out, xq_out,
+               nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0.0f};
     if (out_dtype == OUT_I32) return gv_fused<1, OUT_I32, false>(s, a);
     if (out_dtype == OUT_F32) return bias ? gv_fused<1, OUT_F32, true>(s, a) : gv_fused<1, OUT_F32, false>(s, a);
     return bias ? gv_fused<1, OUT_BF16, true>(s, a) : gv_fused<1, OUT_BF16, false>(s, a);
+}
+
+// The decoder's fused producer + linear for m <= 16 rows, f32 out:
+// mode 3 = [residual add |] RMSNorm + quantize + GEMV, mode 4 = SwiGLU +
+// quantize + GEMV (K = the SwiGLU width, pre_a = [m, 2K]). K % 16 == 0,
+// K <= 4096. Returns hipErrorNotSupported outside those limits.
+hipError_t launch_gemv_i8_pre(hipStream_t s, int mode, const uint32_t* pre_tok, const float* pre_emb,
+                              const float* pre_a, const float* pre_b, const float* pre_w, float* res_out, float eps,
+                              const uint32_t* wq, const float* sw, float* out, int m, int kg, int n) {
+    const int kbytes = kg * 4;
+    if (m < 1 || m > 16 || kbytes % 16 != 0 || kbytes > 4096 || (reinterpret_cast<uintptr_t>(wq) & 15u) != 0)
+        return hipErrorNotSupported;
+    GemvArgs a{nullptr, wq, nullptr, sw, nullptr, out, m, kg, n, nullptr, 0, 0, nullptr, nullptr, nullptr,
+               pre_tok, pre_emb, pre_a, pre_b, pre_w, res_out, eps};
+    const int nchunks = (kbytes + 63) / 64;
+    if (mode == 3) {
+        if (nchunks >= 32) return gv_go<1, OUT_F32, false, true, 4, 1, 16, 3>(s, a);
+        return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3>(s, a);
+    }
+    if (nchunks >= 32) return gv_go<1, OUT_F32, false, true, 4, 1, 16, 4>(s, a);
+    return gv_go<1, OUT_F32, false, true, 4, 1, 8, 4>(s, a);
 }
 
 }  // namespace bh

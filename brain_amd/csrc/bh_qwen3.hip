@@ -38,6 +38,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../include/brain_hip.h"
@@ -51,6 +52,9 @@ hipError_t launch_gemv_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n);
 hipError_t launch_gemm_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n);
+hipError_t launch_gemv_i8_pre(hipStream_t s, int mode, const uint32_t* pre_tok, const float* pre_emb,
+                              const float* pre_a, const float* pre_b, const float* pre_w, float* res_out, float eps,
+                              const uint32_t* wq, const float* sw, float* out, int m, int kg, int n);
 
 int tuned_variant(uint32_t m, uint32_t n, uint32_t k);
 
@@ -621,7 +625,7 @@ struct bh_qwen3 {
     size_t layer_kv = 0;  // elements per layer per cache
     size_t kv_elem = 4;   // bytes per cache element
 
-    float *res = nullptr, *qkv = nullptr, *q = nullptr, *proj = nullptr, *gu = nullptr;
+    float *res = nullptr, *res2 = nullptr, *qkv = nullptr, *q = nullptr, *proj = nullptr, *gu = nullptr;
     float *part_o = nullptr, *part_ml = nullptr;  // attention chunk partials
     uint32_t max_splits = 0;
     const uint32_t* cur_pos = nullptr;
@@ -715,6 +719,16 @@ int launch_combine_quant(bh_qwen3* e, int rows, int splits) {
     return BH_OK;
 }
 
+// The fused producer + GEMV path: at most 4 rows (every workgroup redoes the
+// producer for all rows; at batch 8 that measured 19% slower than the
+// separate kernels, at batch 1 10% faster), K a multiple of 16 up to 4096,
+// and no measured preference for the MFMA tile at this shape.
+bool fused_ok(bh_qwen3* e, int rows, int k, int n) {
+    (void)e;
+    if (rows < 1 || rows > 4 || k % 16 != 0 || k > 4096) return false;
+    return tuned_variant((uint32_t)rows, (uint32_t)n, (uint32_t)k) != BH_VARIANT_PACKED_INT8;
+}
+
 // `splits`: key chunks of KCH covering the longest row of this launch (the
 // workspace stride; chunks past a row's position exit immediately).
 int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, const uint32_t* seq, int n_out,
@@ -722,6 +736,8 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
     e->cur_pos = pos;
     const bh_qwen3_config& c = e->c;
     const int d = (int)c.d_model, ff = (int)c.d_ff, hd = (int)c.head_dim;
+    float* cur = e->res;
+    float* nxt = e->res2;
     const int nh = (int)c.n_heads, nkv = (int)c.n_kv_heads;
     const float scale = 1.0f / sqrtf((float)hd);
     for (uint32_t l = 0; l < c.n_layers; ++l) {
@@ -731,23 +747,35 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
         const size_t lsc = (size_t)l * e->max_batch * e->max_seq * nkv;
         float* ksl = e->c.kv_int8 ? e->kscale + lsc : nullptr;
         float* vsl = e->c.kv_int8 ? e->vscale + lsc : nullptr;
-        NormQuantArgs na{};
-        if (l == 0) {
-            na.tok = tok;
-            na.emb = e->emb;
+        // Residual stream ping-pongs between res and res2 (two swaps per
+        // layer): a fused producer's workgroup 0 writes the new residual while
+        // other workgroups still read the old one.
+        const bool fuse = fused_ok(e, rows, d, (int)e->W) && fused_ok(e, rows, d, 2 * ff) && fused_ok(e, rows, ff, d);
+        if (fuse) {
+            BH_HIP(launch_gemv_i8_pre(e->stream, 3, l == 0 ? tok : nullptr, e->emb, l == 0 ? nullptr : cur,
+                                      l == 0 ? nullptr : e->proj, Ly.ln1, nxt, c.rms_eps, Ly.wqkv, Ly.sqkv, e->qkv,
+                                      rows, d / 4, (int)e->W),
+                   "fused norm + qkv launch");
         } else {
-            na.a = e->res;
-            na.b = e->proj;  // previous layer's down projection
+            NormQuantArgs na{};
+            if (l == 0) {
+                na.tok = tok;
+                na.emb = e->emb;
+            } else {
+                na.a = cur;
+                na.b = e->proj;  // previous layer's down projection
+            }
+            na.res_out = nxt;
+            na.w = Ly.ln1;
+            na.eps = c.rms_eps;
+            na.d = d;
+            na.sx = e->sx;
+            na.xq = e->xq;
+            na.xq_words = d / 4;
+            BH_TRY(launch_norm_quant(e, na, rows));
+            BH_TRY(launch_linear(e, Ly.wqkv, Ly.sqkv, e->qkv, rows, d, (int)e->W));
         }
-        na.res_out = e->res;
-        na.w = Ly.ln1;
-        na.eps = c.rms_eps;
-        na.d = d;
-        na.sx = e->sx;
-        na.xq = e->xq;
-        na.xq_words = d / 4;
-        BH_TRY(launch_norm_quant(e, na, rows));
-        BH_TRY(launch_linear(e, Ly.wqkv, Ly.sqkv, e->qkv, rows, d, (int)e->W));
+        std::swap(cur, nxt);
         RopeArgs ra{e->qkv, e->q, kc, vc, ksl, vsl, e->kclip + (size_t)l * nkv, e->vclip + (size_t)l * nkv, Ly.qn,
                     Ly.kn, pos, seq, nh, nkv, hd, (int)e->hq, (int)e->hkv, (int)e->max_seq, (int)c.qk_norm,
                     c.rms_eps, c.rope_theta};
@@ -761,24 +789,35 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
         BH_HIP(hipGetLastError(), "attention launch");
         BH_TRY(launch_combine_quant(e, rows, splits));
         BH_TRY(launch_linear(e, Ly.wo, Ly.so, e->proj, rows, (int)e->hq, d));
-        NormQuantArgs nb{};
-        nb.a = e->res;
-        nb.b = e->proj;
-        nb.res_out = e->res;
-        nb.w = Ly.ln2;
-        nb.eps = c.rms_eps;
-        nb.d = d;
-        nb.sx = e->sx;
-        nb.xq = e->xq;
-        nb.xq_words = d / 4;
-        BH_TRY(launch_norm_quant(e, nb, rows));
-        BH_TRY(launch_linear(e, Ly.wgu, Ly.sgu, e->gu, rows, d, 2 * ff));
-        BH_TRY(launch_swiglu_quant(e, rows));
-        BH_TRY(launch_linear(e, Ly.wdown, Ly.sdown, e->proj, rows, ff, d));
+        if (fuse) {
+            BH_HIP(launch_gemv_i8_pre(e->stream, 3, nullptr, nullptr, cur, e->proj, Ly.ln2, nxt, c.rms_eps, Ly.wgu,
+                                      Ly.sgu, e->gu, rows, d / 4, 2 * ff),
+                   "fused norm + gate/up launch");
+            std::swap(cur, nxt);
+            BH_HIP(launch_gemv_i8_pre(e->stream, 4, nullptr, nullptr, e->gu, nullptr, nullptr, nullptr, 0.0f, Ly.wdown,
+                                      Ly.sdown, e->proj, rows, ff / 4, d),
+                   "fused swiglu + down launch");
+        } else {
+            NormQuantArgs nb{};
+            nb.a = cur;
+            nb.b = e->proj;
+            nb.res_out = nxt;
+            nb.w = Ly.ln2;
+            nb.eps = c.rms_eps;
+            nb.d = d;
+            nb.sx = e->sx;
+            nb.xq = e->xq;
+            nb.xq_words = d / 4;
+            BH_TRY(launch_norm_quant(e, nb, rows));
+            std::swap(cur, nxt);
+            BH_TRY(launch_linear(e, Ly.wgu, Ly.sgu, e->gu, rows, d, 2 * ff));
+            BH_TRY(launch_swiglu_quant(e, rows));
+            BH_TRY(launch_linear(e, Ly.wdown, Ly.sdown, e->proj, rows, ff, d));
+        }
     }
     if (n_out <= 0) return BH_OK;
     NormQuantArgs nf{};
-    nf.a = e->res;
+    nf.a = cur;
     nf.b = e->proj;
     nf.row_map = out_map;
     nf.w = e->norm;
@@ -960,7 +999,7 @@ int bh_qwen3_create(const bh_qwen3_config* cfg, uint32_t max_batch, uint32_t max
         (rc = dalloc(e, &e->vscale, c.kv_int8 ? (uint64_t)c.n_layers * max_batch * max_seq * c.n_kv_heads : 1)) ||
         (rc = dalloc(e, &e->kclip, (uint64_t)c.n_layers * c.n_kv_heads)) ||
         (rc = dalloc(e, &e->vclip, (uint64_t)c.n_layers * c.n_kv_heads)) ||
-        (rc = dalloc(e, &e->res, R * d)) || (rc = dalloc(e, &e->qkv, R * e->W)) || (rc = dalloc(e, &e->q, R * hq)) ||
+        (rc = dalloc(e, &e->res, R * d)) || (rc = dalloc(e, &e->res2, R * d)) || (rc = dalloc(e, &e->qkv, R * e->W)) || (rc = dalloc(e, &e->q, R * hq)) ||
         (rc = dalloc(e, &e->part_o, R * c.n_heads * e->max_splits * c.head_dim)) || (rc = dalloc(e, &e->part_ml, R * c.n_heads * e->max_splits * 2)) || (rc = dalloc(e, &e->proj, R * d)) || (rc = dalloc(e, &e->gu, R * 2 * ff)) ||
         (rc = dalloc(e, &e->sx, R)) || (rc = dalloc(e, &e->xq, R * e->xq_words)) ||
         (rc = dalloc(e, &e->logits, (uint64_t)max_batch * c.vocab)) || (rc = dalloc(e, &e->tmpw, e->tmpw_floats)) ||
