@@ -36,7 +36,7 @@ hipError_t launch_gemm_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
 hipError_t launch_gemm_i8_static(hipStream_t s, const uint32_t* xq, const uint32_t* wq, float ssx, float ssw,
                                  float* out, int m, int kg, int n);
 
-size_t gemm_workspace_ints(int m, int kg, int n, size_t* counters);
+size_t gemm_workspace_ints(int m, int kg, int n);
 hipError_t launch_gemv_i8_gated(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                                 const float* sw, const float* gate, int gate_stride, int gate_col, float* out, int m,
                                 int kg, int n);
@@ -51,57 +51,46 @@ hipError_t launch_gemv_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
 hipError_t launch_gemm_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int k, int n);
 
-// Split-K workspace, one per (device, stream): i32 sums plus per-tile arrival
-// counters. Zeroed once when (re)allocated; every kernel that uses it leaves
-// it zeroed again, so no per-call clear is needed. Calls on one stream are
-// ordered, so they never share it concurrently.
+// Split-K workspace, one per (device, stream): the S partial slabs of a
+// split GEMM. Every split kernel overwrites the slabs it uses before the
+// reduction reads them, so the buffer is never cleared. Calls on one stream
+// are ordered, so they never share it concurrently.
 struct SplitWs {
     int device;
     hipStream_t stream;
     int* ws;
     size_t ints;
-    int* counters;
-    size_t ncounters;
 };
 static std::mutex g_ws_mu;
 static std::vector<SplitWs> g_ws;
-thread_local hipStream_t g_cur_stream = nullptr;
 
-int* splitk_workspace(size_t ints, size_t counters, int** counters_out, hipError_t* err) {
+int* splitk_workspace(hipStream_t st, size_t ints, hipError_t* err) {
     int dev = 0;
     *err = hipGetDevice(&dev);
     if (*err != hipSuccess) return nullptr;
-    const hipStream_t st = g_cur_stream;  // bound by the C-ABI launcher on this thread
     std::lock_guard<std::mutex> g(g_ws_mu);
     SplitWs* w = nullptr;
     for (auto& x : g_ws)
         if (x.device == dev && x.stream == st) w = &x;
     if (!w) {
-        g_ws.push_back(SplitWs{dev, st, nullptr, 0, nullptr, 0});
+        g_ws.push_back(SplitWs{dev, st, nullptr, 0});
         w = &g_ws.back();
     }
-    if (w->ints < ints || w->ncounters < counters) {
+    if (w->ints < ints) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (st && hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+        if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
             // No allocation inside a capture: the caller reserves beforehand.
             *err = hipErrorStreamCaptureUnsupported;
             return nullptr;
         }
-        // Growing: wait for this stream's queued users of the old buffers.
+        // Growing: wait for this stream's queued users of the old buffer.
         if ((*err = hipStreamSynchronize(st)) != hipSuccess) return nullptr;
         if (w->ws) (void)hipFree(w->ws);
-        if (w->counters) (void)hipFree(w->counters);
         w->ws = nullptr;
-        w->counters = nullptr;
-        w->ints = std::max(ints, w->ints);
-        w->ncounters = std::max(counters, w->ncounters);
-        if ((*err = hipMalloc(&w->ws, w->ints * 4)) != hipSuccess) { w->ints = 0; return nullptr; }
-        if ((*err = hipMalloc(&w->counters, w->ncounters * 4)) != hipSuccess) { w->ncounters = 0; return nullptr; }
-        if ((*err = hipMemset(w->ws, 0, w->ints * 4)) != hipSuccess) return nullptr;
-        if ((*err = hipMemset(w->counters, 0, w->ncounters * 4)) != hipSuccess) return nullptr;
-        if ((*err = hipDeviceSynchronize()) != hipSuccess) return nullptr;
+        w->ints = 0;
+        if ((*err = hipMalloc(&w->ws, ints * 4)) != hipSuccess) return nullptr;
+        w->ints = ints;
     }
-    *counters_out = w->counters;
     return w->ws;
 }
 
@@ -173,6 +162,11 @@ int fail(int code, const char* fmt, ...) {
 
 static int hip_status(hipError_t e, const char* what) {
     if (e == hipSuccess) return BH_OK;
+    if (e == hipErrorStreamCaptureUnsupported)
+        return fail(BH_ERR_INVALID,
+                    "%s: this shape needs the split-K workspace, which cannot be allocated while the stream is "
+                    "capturing; call bh_reserve_workspace on this stream first",
+                    what);
     return fail(BH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
@@ -270,7 +264,6 @@ int bh_matmul_i8_dyn(void* stream, const uint32_t* xq, const uint32_t* wq, const
     if (m == 0 || n == 0) return BH_OK;
     const uint64_t tiles = (((uint64_t)m + 127) / 128) * (((uint64_t)n + 127) / 128);
     if (tiles > I32MAX) return fail(BH_ERR_INVALID, "bh_matmul_i8_dyn: %llu tiles", (unsigned long long)tiles);
-    g_cur_stream = (hipStream_t)stream;
     hipError_t e = launch_gemm_i8((hipStream_t)stream, xq, wq, sx, sw, bias, out, out_dtype, (int)m, (int)kg, (int)n);
     if (e == hipErrorStreamCaptureUnsupported)
         return fail(BH_ERR_INVALID,
@@ -283,13 +276,10 @@ int bh_matmul_i8_dyn(void* stream, const uint32_t* xq, const uint32_t* wq, const
 int bh_reserve_workspace(void* stream, uint32_t m, uint32_t kg, uint32_t n) {
     if ((uint64_t)kg * 4 > I32MAX || m > I32MAX || n > I32MAX)
         return fail(BH_ERR_INVALID, "bh_reserve_workspace: m=%u kg=%u n=%u out of range", m, kg, n);
-    size_t nc = 0;
-    const size_t ints = gemm_workspace_ints((int)m, (int)kg, (int)n, &nc);
+    const size_t ints = gemm_workspace_ints((int)m, (int)kg, (int)n);
     if (!ints) return BH_OK;
-    g_cur_stream = (hipStream_t)stream;
     hipError_t err = hipSuccess;
-    int* counters = nullptr;
-    if (!splitk_workspace(ints, nc, &counters, &err)) {
+    if (!splitk_workspace((hipStream_t)stream, ints, &err)) {
         if (err == hipErrorStreamCaptureUnsupported)
             return fail(BH_ERR_INVALID, "bh_reserve_workspace: stream is capturing; reserve before capture");
         return fail(err == hipErrorOutOfMemory ? BH_ERR_NOMEM : BH_ERR_HIP, "bh_reserve_workspace: %s",

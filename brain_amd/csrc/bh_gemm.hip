@@ -16,11 +16,13 @@
 // 16 distinct 16-byte slots of a 256-byte bank line. This register-staged
 // kernel is the fallback for K % 128 != 0 or unaligned operands.
 //
-// Split-K (SPLITK): S workgroups share one output tile, each summing a slice of
-// K; partial sums are added with i32 atomics into a workspace (exact, so the
-// order does not matter); the last workgroup of a tile (per-tile arrival
-// counter) applies the epilogue and returns the workspace tile and its
-// counter to zero, so the workspace is always clean between calls.
+// Split-K (SPLITK), for shapes with too few output tiles to fill 256 CUs: S
+// workgroups share one output tile, each summing a contiguous slice of K and
+// storing its raw i32 partial tile into its own slab ws[split][m][n] (plain
+// stores, no atomics, nothing to clear). A second kernel adds the S slabs in
+// i32 (exact: integer addition in any order gives the same sum) and applies
+// the epilogue, so the output is bit-identical to the unsplit kernel's.
+#include <algorithm>
 #include <cstdlib>
 
 #include "bh_common.h"
@@ -74,8 +76,7 @@ struct GemmArgs {
     int m, kg, n;
     float ssx, ssw;   // STATIC scales
     int splits;       // S (1 = no split)
-    int* ws;          // [m*n] i32 split-K workspace (zero between calls)
-    int* counters;    // [tiles] arrival counters (zero between calls)
+    int* ws;          // [S][m][n] i32 split-K partials
     // Row gate of moe_linear_gated_i8.wgsl (null: none): row r of the output
     // is +0 when gate[r * gate_stride + gate_col] <= 0.
     const float* gate;
@@ -233,46 +234,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_kernel(GemmArgs a) {
     const int rbase = row0 + wm * C::WTM + 4 * (lane >> 5);
     const int cbase = col0 + wn * C::WTN + (lane & 31);
 
-    if constexpr (SPLITK) {
-        if (S > 1) {
-#pragma unroll
-            for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int row = rbase + i * 32 + 8 * (e >> 2) + (e & 3);
-                    if (row >= m) continue;
-#pragma unroll
-                    for (int j = 0; j < C::FN; ++j) {
-                        const int col = cbase + j * 32;
-                        if (col < n) atomicAdd(&a.ws[(int64_t)row * n + col], acc[i][j][e]);
-                    }
-                }
-            __threadfence();
-            __syncthreads();
-            __shared__ int last;
-            if (t == 0) last = (atomicAdd(&a.counters[tile_id], 1) == S - 1);
-            __syncthreads();
-            if (!last) return;
-            __threadfence();
-            // Last arrival: read the complete sums back, clear the tile.
-#pragma unroll
-            for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int row = rbase + i * 32 + 8 * (e >> 2) + (e & 3);
-                    if (row >= m) continue;
-#pragma unroll
-                    for (int j = 0; j < C::FN; ++j) {
-                        const int col = cbase + j * 32;
-                        if (col >= n) continue;
-                        int* p = &a.ws[(int64_t)row * n + col];
-                        acc[i][j][e] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        *p = 0;
-                    }
-                }
-            if (t == 0) a.counters[tile_id] = 0;
-        }
-    }
+    // Split-K: this workgroup's partial sums go raw to its own slab of the
+    // workspace (the kernel is instantiated with OUT_I32 for it).
+    if constexpr (SPLITK)
+        if (S > 1) a.out = a.ws + (int64_t)split * m * n;
 
     float swv[C::FN], bv[C::FN];
 #pragma unroll
@@ -357,14 +322,19 @@ struct DmaCfg {
     static_assert(STAGES >= 3, "the next stage's first k-step is read during this one");
 };
 
-template <int N>
+// Wait until at most `ahead` stages (N loads each) remain in flight;
+// MAXA is the largest `ahead` the caller passes.
+template <int N, int MAXA>
 __device__ __forceinline__ void wait_ahead(int ahead) {
-    // Wait until at most `ahead` stages (N loads each) remain in flight.
-    if constexpr (N * 2 < 64) {
-        if (ahead >= 2) { wait_vmcnt<2 * N>(); return; }
+    if constexpr (MAXA > 0) {
+        if (ahead >= MAXA) {
+            wait_vmcnt<MAXA * N>();
+            return;
+        }
+        wait_ahead<N, MAXA - 1>(ahead);
+    } else {
+        wait_vmcnt<0>();
     }
-    if (ahead >= 1) wait_vmcnt<N>();
-    else wait_vmcnt<0>();
 }
 
 template <int BM, int BN, int WM, int WN, int STAGES, int DK, int OUT, bool HAS_BIAS, bool STATIC, bool SPLITK,
@@ -428,6 +398,32 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < C::B_LOADS; ++i) dma(bsrc[i] + koff, base + C::A_BYTES + i * C::NT * 16);
     };
+
+    // Epilogue operands of this tile (column scales and bias, row scales and
+    // gate), one per thread, fetched before the first DMA so their latency
+    // hides behind the K loop. They reach the epilogue through LDS: a global
+    // load there would wait (vmcnt is in order) behind the output stores.
+    constexpr bool EP_COLS = !STATIC && OUT != OUT_I32;
+    constexpr bool EP_ROWS = OUT != OUT_I32;
+    static_assert(BM <= C::NT && BN <= C::NT, "one epilogue operand per thread");
+    __shared__ __attribute__((aligned(16))) float ep_sw[EP_COLS ? BN : 1];
+    __shared__ __attribute__((aligned(16))) float ep_b[HAS_BIAS && EP_COLS ? BN : 1];
+    __shared__ float ep_sx[EP_ROWS ? BM : 1];
+    __shared__ int ep_off[EP_ROWS ? BM : 1];
+    float r_sw = 0.0f, r_b = 0.0f, r_sx = 0.0f;
+    bool r_off = false;
+    if constexpr (EP_COLS) {
+        if (t < BN && col0 + t < n) {
+            r_sw = a.sw[col0 + t];
+            if constexpr (HAS_BIAS) r_b = a.bias[col0 + t];
+        }
+    }
+    if constexpr (EP_ROWS) {
+        if (t < BM && row0 + t < m) {
+            if constexpr (!STATIC) r_sx = a.sx[row0 + t];
+            r_off = gated_off(a, row0 + t);
+        }
+    }
 
     v16i acc[C::FM][C::FN];
 #pragma unroll
@@ -498,14 +494,14 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
 
     v4i fa[2][C::FM], fb[2][C::FN];
     if (nk > 0) {
-        wait_ahead<C::LOADS>(min(nk - 1, STAGES - 2));
+        wait_ahead<C::LOADS, STAGES - 2>(min(nk - 1, STAGES - 2));
         __builtin_amdgcn_s_barrier();
         read_frags(lds + (0 % STAGES) * C::STAGE, 0, fa[0], fb[0]);
     }
     for (int it = 0; it < nk; ++it) {
         // Stages it and it+1 must have landed (the tail of this iteration
         // reads stage it+1's first k-step); later ones may still be in flight.
-        wait_ahead<C::LOADS>(min(nk - 2 - it, STAGES - 3));
+        wait_ahead<C::LOADS, STAGES - 3>(min(nk - 2 - it, STAGES - 3));
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
         const bool do_issue = it + STAGES - 1 < nk;
@@ -556,45 +552,23 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
     const int rbase = row0 + wm * C::WTM + (lane & 31);
     const int cbase = col0 + wn * C::WTN + 4 * (lane >> 5);
 
-    if constexpr (SPLITK) {
-        if (S > 1) {
-#pragma unroll
-            for (int i = 0; i < C::FM; ++i) {
-                const int row = rbase + i * 32;
-                if (row >= m) continue;
-#pragma unroll
-                for (int j = 0; j < C::FN; ++j)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        const int col = cbase + j * 32 + 8 * (e >> 2) + (e & 3);
-                        if (col < n) atomicAdd(&a.ws[(int64_t)row * n + col], acc[i][j][e]);
-                    }
-            }
-            __threadfence();
-            __syncthreads();
-            __shared__ int last;
-            if (t == 0) last = (atomicAdd(&a.counters[tile_id], 1) == S - 1);
-            __syncthreads();
-            if (!last) return;
-            __threadfence();
-#pragma unroll
-            for (int i = 0; i < C::FM; ++i) {
-                const int row = rbase + i * 32;
-                if (row >= m) continue;
-#pragma unroll
-                for (int j = 0; j < C::FN; ++j)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        const int col = cbase + j * 32 + 8 * (e >> 2) + (e & 3);
-                        if (col >= n) continue;
-                        int* p = &a.ws[(int64_t)row * n + col];
-                        acc[i][j][e] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        *p = 0;
-                    }
-            }
-            if (t == 0) a.counters[tile_id] = 0;
+    if constexpr (SPLITK)
+        if (S > 1) a.out = a.ws + (int64_t)split * m * n;  // raw partials to this split's slab
+
+    if constexpr (EP_COLS) {
+        if (t < BN) {
+            ep_sw[t] = r_sw;
+            if constexpr (HAS_BIAS) ep_b[t] = r_b;
         }
     }
+    if constexpr (EP_ROWS) {
+        if (t < BM) {
+            ep_sx[t] = r_sx;
+            ep_off[t] = r_off;
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // every DMA and fragment read has landed
+    __builtin_amdgcn_s_barrier();   // ... in every wave, before the stage buffers are reused
 
     // Staged epilogue. Written straight from the fragment layout, every store
     // instruction of a wave would touch 32 rows at 8-16 bytes each; instead
@@ -611,28 +585,26 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
         constexpr int EP_CPR = C::WTN * ESZ / 16;  // 16-byte chunks per tile row
         static_assert(WM * WN * EP_REGION <= STAGES * C::STAGE, "epilogue staging fits in the stage buffers");
         static_assert((32 * EP_CPR) % 64 == 0, "whole copy-out passes");
-        const bool staged = (!SPLITK || S == 1) && (n % 8) == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15u) == 0 &&
-                            (STATIC || OUT == OUT_I32 || (reinterpret_cast<uintptr_t>(a.sw) & 15u) == 0) &&
-                            (!HAS_BIAS || OUT == OUT_I32 || (reinterpret_cast<uintptr_t>(a.bias) & 15u) == 0);
+        const bool staged = (n % 8) == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15u) == 0;
         if (staged) {
-            __builtin_amdgcn_s_waitcnt(0);  // every DMA and fragment read has landed
-            __builtin_amdgcn_s_barrier();   // ... in every wave, before the stage buffers are reused
             uint8_t* reg = lds + wave * EP_REGION;
             const int lrow = lane & 31;
             const int wrow0 = row0 + wm * C::WTM, wcol0 = col0 + wn * C::WTN;
 #pragma unroll
             for (int i = 0; i < C::FM; ++i) {
-                const int row = wrow0 + i * 32 + lrow;
+                const int lr = wm * C::WTM + i * 32 + lrow;  // row within the tile
                 float sxm = 0.0f;
-                if constexpr (!STATIC && OUT != OUT_I32) sxm = row < m ? a.sx[row] : 0.0f;
-                const bool off = OUT != OUT_I32 && row < m && gated_off(a, row);
+                bool off = false;
+                if constexpr (EP_ROWS) {
+                    sxm = ep_sx[lr];
+                    off = ep_off[lr] != 0;
+                }
 #pragma unroll
                 for (int j = 0; j < C::FN; ++j)
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const int lc = j * 32 + 8 * g + 4 * (lane >> 5);
-                        const int col = wcol0 + lc;
-                        const bool live = col < n;  // n % 8 == 0: then col + 3 < n too
+                        const int tc = wn * C::WTN + lc;  // column within the tile
                         const int v0 = acc[i][j][4 * g + 0], v1 = acc[i][j][4 * g + 1];
                         const int v2 = acc[i][j][4 * g + 2], v3 = acc[i][j][4 * g + 3];
                         uint8_t* dst = reg + lrow * EP_PITCH + lc * ESZ;
@@ -644,12 +616,12 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
                                 const float sc = a.ssx * a.ssw;
                                 f0 = (float)v0 * sc; f1 = (float)v1 * sc; f2 = (float)v2 * sc; f3 = (float)v3 * sc;
                             } else {
-                                const float4 swv = live ? *reinterpret_cast<const float4*>(a.sw + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+                                const float4 swv = *reinterpret_cast<const float4*>(ep_sw + tc);
                                 f0 = dequant(v0, sxm, swv.x); f1 = dequant(v1, sxm, swv.y);
                                 f2 = dequant(v2, sxm, swv.z); f3 = dequant(v3, sxm, swv.w);
                             }
                             if constexpr (HAS_BIAS) {
-                                const float4 bv = live ? *reinterpret_cast<const float4*>(a.bias + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+                                const float4 bv = *reinterpret_cast<const float4*>(ep_b + tc);
                                 f0 = f0 + bv.x; f1 = f1 + bv.y; f2 = f2 + bv.z; f3 = f3 + bv.w;
                             }
                             if (off) f0 = f1 = f2 = f3 = 0.0f;
@@ -681,106 +653,211 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
         }
     }
 
-    // Epilogue: four consecutive columns per (fragment, e/4) group.
-    // Vector stores/loads need every 4-column group 16-byte aligned (8 for bf16):
-    // n % 4 == 0 and aligned base pointers (a step_sliced word offset may break that).
+    // Direct epilogue: four consecutive columns per (fragment, e/4) group,
+    // stored as one vector when n % 4 == 0 and the output is aligned for it
+    // (a step_sliced word offset may break that), else element by element.
     const bool vec_ok = (n % 4) == 0 && (reinterpret_cast<uintptr_t>(a.out) & (OUT == OUT_BF16 ? 7u : 15u)) == 0;
-    const bool vec_sw = (reinterpret_cast<uintptr_t>(a.sw) & 15u) == 0;
-    const bool vec_b = (reinterpret_cast<uintptr_t>(a.bias) & 15u) == 0;
 #pragma unroll
     for (int j = 0; j < C::FN; ++j)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int col = cbase + j * 32 + 8 * g;
+            const int tc = col - col0;
             float4 swv = make_float4(0.f, 0.f, 0.f, 0.f), bv = make_float4(0.f, 0.f, 0.f, 0.f);
-            if constexpr (!STATIC && OUT != OUT_I32) {
-                if (vec_sw && col + 3 < n) swv = *reinterpret_cast<const float4*>(a.sw + col);
-                else {
-                    if (col + 0 < n) swv.x = a.sw[col + 0];
-                    if (col + 1 < n) swv.y = a.sw[col + 1];
-                    if (col + 2 < n) swv.z = a.sw[col + 2];
-                    if (col + 3 < n) swv.w = a.sw[col + 3];
-                }
-            }
-            if constexpr (HAS_BIAS && OUT != OUT_I32) {
-                if (vec_b && col + 3 < n) bv = *reinterpret_cast<const float4*>(a.bias + col);
-                else {
-                    if (col + 0 < n) bv.x = a.bias[col + 0];
-                    if (col + 1 < n) bv.y = a.bias[col + 1];
-                    if (col + 2 < n) bv.z = a.bias[col + 2];
-                    if (col + 3 < n) bv.w = a.bias[col + 3];
-                }
+            if constexpr (EP_COLS) {
+                swv = *reinterpret_cast<const float4*>(ep_sw + tc);
+                if constexpr (HAS_BIAS) bv = *reinterpret_cast<const float4*>(ep_b + tc);
             }
 #pragma unroll
             for (int i = 0; i < C::FM; ++i) {
                 const int row = rbase + i * 32;
                 if (row >= m || col >= n) continue;
                 float sxm = 0.0f;
-                if constexpr (!STATIC && OUT != OUT_I32) sxm = a.sx[row];
-                const bool off = OUT != OUT_I32 && gated_off(a, row);
-                const int v0 = acc[i][j][4 * g + 0], v1 = acc[i][j][4 * g + 1];
-                const int v2 = acc[i][j][4 * g + 2], v3 = acc[i][j][4 * g + 3];
-                const int64_t idx = (int64_t)row * n + col;
-                if (vec_ok && col + 3 < n) {
-                    if constexpr (OUT == OUT_I32) {
-                        *reinterpret_cast<v4i*>(reinterpret_cast<int*>(a.out) + idx) = v4i{v0, v1, v2, v3};
-                    } else {
-                        float f0, f1, f2, f3;
-                        if constexpr (STATIC) {
-                            const float sc = a.ssx * a.ssw;
-                            f0 = (float)v0 * sc; f1 = (float)v1 * sc; f2 = (float)v2 * sc; f3 = (float)v3 * sc;
-                        } else {
-                            f0 = dequant(v0, sxm, swv.x); f1 = dequant(v1, sxm, swv.y);
-                            f2 = dequant(v2, sxm, swv.z); f3 = dequant(v3, sxm, swv.w);
-                        }
-                        if constexpr (HAS_BIAS) { f0 = f0 + bv.x; f1 = f1 + bv.y; f2 = f2 + bv.z; f3 = f3 + bv.w; }
-                        if (off) f0 = f1 = f2 = f3 = 0.0f;
-                        if constexpr (OUT == OUT_F32) {
-                            *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + idx) = make_float4(f0, f1, f2, f3);
-                        } else {
-                            const uint32_t lo = pack_bf16x2(f0, f1);
-                            const uint32_t hi = pack_bf16x2(f2, f3);
-                            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.out) + idx) = make_uint2(lo, hi);
-                        }
-                    }
-                } else {
-                    const int vv[4] = {v0, v1, v2, v3};
+                bool off = false;
+                if constexpr (EP_ROWS) {
+                    sxm = ep_sx[row - row0];
+                    off = ep_off[row - row0] != 0;
+                }
+                const int v[4] = {acc[i][j][4 * g + 0], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+                float f[4] = {0.f, 0.f, 0.f, 0.f};
+                if constexpr (OUT != OUT_I32) {
                     const float sv[4] = {swv.x, swv.y, swv.z, swv.w};
                     const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        if (col + q < n) emit<OUT, HAS_BIAS, STATIC>(a, row, col + q, vv[q], sxm, sv[q], bb[q]);
+                    for (int q = 0; q < 4; ++q) {
+                        if constexpr (STATIC) f[q] = (float)v[q] * (a.ssx * a.ssw);
+                        else f[q] = dequant(v[q], sxm, sv[q]);
+                        if constexpr (HAS_BIAS) f[q] = f[q] + bb[q];
+                        if (off) f[q] = 0.0f;
+                    }
+                }
+                const int64_t idx = (int64_t)row * n + col;
+                if (vec_ok && col + 3 < n) {
+                    if constexpr (OUT == OUT_I32)
+                        *reinterpret_cast<v4i*>(reinterpret_cast<int*>(a.out) + idx) = v4i{v[0], v[1], v[2], v[3]};
+                    else if constexpr (OUT == OUT_F32)
+                        *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + idx) = make_float4(f[0], f[1], f[2], f[3]);
+                    else
+                        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.out) + idx) =
+                            make_uint2(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]));
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        if (col + q >= n) continue;
+                        if constexpr (OUT == OUT_I32) reinterpret_cast<int*>(a.out)[idx + q] = v[q];
+                        else store_out<OUT>(a.out, idx + q, f[q]);
+                    }
                 }
             }
         }
 #endif
 }
 
+// ---------------------------------------------------------------- split-K reduction
+// out[r, c] = epilogue(sum_s ws[s][r][c]). VEC: four consecutive columns per
+// thread (n % 4 == 0 and the output aligned for a 4-element store).
+template <int OUT, bool HAS_BIAS, bool STATIC, bool VEC>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a) {
+    const int n = a.n, S = a.splits;
+    const int64_t mn = (int64_t)a.m * n;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    if constexpr (VEC) {
+        const v4i* ws = reinterpret_cast<const v4i*>(a.ws);
+        const int64_t q4 = mn >> 2;
+        for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < q4; q += stride) {
+            v4i acc = ws[q];
+            for (int sp = 1; sp < S; ++sp) {
+                const v4i v = ws[(int64_t)sp * q4 + q];
+                acc[0] += v[0]; acc[1] += v[1]; acc[2] += v[2]; acc[3] += v[3];
+            }
+            const int64_t idx = q << 2;
+            const int row = (int)(idx / n), col = (int)(idx - (int64_t)row * n);
+            if constexpr (OUT == OUT_I32) {
+                reinterpret_cast<v4i*>(a.out)[q] = acc;
+            } else {
+                float f[4];
+                const float sxm = STATIC ? 0.0f : a.sx[row];
+                const bool off = gated_off(a, row);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (STATIC) f[e] = (float)acc[e] * (a.ssx * a.ssw);
+                    else f[e] = dequant(acc[e], sxm, a.sw[col + e]);
+                    if constexpr (HAS_BIAS) f[e] = f[e] + a.bias[col + e];
+                    if (off) f[e] = 0.0f;
+                }
+                if constexpr (OUT == OUT_F32)
+                    reinterpret_cast<float4*>(a.out)[q] = make_float4(f[0], f[1], f[2], f[3]);
+                else
+                    reinterpret_cast<uint2*>(a.out)[q] = make_uint2(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]));
+            }
+        }
+    } else {
+        for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < mn; idx += stride) {
+            int acc = a.ws[idx];
+            for (int sp = 1; sp < S; ++sp) acc += a.ws[(int64_t)sp * mn + idx];
+            const int row = (int)(idx / n), col = (int)(idx - (int64_t)row * n);
+            const float sxm = (STATIC || OUT == OUT_I32) ? 0.0f : a.sx[row];
+            const float swn = (STATIC || OUT == OUT_I32) ? 0.0f : a.sw[col];
+            const float bn = (HAS_BIAS && OUT != OUT_I32) ? a.bias[col] : 0.0f;
+            emit<OUT, HAS_BIAS, STATIC>(a, row, col, acc, sxm, swn, bn);
+        }
+    }
+}
+
 // ---------------------------------------------------------------- host side
-struct TileChoice {
-    int cfg;     // 0: 256x256 (4 waves, 128x128 each), 1: 128x128 (4 waves, 64x64 each)
-    int splits;  // split-K factor
+// Tile configurations of the DMA kernel (the register-staged fallback has
+// only 256x256 and 128x128; every smaller choice maps to its 128x128).
+enum TileCfg {
+    TILE_256 = 0,     // 256x256, 8 waves of 128x64, 4 stages
+    TILE_128 = 1,     // 128x128, 4 waves of 64x64, 4 stages
+    TILE_64x128 = 2,  // 64x128, 4 waves of 32x64, 4 stages
+    TILE_64 = 3,      // 64x64, 4 waves of 32x32, 4 stages
+    TILE_64_DEEP = 4  // 64x64 with 8 stages in flight (long K on a few tiles)
 };
 
-// Pick the tile shape that finishes first on 256 CUs. A launch runs in rounds
-// of 256 workgroups, so its time is ~ rounds x (time of one tile). A 256x256
-// tile does 4x the work of a 128x128 one at ~1.25x its efficiency (half the
-// LDS-staging bytes per op), measured on MI355X. Hence the costs:
-//   256x256: 4 * ceil(tiles256 / 256)
-//   128x128: 1.25 * ceil(tiles128 / 256)
-// The smaller wins. On the measured configs[2] and configs[4] shapes this
-// picks the faster tile in every case; e.g. 8192x1024x3072 runs 384 big tiles
-// (2 rounds, one half-empty) but 1536 small ones (6 full rounds).
-// Split-K through i32 atomics measured slower than an under-filled grid
-// (2048x1024x3072: 457 us split vs ~60 us unsplit), so it stays off.
+struct TileChoice {
+    int cfg;     // TileCfg
+    int splits;  // split-K factor S
+};
+
+// Measurement overrides, read once: BH_GEMM_TILE=c forces TileCfg c,
+// BH_SPLITK=S forces the split factor (1 = never split).
+static int env_int(const char* name, int dflt) {
+    const char* e = getenv(name);
+    return e ? atoi(e) : dflt;
+}
+static int tile_env() {
+    static int v = env_int("BH_GEMM_TILE", -1);
+    return v;
+}
+static int splitk_env() {
+    static int v = env_int("BH_SPLITK", 0);
+    return v;
+}
+
+constexpr size_t SPLITK_MAX_BYTES = size_t(64) << 20;  // workspace cap per call
+
+// Split-K. Measured on MI355X, a tile alone on its CU costs a few us fixed
+// (launch, first loads, epilogue) plus P us per 64-byte K stage (0.25 for
+// 128x128, 0.18 for the 64-row tiles), so splitting K S ways shortens the
+// chain by P * stages * (1 - 1/S) us. It pays for the i32 partial slabs
+// (S*m*n*4 bytes written and read back, ~3 TB/s effective) and the reduction
+// launch (~3 us). S is the largest value with tiles x S within two workgroups
+// per CU and at least 8 stages per split, used only when the modelled gain
+// exceeds 3 us (a margin for the model).
+static int choose_splits(long tiles, double per_stage, int m, int kg, int n) {
+    constexpr long CUS = 256;
+    const long stages = (long)kg * 4 / 64;
+    const double slab = (double)m * n * 4;
+    const int forced = splitk_env();
+    long S = forced > 0 ? forced : std::min<long>(8, (2 * CUS) / std::max<long>(tiles, 1));
+    if (forced <= 0) {
+        while (S > 1 && stages / S < 8) --S;
+        if (S > 1) {
+            const double gain = per_stage * stages * (1.0 - 1.0 / S) - 3.0 - S * slab / 3.0e6;
+            if (gain < 3.0) S = 1;
+        }
+    }
+    while (S > 1 && (stages / S < 1 || S * slab > (double)SPLITK_MAX_BYTES)) --S;
+    return (int)std::max<long>(S, 1);
+}
+
+// Pick the tile that finishes first on 256 CUs.
+//  - Enough 128x128 tiles to fill the chip: a launch runs in rounds of 256
+//    workgroups, so its time is ~ rounds x (time of one tile). A 256x256 tile
+//    does 4x the work of a 128x128 one at ~1.25x its efficiency (half the
+//    LDS-staging bytes per op), hence the costs 4 * ceil(tiles256 / 256) and
+//    1.25 * ceil(tiles128 / 256); the smaller wins (e.g. 8192x1024x3072 runs
+//    384 big tiles, 2 rounds with one half empty, or 1536 small ones in 6
+//    full rounds).
+//  - Fewer 128x128 tiles than CUs: smaller tiles put more CUs to work. A lone
+//    tile's time is set by how fast one CU streams its operands, so halving a
+//    tile side nearly halves its time. Measured on the configs[2] shapes at
+//    M=128..2048: 128-255 tiles of 128x128 run fastest as 64x128 tiles, fewer
+//    as 64x64 tiles, and 64x64 tiles on at most one round of CUs with 32+
+//    K stages run fastest with 8 stages in flight.
 static TileChoice choose_tiles(int m, int kg, int n) {
-    (void)kg;
     constexpr long CUS = 256;
     const long t256 = (long)((m + 255) / 256) * ((n + 255) / 256);
     const long t128 = (long)((m + 127) / 128) * ((n + 127) / 128);
+    const long t64 = (long)((m + 63) / 64) * ((n + 63) / 64);
+    const long stages = (long)kg * 4 / 64;
     const double c256 = 4.0 * (double)((t256 + CUS - 1) / CUS);
     const double c128 = 1.25 * (double)((t128 + CUS - 1) / CUS);
-    return {c256 <= c128 ? 0 : 1, 1};
+    TileChoice tc{TILE_128, 1};
+    if (c256 <= c128) tc.cfg = TILE_256;
+    else if (t128 >= CUS) tc.cfg = TILE_128;
+    else if (t128 >= CUS / 2) tc.cfg = TILE_64x128;
+    else tc.cfg = (t64 <= CUS && stages >= 32) ? TILE_64_DEEP : TILE_64;
+    if (tile_env() >= 0) tc.cfg = tile_env();
+    switch (tc.cfg) {
+        case TILE_128: tc.splits = choose_splits(t128, 0.25, m, kg, n); break;
+        case TILE_64x128: tc.splits = choose_splits(t128 * 2, 0.2, m, kg, n); break;
+        case TILE_64:
+        case TILE_64_DEEP: tc.splits = choose_splits(t64, 0.18, m, kg, n); break;
+        default: break;
+    }
+    return tc;
 }
 
 template <int BM, int BN, int WM, int WN, int OUT, bool HAS_BIAS, bool STATIC, bool SPLITK, bool Q4 = false>
@@ -804,20 +881,28 @@ static hipError_t go_dma(hipStream_t s, const GemmArgs& a) {
     return hipGetLastError();
 }
 
-// Tuning knob for the large-tile DMA configuration (read once):
-// BH_GEMM_BIG=0: 256x256, 8 waves (128x64 each: 2 waves per SIMD, 196 VGPRs),
-//                DK=64, 4 stages, DMA issue interleaved with the MFMAs (default;
-//                measured 5-10% above the 4-wave form on the large shapes)
-// BH_GEMM_BIG=1: 256x128, 4 waves (128x64 each), DK=128, 3 stages
-// BH_GEMM_BIG=2: the default without the DMA interleave
-// BH_GEMM_BIG=3: 256x256, 4 waves (128x128 each), no interleave
-// BH_GEMM_BIG=4: 256x256, 4 waves (128x128 each), DMA interleave
+// Alternative large-tile DMA configurations for measurement (BH_GEMM_BIG):
+// 0: 256x256, 8 waves (128x64 each: 2 waves per SIMD, ~200 VGPRs), DK=64,
+//    4 stages, DMA issue interleaved with the MFMAs (default; measured 5-10%
+//    above the 4-wave form on the large shapes)
+// 1: 256x128, 4 waves (128x64 each), DK=128, 3 stages
+// 2: the default without the DMA interleave
+// 3: 256x256, 4 waves (128x128 each), no interleave
+// 4: 256x256, 4 waves (128x128 each), DMA interleave
 static int big_cfg() {
-    static int v = [] {
-        const char* e = getenv("BH_GEMM_BIG");
-        return e ? atoi(e) : 0;
-    }();
+    static int v = env_int("BH_GEMM_BIG", 0);
     return v;
+}
+
+// The DMA kernel for every tile but 256x256.
+template <int OUT, bool HAS_BIAS, bool STATIC, bool SPLITK>
+static hipError_t go_small(hipStream_t s, int cfg, const GemmArgs& a) {
+    switch (cfg) {
+        case TILE_64x128: return go_dma<64, 128, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
+        case TILE_64: return go_dma<64, 64, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
+        case TILE_64_DEEP: return go_dma<64, 64, 2, 2, 8, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
+        default: return go_dma<128, 128, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
+    }
 }
 
 // dma: K % 64 == 0 and both operands 16-byte aligned (the DMA path cannot
@@ -825,7 +910,7 @@ static int big_cfg() {
 template <int OUT, bool HAS_BIAS, bool STATIC>
 static hipError_t go_cfg(hipStream_t s, bool aligned, bool dma, const TileChoice& tc, const GemmArgs& a) {
     if (dma) {
-        if (tc.cfg == 0) {
+        if (tc.cfg == TILE_256) {
             switch (big_cfg()) {
                 case 1: return go_dma<256, 128, 2, 2, 3, 128, OUT, HAS_BIAS, STATIC, false>(s, a);
                 case 2: return go_dma<256, 256, 2, 4, 4, 64, OUT, HAS_BIAS, STATIC, false>(s, a);
@@ -834,11 +919,9 @@ static hipError_t go_cfg(hipStream_t s, bool aligned, bool dma, const TileChoice
                 default: return go_dma<256, 256, 2, 4, 4, 64, OUT, HAS_BIAS, STATIC, false, true>(s, a);
             }
         }
-        if (tc.splits > 1) return go_dma<128, 128, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, true>(s, a);
-        return go_dma<128, 128, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, false>(s, a);
+        return go_small<OUT, HAS_BIAS, STATIC, false>(s, tc.cfg, a);
     }
-    if (tc.cfg == 0) return go<256, 256, 2, 2, OUT, HAS_BIAS, STATIC, false>(s, aligned, a);
-    if (tc.splits > 1) return go<128, 128, 2, 2, OUT, HAS_BIAS, STATIC, true>(s, aligned, a);
+    if (tc.cfg == TILE_256) return go<256, 256, 2, 2, OUT, HAS_BIAS, STATIC, false>(s, aligned, a);
     return go<128, 128, 2, 2, OUT, HAS_BIAS, STATIC, false>(s, aligned, a);
 }
 
@@ -847,51 +930,65 @@ static inline bool gemm_aligned(const void* xq, const void* wq, int kg) {
            ((reinterpret_cast<uintptr_t>(wq) & 15u) == 0);
 }
 
-// Split-K workspace of one device: [m*n] i32 sums plus per-tile counters,
-// zeroed once at allocation and left zeroed by every kernel that uses them.
-int* splitk_workspace(size_t ints, size_t counters, int** counters_out, hipError_t* err);
+// Split-K workspace of the stream: at least `ints` i32 (grown outside graph
+// capture only; hipErrorStreamCaptureUnsupported otherwise).
+int* splitk_workspace(hipStream_t s, size_t ints, hipError_t* err);
 
 // Workspace elements the GEMM needs for this shape (0 = no split-K).
-size_t gemm_workspace_ints(int m, int kg, int n, size_t* counters) {
-    TileChoice tc = choose_tiles(m, kg, n);
-    if (tc.splits <= 1) {
-        *counters = 0;
-        return 0;
-    }
-    *counters = (size_t)((m + 127) / 128) * ((n + 127) / 128);
-    return (size_t)m * n;
+size_t gemm_workspace_ints(int m, int kg, int n) {
+    const TileChoice tc = choose_tiles(m, kg, n);
+    return tc.splits > 1 ? (size_t)tc.splits * m * n : 0;
+}
+
+hipError_t gemm_reserve(hipStream_t s, int m, int kg, int n) {
+    const size_t ints = gemm_workspace_ints(m, kg, n);
+    if (!ints) return hipSuccess;
+    hipError_t err = hipSuccess;
+    return splitk_workspace(s, ints, &err) ? hipSuccess : err;
+}
+
+// Launches the chosen configuration: one kernel, or for S > 1 the split
+// kernel (raw i32 partials) and the reduction that applies the epilogue.
+template <int OUT, bool HAS_BIAS, bool STATIC>
+static hipError_t run_gemm(hipStream_t s, bool al, bool dma, const TileChoice& tc, GemmArgs a) {
+    if (tc.splits <= 1) return go_cfg<OUT, HAS_BIAS, STATIC>(s, al, dma, tc, a);
+    hipError_t err = hipSuccess;
+    a.ws = splitk_workspace(s, (size_t)tc.splits * a.m * a.n, &err);
+    if (!a.ws) return err == hipSuccess ? hipErrorOutOfMemory : err;
+    a.splits = tc.splits;
+    err = dma ? go_small<OUT_I32, false, false, true>(s, tc.cfg, a)
+              : go<128, 128, 2, 2, OUT_I32, false, false, true>(s, al, a);
+    if (err != hipSuccess) return err;
+    const int64_t mn = (int64_t)a.m * a.n;
+    const uintptr_t need = OUT == OUT_BF16 ? 7u : 15u;
+    const bool vec = (a.n % 4) == 0 && (reinterpret_cast<uintptr_t>(a.out) & need) == 0;
+    const int64_t work = vec ? mn / 4 : mn;
+    const unsigned grid = (unsigned)std::min<int64_t>((work + 255) / 256, 256 * 16);
+    if (vec) splitk_reduce_kernel<OUT, HAS_BIAS, STATIC, true><<<grid, 256, 0, s>>>(a);
+    else splitk_reduce_kernel<OUT, HAS_BIAS, STATIC, false><<<grid, 256, 0, s>>>(a);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemm_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n) {
-    GemmArgs a{xq, wq, sx, sw, bias, out, m, kg, n, 0.f, 0.f, 1, nullptr, nullptr};
+    GemmArgs a{xq, wq, sx, sw, bias, out, m, kg, n, 0.f, 0.f, 1, nullptr};
     const bool al = gemm_aligned(xq, wq, kg);
     const bool dma = al && ((kg * 4) % 128 == 0);
-    TileChoice tc = choose_tiles(m, kg, n);
-    if (tc.splits > 1) {
-        hipError_t err = hipSuccess;
-        size_t nc = 0;
-        const size_t ints = gemm_workspace_ints(m, kg, n, &nc);
-        a.ws = splitk_workspace(ints, nc, &a.counters, &err);
-        if (!a.ws) return err == hipSuccess ? hipErrorOutOfMemory : err;
-        a.splits = tc.splits;
-    }
-    if (out_dtype == OUT_I32) return go_cfg<OUT_I32, false, false>(s, al, dma, tc, a);
+    const TileChoice tc = choose_tiles(m, kg, n);
+    if (out_dtype == OUT_I32) return run_gemm<OUT_I32, false, false>(s, al, dma, tc, a);
     if (out_dtype == OUT_F32) {
-        if (bias) return go_cfg<OUT_F32, true, false>(s, al, dma, tc, a);
-        return go_cfg<OUT_F32, false, false>(s, al, dma, tc, a);
+        if (bias) return run_gemm<OUT_F32, true, false>(s, al, dma, tc, a);
+        return run_gemm<OUT_F32, false, false>(s, al, dma, tc, a);
     }
-    if (bias) return go_cfg<OUT_BF16, true, false>(s, al, dma, tc, a);
-    return go_cfg<OUT_BF16, false, false>(s, al, dma, tc, a);
+    if (bias) return run_gemm<OUT_BF16, true, false>(s, al, dma, tc, a);
+    return run_gemm<OUT_BF16, false, false>(s, al, dma, tc, a);
 }
 
 hipError_t launch_gemm_i8_static(hipStream_t s, const uint32_t* xq, const uint32_t* wq, float ssx, float ssw,
                                  float* out, int m, int kg, int n) {
-    GemmArgs a{xq, wq, nullptr, nullptr, nullptr, out, m, kg, n, ssx, ssw, 1, nullptr, nullptr};
-    TileChoice tc = choose_tiles(m, kg, n);
-    tc.splits = 1;  // the static variant stays on plain tiles
+    GemmArgs a{xq, wq, nullptr, nullptr, nullptr, out, m, kg, n, ssx, ssw, 1, nullptr};
     const bool al = gemm_aligned(xq, wq, kg);
-    return go_cfg<OUT_F32, false, true>(s, al, al && ((kg * 4) % 128 == 0), tc, a);
+    return run_gemm<OUT_F32, false, true>(s, al, al && ((kg * 4) % 128 == 0), choose_tiles(m, kg, n), a);
 }
 
 // W4A8 prefill GEMM (matmul_q4_dyn, crates/kernels/wgsl/matmul_q4_dyn.wgsl):
@@ -900,13 +997,13 @@ hipError_t launch_gemm_i8_static(hipStream_t s, const uint32_t* xq, const uint32
 template <int OUT, bool HAS_BIAS>
 static hipError_t go_q4(hipStream_t s, bool aligned, const GemmArgs& a) {
     TileChoice tc = choose_tiles(a.m, a.kg, a.n);
-    if (tc.cfg == 0) return go<256, 256, 2, 2, OUT, HAS_BIAS, false, false, true>(s, aligned, a);
+    if (tc.cfg == TILE_256) return go<256, 256, 2, 2, OUT, HAS_BIAS, false, false, true>(s, aligned, a);
     return go<128, 128, 2, 2, OUT, HAS_BIAS, false, false, true>(s, aligned, a);
 }
 
 hipError_t launch_gemm_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int k, int n) {
-    GemmArgs a{xq, wq, sx, sw, bias, out, m, k / 4, n, 0.f, 0.f, 1, nullptr, nullptr};
+    GemmArgs a{xq, wq, sx, sw, bias, out, m, k / 4, n, 0.f, 0.f, 1, nullptr};
     // Aligned 16-byte loads need 16-byte rows in both operands: K % 32 == 0.
     const bool al = (k % 32) == 0 && ((reinterpret_cast<uintptr_t>(xq) | reinterpret_cast<uintptr_t>(wq)) & 15u) == 0;
     switch (out_dtype) {
@@ -919,10 +1016,10 @@ hipError_t launch_gemm_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
 hipError_t launch_gemm_i8_gated(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                                 const float* sw, const float* gate, int gate_stride, int gate_col, float* out, int m,
                                 int kg, int n) {
-    GemmArgs a{xq, wq, sx, sw, nullptr, out, m, kg, n, 0.f, 0.f, 1, nullptr, nullptr, gate, gate_stride, gate_col};
+    GemmArgs a{xq, wq, sx, sw, nullptr, out, m, kg, n, 0.f, 0.f, 1, nullptr, gate, gate_stride, gate_col};
     const bool al = gemm_aligned(xq, wq, kg);
     const bool dma = al && ((kg * 4) % 128 == 0);
-    return go_cfg<OUT_F32, false, false>(s, al, dma, choose_tiles(m, kg, n), a);
+    return run_gemm<OUT_F32, false, false>(s, al, dma, choose_tiles(m, kg, n), a);
 }
 
 }  // namespace bh

@@ -50,6 +50,7 @@ hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, flo
 hipError_t launch_quantize_weight(hipStream_t s, const float* w, int n, int k, uint32_t* packed, float* sw);
 hipError_t launch_gemv_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n);
+hipError_t gemm_reserve(hipStream_t s, int m, int kg, int n);
 hipError_t launch_gemm_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n);
 hipError_t launch_gemv_i8_pre(hipStream_t s, int mode, const uint32_t* pre_tok, const float* pre_emb,
@@ -674,6 +675,19 @@ int dalloc(bh_qwen3* e, T** p, size_t count) {
         if (_e != hipSuccess) return fail(BH_ERR_HIP, "bh_qwen3: %s: %s", what, hipGetErrorString(_e)); \
     } while (0)
 
+// Sizes the split-K workspace of the engine's stream for every GEMM-routed
+// linear of `rows` rows, so a captured step never needs to allocate.
+int reserve_linears(bh_qwen3* e, int rows) {
+    const int d = (int)e->c.d_model, ff = (int)e->c.d_ff;
+    const int shapes[5][2] = {{d, (int)e->W}, {(int)e->hq, d}, {d, 2 * ff}, {ff, d}, {d, (int)e->c.vocab}};
+    for (const auto& kn : shapes) {
+        const int tuned = tuned_variant((uint32_t)rows, (uint32_t)kn[1], (uint32_t)kn[0]);
+        const bool gemv = tuned ? tuned == BH_VARIANT_WORKGROUP_PER_OUTPUT : rows <= 32;
+        if (!gemv) BH_HIP(gemm_reserve(e->stream, rows, kn[0] / 4, kn[1]), "split-K workspace");
+    }
+    return BH_OK;
+}
+
 int launch_linear(bh_qwen3* e, const uint32_t* w, const float* sw, float* out, int m, int k, int n) {
     const int tuned = tuned_variant((uint32_t)m, (uint32_t)n, (uint32_t)k);
     const bool gemv = tuned ? tuned == BH_VARIANT_WORKGROUP_PER_OUTPUT : m <= 32;
@@ -1234,6 +1248,7 @@ int bh_qwen3_decode(bh_qwen3* e, uint32_t steps, uint32_t flags, uint32_t* out) 
                 (void)hipGraphExecDestroy(e->graph);
                 e->graph = nullptr;
             }
+            BH_TRY(reserve_linears(e, b));
             hipGraph_t g = nullptr;
             BH_HIP(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal), "begin capture");
             const int rc = run_rows(e, b, e->tok_dec, e->pos_dec, e->seq_dec, b, nullptr, true, (int)e->max_splits);

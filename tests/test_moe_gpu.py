@@ -18,7 +18,8 @@ def dev_u32(a, device):
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(device)
 
 
-@pytest.mark.parametrize("m,k,n", [(1, 1024, 768), (8, 1024, 768), (32, 2048, 512), (33, 512, 300), (512, 1024, 1536)])
+@pytest.mark.parametrize("m,k,n", [(1, 1024, 768), (8, 1024, 768), (32, 2048, 512), (33, 512, 300), (512, 1024, 1536),
+                                   (200, 4096, 300)])
 def test_moe_linear_gated_i8(gpu, m, k, n):
     rng = np.random.default_rng(m + k + n)
     n_experts, e_idx = 8, 3

@@ -169,6 +169,26 @@ def test_gemm_edges(gpu, m, k, n):
     run_and_check(gpu, m, k, n, "dyn", seed=m * 3 + k + n, bias=True)
 
 
+# Few output tiles and long K: the GEMM splits K over workgroups and adds the
+# i32 partials in a second kernel. Covered: the LDS-DMA and register-staged
+# (K % 128 != 0, K % 64 != 0) split kernels, the 4-column and per-element
+# (N % 4 != 0) reductions, and the largest split factor (8).
+@pytest.mark.parametrize("m,k,n", [(300, 4096, 520), (256, 4104, 130), (40, 8192, 64), (129, 5000, 255),
+                                   (128, 3072, 1024), (64, 16384, 128)])
+def test_gemm_split_k(gpu, m, k, n):
+    run_and_check(gpu, m, k, n, "dyn", seed=m + 5 * k + n, bias=True)
+
+
+def test_static_scale_matmul_split_k(gpu):
+    m, k, n = 64, 4096, 256
+    xq = o.quant_pack(o.synth_acts(m, k, 3), np.full(m, 0.02, np.float32))
+    wq, _ = o.synth_weights(n, k, 4)
+    sx, sw = np.float32(0.0031), np.float32(0.0007)
+    got = ops.matmul_i8_static(dev_u32(xq, gpu), dev_u32(wq, gpu), sx, sw).cpu().numpy()
+    want = o.epilogue_static(o.acc_exact(xq, wq), sx, sw)
+    assert (got.view(np.uint32) == want.view(np.uint32)).all()
+
+
 def test_auto_variant_and_gemv_equals_gemm(gpu):
     for m in (1, 16, 32, 33, 64):
         run_and_check(gpu, m, 1024, 640, "auto", seed=m)
