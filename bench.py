@@ -12,7 +12,8 @@ from HBM, not the Infinity Cache.
   roofline = the GEMV kernel alone: its algorithmic bytes (N*K + 4N + M*K + 2*M*N)
              / its average launch duration, timed with HIP events on the stream
              it runs on, vs 8 TB/s
-Also reported: the prefill GEMM sweep in TOPS vs the 5.0 POPS int8
+Also reported: the prefill GEMM sweep (configs[2], each shape timed as one HIP
+graph of back-to-back launches) in TOPS vs the 5.0 POPS int8
 dense MFMA peak, an MFMA roof probe, and the CPU baseline (the restated
 backend-cpu decode path, OpenMP, timed on this host on a bounded sample).
 """
@@ -222,22 +223,33 @@ def bench_prefill(torch, lib, dev, gen, reps):
             bias = torch.randn(n, device=dev, generator=gen)
             out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
 
-            def run():
-                check(lib.bh_matmul_i8_dyn(sp, xq.data_ptr(), wq.data_ptr(), sx.data_ptr(), sw.data_ptr(),
+            def run(stream_ptr):
+                check(lib.bh_matmul_i8_dyn(stream_ptr, xq.data_ptr(), wq.data_ptr(), sx.data_ptr(), sw.data_ptr(),
                                            bias.data_ptr(), out.data_ptr(), BH_OUT_BF16, m, k // 4, n))
 
-            run()
+            # `reps` back-to-back launches in one HIP graph, so host launch
+            # cost stays out of the per-launch time.
+            run(sp)
+            torch.cuda.synchronize()
+            cap = torch.cuda.Stream()
+            check(lib.bh_reserve_workspace(cap.cuda_stream, m, k // 4, n))
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=cap):
+                for _ in range(reps):
+                    run(cap.cuda_stream)
+            g.replay()
             torch.cuda.synchronize()
             ts = []
-            for _ in range(reps):
+            for _ in range(3):
                 a = torch.cuda.Event(enable_timing=True)
                 b = torch.cuda.Event(enable_timing=True)
                 a.record(stream)
-                run()
+                g.replay()
                 b.record(stream)
                 ts.append((a, b))
             torch.cuda.synchronize()
-            us = 1e3 * sorted(a.elapsed_time(b) for a, b in ts)[reps // 2]
+            us = 1e3 * sorted(a.elapsed_time(b) for a, b in ts)[1] / reps
+            del g
             ops = 2.0 * m * n * k
             byts = m * k + n * k + 2 * m * n + 4 * m + 8 * n
             tops = ops / us / 1e6

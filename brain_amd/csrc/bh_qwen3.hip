@@ -42,6 +42,7 @@
 #include <vector>
 
 #include "../../include/brain_hip.h"
+#include "bh_attn.h"
 #include "bh_common.h"
 #include "bh_st.h"
 
@@ -229,25 +230,13 @@ __device__ __forceinline__ uint8_t kv8_code(float v, float scale) {
     return (uint8_t)(int8_t)(int)q;
 }
 
-// One wave per (row, head): heads [0,nh) are queries, [nh, nh+nkv) keys,
-// [nh+nkv, nh+2nkv) values. Queries and keys get the per-head RMSNorm and the
+// One head of the q|k|v row through the per-head RMSNorm and the
 // rotate-half RoPE of rope_paged.wgsl:27-38 (pair (m, m+hd/2), angle
-// pos * theta^(-2m/hd)); keys and values land in the cache at (seq, pos)
-// (paged_kv_append_batched.wgsl with a contiguous slab per sequence). KV8
-// stores them as int8 with one scale per (token, kv head),
-// min(max|x|, clip[head]) / 127 (1 when that is 0), as
-// paged_kv_append_i8_clipped_batched.wgsl.
-template <bool KV8>
-__global__ __launch_bounds__(64) void qk_rope_append_kernel(RopeArgs p) {
-    const int r = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
-    const int W = p.hq + 2 * p.hkv, half = p.hd >> 1;
-    const uint32_t pos = p.pos[r];
-    const size_t tok = (size_t)p.seq[r] * p.max_seq + pos;
-    const bool is_q = h < p.nh, is_k = !is_q && h < p.nh + p.nkv;
-    const int kh = is_q ? 0 : (is_k ? h - p.nh : h - p.nh - p.nkv);
-    const float* src = p.qkv + (size_t)r * W +
-                       (is_q ? h * p.hd : (is_k ? p.hq + kh * p.hd : p.hq + p.hkv + kh * p.hd));
-    float y0[2], y1[2];
+// pos * theta^(-2m/hd)) when `rot` (queries and keys), else unchanged
+// (values). One wave; lane l holds pairs m = l and l + 64 (hd <= 256).
+__device__ __forceinline__ void rope_head(const RopeArgs& p, const float* src, const float* nw, bool rot, uint32_t pos,
+                                          int lane, float (&y0)[2], float (&y1)[2]) {
+    const int half = p.hd >> 1;
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -259,31 +248,39 @@ __global__ __launch_bounds__(64) void qk_rope_append_kernel(RopeArgs p) {
             ss += y0[u] * y0[u] + y1[u] * y1[u];
         }
     }
-    if (is_q || is_k) {
-        const float* nw = is_q ? p.qn : p.kn;
-        float inv = 1.0f;
-        if (p.qk_norm) {
-            ss = wave_sum(ss);
-            inv = 1.0f / sqrtf(ss / (float)p.hd + p.eps);
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int m = lane + 64 * u;
-            if (m >= half) continue;
-            float a = y0[u], b = y1[u];
-            if (p.qk_norm) {
-                a = a * inv * nw[m];
-                b = b * inv * nw[m + half];
-            }
-            const float angle = (float)pos * powf(p.theta, -(float)(2 * m) / (float)p.hd);
-            const float c = cosf(angle), s = sinf(angle);
-            y0[u] = a * c - b * s;
-            y1[u] = b * c + a * s;
-        }
+    if (!rot) return;
+    float inv = 1.0f;
+    if (p.qk_norm) {
+        ss = wave_sum(ss);
+        inv = 1.0f / sqrtf(ss / (float)p.hd + p.eps);
     }
-    if (is_q || !KV8) {
-        float* dst = is_q ? p.q + (size_t)r * p.hq + h * p.hd
-                          : static_cast<float*>(is_k ? p.kc : p.vc) + tok * p.hkv + kh * p.hd;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int m = lane + 64 * u;
+        if (m >= half) continue;
+        float a = y0[u], b = y1[u];
+        if (p.qk_norm) {
+            a = a * inv * nw[m];
+            b = b * inv * nw[m + half];
+        }
+        const float angle = (float)pos * powf(p.theta, -(float)(2 * m) / (float)p.hd);
+        const float c = cosf(angle), s = sinf(angle);
+        y0[u] = a * c - b * s;
+        y1[u] = b * c + a * s;
+    }
+}
+
+// Appends one key or value head at cache slot `tok`: f32 as is, or (KV8)
+// int8 codes with one scale per (token, kv head), min(max|x|, clip) / 127
+// (1 when that is 0), as paged_kv_append_i8_clipped_batched.wgsl. With KV8
+// the values are replaced by their codes (as floats) and the scale returned,
+// which is what a reader of the cache sees.
+template <bool KV8>
+__device__ __forceinline__ float kv_append(const RopeArgs& p, bool is_k, int kh, size_t tok, int lane, float (&y0)[2],
+                                           float (&y1)[2]) {
+    const int half = p.hd >> 1;
+    if constexpr (!KV8) {
+        float* dst = static_cast<float*>(is_k ? p.kc : p.vc) + tok * p.hkv + kh * p.hd;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int m = lane + 64 * u;
@@ -291,27 +288,63 @@ __global__ __launch_bounds__(64) void qk_rope_append_kernel(RopeArgs p) {
             dst[m] = y0[u];
             dst[m + half] = y1[u];
         }
+        return 1.0f;
+    } else {
+        float mx = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            if (lane + 64 * u < half) mx = fmaxf(mx, fmaxf(fabsf(y0[u]), fabsf(y1[u])));
+        mx = wave_max(mx);
+        float scale = fminf(mx, (is_k ? p.kclip : p.vclip)[kh]) / 127.0f;
+        if (scale == 0.0f) scale = 1.0f;
+        uint8_t* d8 = static_cast<uint8_t*>(is_k ? p.kc : p.vc) + tok * p.hkv + kh * p.hd;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int m = lane + 64 * u;
+            if (m >= half) continue;
+            const uint8_t c0 = kv8_code(y0[u], scale), c1 = kv8_code(y1[u], scale);
+            d8[m] = c0;
+            d8[m + half] = c1;
+            y0[u] = (float)(int8_t)c0;
+            y1[u] = (float)(int8_t)c1;
+        }
+        if (lane == 0) (is_k ? p.ks : p.vs)[tok * p.nkv + kh] = scale;
+        return scale;
+    }
+}
+
+// One wave per (row, head): heads [0,nh) are queries, [nh, nh+nkv) keys,
+// [nh+nkv, nh+2nkv) values. Queries and keys get rope_head; keys and values
+// land in the cache at (seq, pos) (paged_kv_append_batched.wgsl with a
+// contiguous slab per sequence), queries in q.
+template <bool KV8>
+__global__ __launch_bounds__(64) void qk_rope_append_kernel(RopeArgs p) {
+    const int r = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int W = p.hq + 2 * p.hkv;
+    const uint32_t pos = p.pos[r];
+    const size_t tok = (size_t)p.seq[r] * p.max_seq + pos;
+    const bool is_q = h < p.nh, is_k = !is_q && h < p.nh + p.nkv;
+    const int kh = is_q ? 0 : (is_k ? h - p.nh : h - p.nh - p.nkv);
+    const float* src = p.qkv + (size_t)r * W +
+                       (is_q ? h * p.hd : (is_k ? p.hq + kh * p.hd : p.hq + p.hkv + kh * p.hd));
+    float y0[2], y1[2];
+    rope_head(p, src, is_q ? p.qn : p.kn, is_q || is_k, pos, lane, y0, y1);
+    if (!is_q) {
+        (void)kv_append<KV8>(p, is_k, kh, tok, lane, y0, y1);
         return;
     }
-    float mx = 0.0f;
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-        if (lane + 64 * u < half) mx = fmaxf(mx, fmaxf(fabsf(y0[u]), fabsf(y1[u])));
-    mx = wave_max(mx);
-    float scale = fminf(mx, (is_k ? p.kclip : p.vclip)[kh]) / 127.0f;
-    if (scale == 0.0f) scale = 1.0f;
-    uint8_t* d8 = static_cast<uint8_t*>(is_k ? p.kc : p.vc) + tok * p.hkv + kh * p.hd;
+    const int half = p.hd >> 1;
+    float* dst = p.q + (size_t)r * p.hq + h * p.hd;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int m = lane + 64 * u;
         if (m >= half) continue;
-        d8[m] = kv8_code(y0[u], scale);
-        d8[m + half] = kv8_code(y1[u], scale);
+        dst[m] = y0[u];
+        dst[m + half] = y1[u];
     }
-    if (lane == 0) (is_k ? p.ks : p.vs)[tok * p.nkv + kh] = scale;
 }
 
-constexpr int KCH = 32;  // keys per attention workgroup
+constexpr int KCH = ATTN_KCH;  // keys per attention workgroup
 
 struct AttnArgs {
     const float* q;    // [rows, hq]
@@ -325,6 +358,7 @@ struct AttnArgs {
     float* part_ml;    // [rows, nh, splits, 2]   (m, sum_k exp(s_k - m))
     int nh, nkv, hd, hq, hkv, max_seq, splits;
     float scale;
+    RopeArgs ro;       // ROPE: the q|k|v row, norms and cache of this step
 };
 
 // Causal GQA, split over the keys (flash-decoding): one workgroup per (row,
@@ -343,44 +377,123 @@ __device__ __forceinline__ float4 i8x4(uint32_t w) {
                        (float)(int8_t)((w >> 16) & 0xffu), (float)(int8_t)(w >> 24));
 }
 
-template <bool KV8>
+// ROPE (decode, one new token per row, rows in distinct sequences): the
+// workgroup also does this step's qk_rope_append work for its kv head. Every
+// workgroup rotates the G query heads it reads; the one whose chunk ends at
+// pos (the new key) also rotates the new key, appends key and value to the
+// cache, and takes them from LDS instead of reading the cache back. Same
+// arithmetic, in the same order, as the separate kernels.
+template <bool KV8, bool ROPE = false>
 __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     __shared__ float qs[MAX_GROUP * 256];
     __shared__ float es[MAX_GROUP * KCH];
     __shared__ float ml[MAX_GROUP * 2];
     __shared__ float ksc[KCH], vsc[KCH];  // KV8: this chunk's per-key scales
+    __shared__ __attribute__((aligned(16))) float newkv[2][256];  // ROPE: the new key and value (KV8: codes)
+    __shared__ float newsc[2];
+    // This chunk's V rows read from the cache: f32, or KV8 codes as bytes.
+    __shared__ __attribute__((aligned(16))) float vls[KCH * 256];
     const int r = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z, tid = threadIdx.x;
     const int t = (int)p.pos[r] + 1;
     const int j0 = sp * KCH;
     if (j0 >= t) return;
     const int n = min(KCH, t - j0);
     const int G = p.nh / p.nkv;
+    const bool last = ROPE && j0 + n == t;  // this chunk ends at the new key
+    const int nc = last ? n - 1 : n;        // keys read from the cache
     const size_t tok0 = (size_t)p.seq[r] * p.max_seq + j0;  // cache slot of this chunk's first key
-    for (int i = tid; i < G * p.hd; i += RT) qs[i] = p.q[(size_t)r * p.hq + (size_t)kh * G * p.hd + i];
-    if constexpr (KV8) {
-        if (tid < KCH) ksc[tid] = tid < n ? p.ks[(tok0 + tid) * p.nkv + kh] : 0.0f;
-        else if (tid < 2 * KCH) vsc[tid - KCH] = tid - KCH < n ? p.vs[(tok0 + tid - KCH) * p.nkv + kh] : 0.0f;
-    }
-    __syncthreads();
     const size_t base = (size_t)p.seq[r] * p.max_seq * p.hkv + (size_t)kh * p.hd;
-    {
-        const int kk = tid >> 3, l8 = tid & 7;
-        float acc[MAX_GROUP];
+
+    // Every cache read of the chunk is issued first, so its latency overlaps
+    // the query rotation: this lane's K pieces (8 lanes per key, float4
+    // along head_dim, at most 8 pieces for head_dim <= 256), the V rows
+    // (4 elements per piece) and the KV8 scales.
+    const int kk = tid >> 3, l8 = tid & 7;
+    constexpr int KP = 256 / 32;
+    float4 kv[KP];
+    const size_t kro = base + (size_t)(j0 + kk) * p.hkv;
 #pragma unroll
-        for (int g = 0; g < MAX_GROUP; ++g) acc[g] = 0.0f;
-        // All of this lane's K pieces (head_dim <= 256: at most 8) are loaded
-        // before the first product.
-        constexpr int KP = 256 / 32;
-        float4 kv[KP];
-        const size_t kro = base + (size_t)(j0 + kk) * p.hkv;
+    for (int u = 0; u < KP; ++u) {
+        const int c = l8 * 4 + 32 * u;
+        kv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (kk < nc && c < p.hd)
+            kv[u] = KV8 ? i8x4(*reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.kc) + kro + c))
+                        : *reinterpret_cast<const float4*>(static_cast<const float*>(p.kc) + kro + c);
+    }
+    constexpr int VPT = KCH * 256 / 4 / RT;
+    const int hd4 = p.hd >> 2;
+    const size_t vbo = base + (size_t)j0 * p.hkv;
+    float4 vf[KV8 ? 1 : VPT];
+    uint32_t v8[KV8 ? VPT : 1];
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+        const int q = tid + u * RT;
+        if (q >= nc * hd4) break;
+        const int k = q / hd4, c = (q - k * hd4) * 4;
+        if constexpr (KV8) v8[u] = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.vc) + vbo + (size_t)k * p.hkv + c);
+        else vf[u] = *reinterpret_cast<const float4*>(static_cast<const float*>(p.vc) + vbo + (size_t)k * p.hkv + c);
+    }
+    float scl = 0.0f;  // KV8: ksc[tid] (tid < KCH) or vsc[tid - KCH]
+    if constexpr (KV8) {
+        const int k = tid < KCH ? tid : tid - KCH;
+        if (tid < 2 * KCH && k < nc) scl = (tid < KCH ? p.ks : p.vs)[(tok0 + k) * p.nkv + kh];
+    }
+
+    if constexpr (ROPE) {
+        const int wave = tid >> 6, lane = tid & 63, half = p.hd >> 1;
+        const RopeArgs& ro = p.ro;
+        const uint32_t pos = p.pos[r];
+        const float* row = ro.qkv + (size_t)r * (ro.hq + 2 * ro.hkv);
+        for (int h = wave; h < G + 2; h += RT / 64) {
+            if (h >= G && !last) continue;
+            float y0[2], y1[2];
+            float* dst;
+            if (h < G) {
+                rope_head(ro, row + (size_t)(kh * G + h) * p.hd, ro.qn, true, pos, lane, y0, y1);
+                dst = qs + h * p.hd;
+            } else {
+                const bool is_k = h == G;
+                rope_head(ro, row + ro.hq + (is_k ? 0 : ro.hkv) + kh * p.hd, ro.kn, is_k, pos, lane, y0, y1);
+                const float sc = kv_append<KV8>(ro, is_k, kh, (size_t)p.seq[r] * p.max_seq + pos, lane, y0, y1);
+                dst = newkv[is_k ? 0 : 1];
+                if (lane == 0) newsc[is_k ? 0 : 1] = sc;
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int m = lane + 64 * u;
+                if (m >= half) continue;
+                dst[m] = y0[u];
+                dst[m + half] = y1[u];
+            }
+        }
+    } else {
+        for (int i = tid; i < G * p.hd; i += RT) qs[i] = p.q[(size_t)r * p.hq + (size_t)kh * G * p.hd + i];
+    }
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) {
+        const int q = tid + u * RT;
+        if (q >= nc * hd4) break;
+        const int k = q / hd4, c = (q - k * hd4) * 4;
+        if constexpr (KV8) *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(vls) + k * p.hd + c) = v8[u];
+        else *reinterpret_cast<float4*>(vls + k * p.hd + c) = vf[u];
+    }
+    __syncthreads();  // qs, newkv, newsc, vls
+    if constexpr (KV8) {
+        if (tid < KCH) ksc[tid] = tid < n ? (tid < nc ? scl : newsc[0]) : 0.0f;
+        else if (tid < 2 * KCH) vsc[tid - KCH] = tid - KCH < n ? (tid - KCH < nc ? scl : newsc[1]) : 0.0f;
+    }
+    if (last && kk == n - 1) {
 #pragma unroll
         for (int u = 0; u < KP; ++u) {
             const int c = l8 * 4 + 32 * u;
-            kv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (kk < n && c < p.hd)
-                kv[u] = KV8 ? i8x4(*reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.kc) + kro + c))
-                            : *reinterpret_cast<const float4*>(static_cast<const float*>(p.kc) + kro + c);
+            if (c < p.hd) kv[u] = *reinterpret_cast<const float4*>(&newkv[0][c]);
         }
+    }
+    if constexpr (KV8) __syncthreads();  // ksc, vsc
+    {
+        float acc[MAX_GROUP];
+#pragma unroll
+        for (int g = 0; g < MAX_GROUP; ++g) acc[g] = 0.0f;
 #pragma unroll
         for (int u = 0; u < KP; ++u) {
             const int c = l8 * 4 + 32 * u;
@@ -424,18 +537,18 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
         }
     }
     __syncthreads();
-    const size_t vbo = base + (size_t)j0 * p.hkv;
     for (int i = tid; i < G * p.hd; i += RT) {
         const int g = i / p.hd, d = i - g * p.hd;
         float acc = 0.0f;
         if constexpr (KV8) {
-            const int8_t* vb = reinterpret_cast<const int8_t*>(p.vc) + vbo;
+            const int8_t* vb = reinterpret_cast<const int8_t*>(vls);
 #pragma unroll 8
-            for (int k = 0; k < n; ++k) acc += es[g * KCH + k] * (float)vb[(size_t)k * p.hkv + d] * vsc[k];
+            for (int k = 0; k < nc; ++k) acc += es[g * KCH + k] * (float)vb[k * p.hd + d] * vsc[k];
+            if (last) acc += es[g * KCH + nc] * newkv[1][d] * vsc[nc];
         } else {
-            const float* vb = static_cast<const float*>(p.vc) + vbo;
 #pragma unroll 8
-            for (int k = 0; k < n; ++k) acc += es[g * KCH + k] * vb[(size_t)k * p.hkv + d];
+            for (int k = 0; k < nc; ++k) acc += es[g * KCH + k] * vls[k * p.hd + d];
+            if (last) acc += es[g * KCH + nc] * newkv[1][d];
         }
         const size_t slot = ((size_t)r * p.nh + kh * G + g) * p.splits + sp;
         p.part_o[slot * p.hd + d] = acc;
@@ -455,49 +568,12 @@ __global__ __launch_bounds__(RT) void attn_combine_quant_kernel(const float* par
                                                                 int splits, float* sx, uint32_t* xq) {
     __shared__ float red[RT / 64];
     const int r = blockIdx.x;
-    const int ns = ((int)pos[r] + KCH) / KCH;  // chunks holding positions 0..pos
     const int q4 = hq >> 2;
     float4 y[GQ];
 #pragma unroll
     for (int g = 0; g < GQ; ++g) {
         const int i = threadIdx.x + g * RT;
-        y[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (i >= q4) continue;
-        const int e = i * 4, h = e / hd, d = e - h * hd;
-        const size_t hs = ((size_t)r * nh + h) * splits;
-        // Loads in batches of SB splits, all issued before use (one memory
-        // round trip per batch rather than per split).
-        constexpr int SB = 8;
-        float M = -INFINITY;
-        for (int s0 = 0; s0 < ns; s0 += SB) {
-            float mv[SB];
-#pragma unroll
-            for (int j = 0; j < SB; ++j) mv[j] = s0 + j < ns ? part_ml[2 * (hs + s0 + j)] : -INFINITY;
-#pragma unroll
-            for (int j = 0; j < SB; ++j) M = fmaxf(M, mv[j]);
-        }
-        float L = 0.0f;
-        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int s0 = 0; s0 < ns; s0 += SB) {
-            float mv[SB], lv[SB];
-            float4 ov[SB];
-#pragma unroll
-            for (int j = 0; j < SB; ++j) {
-                const bool live = s0 + j < ns;
-                mv[j] = live ? part_ml[2 * (hs + s0 + j)] : -INFINITY;
-                lv[j] = live ? part_ml[2 * (hs + s0 + j) + 1] : 0.0f;
-                ov[j] = live ? *reinterpret_cast<const float4*>(part_o + (hs + s0 + j) * hd + d) : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-#pragma unroll
-            for (int j = 0; j < SB; ++j) {
-                if (s0 + j >= ns) continue;
-                const float w = expf(mv[j] - M);
-                L += lv[j] * w;
-                o = make_float4(o.x + ov[j].x * w, o.y + ov[j].y * w, o.z + ov[j].z * w, o.w + ov[j].w * w);
-            }
-        }
-        const float inv = 1.0f / L;
-        y[g] = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+        y[g] = i < q4 ? attn_combine_row4(part_o, part_ml, r, pos[r], nh, hd, splits, i) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     quant_row<GQ>(y, q4, red, sx + r, xq + (size_t)r * q4);
 }
@@ -640,6 +716,8 @@ struct bh_qwen3 {
     uint32_t batch = 0, prompt_len = 0, decoded = 0;
     hipGraphExec_t graph = nullptr;
     uint32_t graph_batch = 0;
+    bool nofuse = false;        // BH_QWEN3_UNFUSED for the current decode call
+    bool graph_nofuse = false;  // the mode the captured step was recorded in
     std::vector<void*> allocs;
 
     ~bh_qwen3() {
@@ -764,7 +842,8 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
         // Residual stream ping-pongs between res and res2 (two swaps per
         // layer): a fused producer's workgroup 0 writes the new residual while
         // other workgroups still read the old one.
-        const bool fuse = fused_ok(e, rows, d, (int)e->W) && fused_ok(e, rows, d, 2 * ff) && fused_ok(e, rows, ff, d);
+        const bool fuse = !e->nofuse && fused_ok(e, rows, d, (int)e->W) && fused_ok(e, rows, d, 2 * ff) &&
+                          fused_ok(e, rows, ff, d);
         if (fuse) {
             BH_HIP(launch_gemv_i8_pre(e->stream, 3, l == 0 ? tok : nullptr, e->emb, l == 0 ? nullptr : cur,
                                       l == 0 ? nullptr : e->proj, Ly.ln1, nxt, c.rms_eps, Ly.wqkv, Ly.sqkv, e->qkv,
@@ -793,14 +872,26 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
         RopeArgs ra{e->qkv, e->q, kc, vc, ksl, vsl, e->kclip + (size_t)l * nkv, e->vclip + (size_t)l * nkv, Ly.qn,
                     Ly.kn, pos, seq, nh, nkv, hd, (int)e->hq, (int)e->hkv, (int)e->max_seq, (int)c.qk_norm,
                     c.rms_eps, c.rope_theta};
-        if (c.kv_int8) qk_rope_append_kernel<true><<<dim3(rows, nh + 2 * nkv), 64, 0, e->stream>>>(ra);
-        else qk_rope_append_kernel<false><<<dim3(rows, nh + 2 * nkv), 64, 0, e->stream>>>(ra);
-        BH_HIP(hipGetLastError(), "qk_rope_append launch");
         AttnArgs aa{e->q, kc, vc, ksl, vsl, pos, seq, e->part_o, e->part_ml, nh, nkv, hd, (int)e->hq,
-                    (int)e->hkv, (int)e->max_seq, splits, scale};
-        if (c.kv_int8) attn_split_kernel<true><<<dim3(rows, nkv, splits), RT, 0, e->stream>>>(aa);
-        else attn_split_kernel<false><<<dim3(rows, nkv, splits), RT, 0, e->stream>>>(aa);
-        BH_HIP(hipGetLastError(), "attention launch");
+                    (int)e->hkv, (int)e->max_seq, splits, scale, ra};
+        const dim3 agrid(rows, nkv, splits);
+        if (decode && !e->nofuse) {
+            // One new token per row, each row its own sequence: the rotation
+            // and cache append run inside the attention launch.
+            if (c.kv_int8) attn_split_kernel<true, true><<<agrid, RT, 0, e->stream>>>(aa);
+            else attn_split_kernel<false, true><<<agrid, RT, 0, e->stream>>>(aa);
+            BH_HIP(hipGetLastError(), "attention launch");
+        } else {
+            if (c.kv_int8) qk_rope_append_kernel<true><<<dim3(rows, nh + 2 * nkv), 64, 0, e->stream>>>(ra);
+            else qk_rope_append_kernel<false><<<dim3(rows, nh + 2 * nkv), 64, 0, e->stream>>>(ra);
+            BH_HIP(hipGetLastError(), "qk_rope_append launch");
+            if (c.kv_int8) attn_split_kernel<true><<<agrid, RT, 0, e->stream>>>(aa);
+            else attn_split_kernel<false><<<agrid, RT, 0, e->stream>>>(aa);
+            BH_HIP(hipGetLastError(), "attention launch");
+        }
+        // (Merging inside the output projection's prologue measured 4x slower
+        // than this separate launch: every GEMV workgroup re-read all the
+        // partials of the row.)
         BH_TRY(launch_combine_quant(e, rows, splits));
         BH_TRY(launch_linear(e, Ly.wo, Ly.so, e->proj, rows, (int)e->hq, d));
         if (fuse) {
@@ -1190,6 +1281,7 @@ int bh_qwen3_prefill(bh_qwen3* e, const uint32_t* tokens, uint32_t batch, uint32
     if (!batch || batch > e->max_batch || !len || len > e->max_seq)
         return fail(BH_ERR_INVALID, "bh_qwen3_prefill: batch %u (max %u), len %u (max %u)", batch, e->max_batch, len,
                     e->max_seq);
+    e->nofuse = false;  // the decode flag does not carry over
     for (uint64_t i = 0; i < (uint64_t)batch * len; ++i)
         if (tokens[i] >= e->c.vocab) return fail(BH_ERR_INVALID, "bh_qwen3_prefill: token %u outside the vocabulary (%u)", tokens[i], e->c.vocab);
     (void)hipSetDevice(e->device);
@@ -1239,11 +1331,12 @@ int bh_qwen3_decode(bh_qwen3* e, uint32_t steps, uint32_t flags, uint32_t* out) 
     if (!steps) return BH_OK;
     (void)hipSetDevice(e->device);
     const int b = (int)e->batch;
+    e->nofuse = (flags & BH_QWEN3_UNFUSED) != 0;
     if (flags & BH_QWEN3_EAGER) {
         for (uint32_t s = 0; s < steps; ++s)
             BH_TRY(run_rows(e, b, e->tok_dec, e->pos_dec, e->seq_dec, b, nullptr, true, (int)e->max_splits));
     } else {
-        if (!e->graph || e->graph_batch != e->batch) {
+        if (!e->graph || e->graph_batch != e->batch || e->graph_nofuse != e->nofuse) {
             if (e->graph) {
                 (void)hipGraphExecDestroy(e->graph);
                 e->graph = nullptr;
@@ -1262,6 +1355,7 @@ int bh_qwen3_decode(bh_qwen3* e, uint32_t steps, uint32_t flags, uint32_t* out) 
             (void)hipGraphDestroy(g);
             BH_HIP(ie, "graph instantiate");
             e->graph_batch = e->batch;
+            e->graph_nofuse = e->nofuse;
         }
         for (uint32_t s = 0; s < steps; ++s) BH_HIP(hipGraphLaunch(e->graph, e->stream), "graph launch");
     }

@@ -18,6 +18,7 @@ QWEN3_0_6B = dict(vocab=151936, n_layers=28, d_model=1024, n_heads=16, n_kv_head
 """QwenConfig::qwen3_0_6b (crates/qwen3/src/config.rs:100-118)."""
 
 EAGER = 1
+UNFUSED = 2
 
 
 class Qwen3Engine:
@@ -88,10 +89,12 @@ class Qwen3Engine:
         self.batch = batch
         return nxt
 
-    def decode(self, steps, eager=False):
-        """`steps` greedy steps -> tokens [steps, batch]."""
+    def decode(self, steps, eager=False, unfused=False):
+        """`steps` greedy steps -> tokens [steps, batch]. `unfused`: every
+        producer as its own kernel (bit-identical results; validation aid)."""
         out = np.zeros((steps, self.batch), np.uint32)
-        check(load().bh_qwen3_decode(self._h, steps, EAGER if eager else 0, out.ctypes.data))
+        flags = (EAGER if eager else 0) | (UNFUSED if unfused else 0)
+        check(load().bh_qwen3_decode(self._h, steps, flags, out.ctypes.data))
         return out
 
     def logits(self):
@@ -99,8 +102,8 @@ class Qwen3Engine:
         check(load().bh_qwen3_logits(self._h, out.ctypes.data, out.size))
         return out
 
-    def generate(self, prompts, steps, eager=False):
+    def generate(self, prompts, steps, eager=False, unfused=False):
         """Greedy tokens [(steps+1), batch]: row 0 from the prefill, then `steps` decode steps."""
         first = self.prefill(prompts)
-        rest = self.decode(steps, eager) if steps else np.zeros((0, len(first)), np.uint32)
+        rest = self.decode(steps, eager, unfused) if steps else np.zeros((0, len(first)), np.uint32)
         return np.vstack([first[None, :], rest])

@@ -386,8 +386,12 @@ int bh_qwen3_prefill(bh_qwen3* e, const uint32_t* tokens, uint32_t batch, uint32
 /* `steps` greedy decode steps of every live sequence: each step feeds the
  * previous token back on the device (no host round trip) and appends the new
  * one. out[steps][batch] receives the generated tokens. The step is captured
- * once in a HIP graph and replayed (flags & BH_QWEN3_EAGER: launch eagerly). */
+ * once in a HIP graph and replayed (flags & BH_QWEN3_EAGER: launch eagerly).
+ * flags & BH_QWEN3_UNFUSED: run every producer (norm, rotation + cache append,
+ * attention merge, SwiGLU) as its own kernel instead of inside its consumer;
+ * the results are the same bit for bit (a validation aid). */
 #define BH_QWEN3_EAGER 1u
+#define BH_QWEN3_UNFUSED 2u
 int bh_qwen3_decode(bh_qwen3* e, uint32_t steps, uint32_t flags, uint32_t* out);
 /* Logits [batch, vocab] f32 of the most recent head evaluation (prefill or
  * the last decode step). */

@@ -220,3 +220,40 @@ def test_kv_int8_chunking_graph_and_clip(gpu):
     assert not np.array_equal(a.logits(), c.logits())
     for e in (a, b, c):
         e.close()
+
+
+@pytest.mark.parametrize("batch,kv_int8", [(1, 0), (3, 0), (6, 0), (2, 1), (6, 1)])
+def test_fused_decode_is_bit_identical_to_unfused(gpu, batch, kv_int8):
+    """Decode with the producers inside their consumers (rotation + cache
+    append inside attention; merge, RMSNorm and SwiGLU inside the following
+    GEMV's prologue; up to 4 rows) against every producer as its own kernel:
+    tokens, logits and the KV cache contents they leave must agree exactly.
+    Batch 6 keeps the separate GEMV producers but still fuses the rotation."""
+    cfg = dict(SMALL, kv_int8=kv_int8)
+    w = scaled_weights(cfg, seed=31 + batch)
+    prompts = np.random.default_rng(batch).integers(0, cfg["vocab"], size=(batch, 37))
+    a = engine_for(cfg, w, batch, 96)
+    b = engine_for(cfg, w, batch, 96)
+    ta = a.generate(prompts, 40)
+    tb = b.generate(prompts, 40, eager=True, unfused=True)
+    assert (ta == tb).all()
+    assert np.array_equal(a.logits(), b.logits())
+    # Both continue from caches the two modes wrote: still identical.
+    assert (a.decode(5, eager=True, unfused=True) == b.decode(5)).all()
+    assert np.array_equal(a.logits(), b.logits())
+    a.close()
+    b.close()
+
+
+def test_qwen3_0_6b_fused_decode_matches_unfused(gpu):
+    """The fused decode kernels at the config-3 shapes (head_dim 128, K=2048
+    merge prologue, 16 waves per GEMV workgroup) against the separate ones."""
+    prompts = np.random.default_rng(5).integers(0, QWEN3_0_6B["vocab"], size=(2, 40))
+    out = []
+    for unfused in (False, True):
+        e = Qwen3Engine(QWEN3_0_6B, 2, 64, max_rows=128)
+        e.init_random(11)
+        out.append((e.generate(prompts, 6, eager=unfused, unfused=unfused), e.logits()))
+        e.close()
+    assert (out[0][0] == out[1][0]).all()
+    assert np.array_equal(out[0][1], out[1][1])
