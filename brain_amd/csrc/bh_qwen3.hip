@@ -385,20 +385,26 @@ __device__ __forceinline__ float4 i8x4(uint32_t w) {
 // arithmetic, in the same order, as the separate kernels.
 template <bool KV8, bool ROPE = false>
 __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
-    __shared__ float qs[MAX_GROUP * 256];
     __shared__ float es[MAX_GROUP * KCH];
     __shared__ float ml[MAX_GROUP * 2];
     __shared__ float ksc[KCH], vsc[KCH];  // KV8: this chunk's per-key scales
-    __shared__ __attribute__((aligned(16))) float newkv[2][256];  // ROPE: the new key and value (KV8: codes)
     __shared__ float newsc[2];
-    // This chunk's V rows read from the cache: f32, or KV8 codes as bytes.
-    __shared__ __attribute__((aligned(16))) float vls[KCH * 256];
+    // Sized by attn_lds_bytes: the G query heads, the new key and value
+    // (ROPE; KV8: codes), and this chunk's V rows read from the cache (f32,
+    // or KV8 codes as bytes). Sized to head_dim, not its 256 maximum, so
+    // more workgroups fit on a CU.
+    extern __shared__ __attribute__((aligned(16))) float attn_dyn[];
     const int r = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z, tid = threadIdx.x;
+
     const int t = (int)p.pos[r] + 1;
     const int j0 = sp * KCH;
     if (j0 >= t) return;
     const int n = min(KCH, t - j0);
     const int G = p.nh / p.nkv;
+    float* qs = attn_dyn;
+    float* nk = qs + G * p.hd;
+    float* nv = nk + p.hd;
+    float* vls = nv + p.hd;
     const bool last = ROPE && j0 + n == t;  // this chunk ends at the new key
     const int nc = last ? n - 1 : n;        // keys read from the cache
     const size_t tok0 = (size_t)p.seq[r] * p.max_seq + j0;  // cache slot of this chunk's first key
@@ -420,11 +426,15 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
             kv[u] = KV8 ? i8x4(*reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.kc) + kro + c))
                         : *reinterpret_cast<const float4*>(static_cast<const float*>(p.kc) + kro + c);
     }
-    constexpr int VPT = KCH * 256 / 4 / RT;
+    // V is staged through LDS on the decode path only: prefill launches
+    // thousands of these workgroups, and the staging registers cost them
+    // occupancy (measured slower there).
+    constexpr bool VST = ROPE;
+    constexpr int VPT = VST ? KCH * 256 / 4 / RT : 0;
     const int hd4 = p.hd >> 2;
     const size_t vbo = base + (size_t)j0 * p.hkv;
-    float4 vf[KV8 ? 1 : VPT];
-    uint32_t v8[KV8 ? VPT : 1];
+    float4 vf[KV8 || !VST ? 1 : VPT];
+    uint32_t v8[KV8 && VST ? VPT : 1];
 #pragma unroll
     for (int u = 0; u < VPT; ++u) {
         const int q = tid + u * RT;
@@ -455,7 +465,7 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
                 const bool is_k = h == G;
                 rope_head(ro, row + ro.hq + (is_k ? 0 : ro.hkv) + kh * p.hd, ro.kn, is_k, pos, lane, y0, y1);
                 const float sc = kv_append<KV8>(ro, is_k, kh, (size_t)p.seq[r] * p.max_seq + pos, lane, y0, y1);
-                dst = newkv[is_k ? 0 : 1];
+                dst = is_k ? nk : nv;
                 if (lane == 0) newsc[is_k ? 0 : 1] = sc;
             }
 #pragma unroll
@@ -477,7 +487,7 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
         if constexpr (KV8) *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(vls) + k * p.hd + c) = v8[u];
         else *reinterpret_cast<float4*>(vls + k * p.hd + c) = vf[u];
     }
-    __syncthreads();  // qs, newkv, newsc, vls
+    __syncthreads();  // qs, nk, nv, newsc, vls
     if constexpr (KV8) {
         if (tid < KCH) ksc[tid] = tid < n ? (tid < nc ? scl : newsc[0]) : 0.0f;
         else if (tid < 2 * KCH) vsc[tid - KCH] = tid - KCH < n ? (tid - KCH < nc ? scl : newsc[1]) : 0.0f;
@@ -486,7 +496,7 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
 #pragma unroll
         for (int u = 0; u < KP; ++u) {
             const int c = l8 * 4 + 32 * u;
-            if (c < p.hd) kv[u] = *reinterpret_cast<const float4*>(&newkv[0][c]);
+            if (c < p.hd) kv[u] = *reinterpret_cast<const float4*>(nk + c);
         }
     }
     if constexpr (KV8) __syncthreads();  // ksc, vsc
@@ -540,15 +550,18 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     for (int i = tid; i < G * p.hd; i += RT) {
         const int g = i / p.hd, d = i - g * p.hd;
         float acc = 0.0f;
+        // Cache rows from LDS (VST) or straight from the cache, same order.
+        const size_t vstride = VST ? (size_t)p.hd : (size_t)p.hkv;
         if constexpr (KV8) {
-            const int8_t* vb = reinterpret_cast<const int8_t*>(vls);
+            const int8_t* vb = VST ? reinterpret_cast<const int8_t*>(vls) : reinterpret_cast<const int8_t*>(p.vc) + vbo;
 #pragma unroll 8
-            for (int k = 0; k < nc; ++k) acc += es[g * KCH + k] * (float)vb[k * p.hd + d] * vsc[k];
-            if (last) acc += es[g * KCH + nc] * newkv[1][d] * vsc[nc];
+            for (int k = 0; k < nc; ++k) acc += es[g * KCH + k] * (float)vb[k * vstride + d] * vsc[k];
+            if (last) acc += es[g * KCH + nc] * nv[d] * vsc[nc];
         } else {
+            const float* vb = VST ? vls : static_cast<const float*>(p.vc) + vbo;
 #pragma unroll 8
-            for (int k = 0; k < nc; ++k) acc += es[g * KCH + k] * vls[k * p.hd + d];
-            if (last) acc += es[g * KCH + nc] * newkv[1][d];
+            for (int k = 0; k < nc; ++k) acc += es[g * KCH + k] * vb[k * vstride + d];
+            if (last) acc += es[g * KCH + nc] * nv[d];
         }
         const size_t slot = ((size_t)r * p.nh + kh * G + g) * p.splits + sp;
         p.part_o[slot * p.hd + d] = acc;
@@ -875,18 +888,20 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
         AttnArgs aa{e->q, kc, vc, ksl, vsl, pos, seq, e->part_o, e->part_ml, nh, nkv, hd, (int)e->hq,
                     (int)e->hkv, (int)e->max_seq, splits, scale, ra};
         const dim3 agrid(rows, nkv, splits);
+        const size_t alds_pre = ((size_t)(nh / nkv) * hd + 2 * hd) * 4;                     // no V staging
+        const size_t alds = alds_pre + (size_t)KCH * hd * (c.kv_int8 ? 1 : 4);                 // decode
         if (decode && !e->nofuse) {
             // One new token per row, each row its own sequence: the rotation
             // and cache append run inside the attention launch.
-            if (c.kv_int8) attn_split_kernel<true, true><<<agrid, RT, 0, e->stream>>>(aa);
-            else attn_split_kernel<false, true><<<agrid, RT, 0, e->stream>>>(aa);
+            if (c.kv_int8) attn_split_kernel<true, true><<<agrid, RT, alds, e->stream>>>(aa);
+            else attn_split_kernel<false, true><<<agrid, RT, alds, e->stream>>>(aa);
             BH_HIP(hipGetLastError(), "attention launch");
         } else {
             if (c.kv_int8) qk_rope_append_kernel<true><<<dim3(rows, nh + 2 * nkv), 64, 0, e->stream>>>(ra);
             else qk_rope_append_kernel<false><<<dim3(rows, nh + 2 * nkv), 64, 0, e->stream>>>(ra);
             BH_HIP(hipGetLastError(), "qk_rope_append launch");
-            if (c.kv_int8) attn_split_kernel<true><<<agrid, RT, 0, e->stream>>>(aa);
-            else attn_split_kernel<false><<<agrid, RT, 0, e->stream>>>(aa);
+            if (c.kv_int8) attn_split_kernel<true><<<agrid, RT, alds_pre, e->stream>>>(aa);
+            else attn_split_kernel<false><<<agrid, RT, alds_pre, e->stream>>>(aa);
             BH_HIP(hipGetLastError(), "attention launch");
         }
         // (Merging inside the output projection's prologue measured 4x slower
