@@ -772,7 +772,8 @@ enum TileCfg {
     TILE_128 = 1,     // 128x128, 4 waves of 64x64, 4 stages
     TILE_64x128 = 2,  // 64x128, 4 waves of 32x64, 4 stages
     TILE_64 = 3,      // 64x64, 4 waves of 32x32, 4 stages
-    TILE_64_DEEP = 4  // 64x64 with 8 stages in flight (long K on a few tiles)
+    TILE_64_DEEP = 4,  // 64x64 with 8 stages in flight (long K on a few tiles)
+    TILE_256x128 = 5   // 256x128, 8 waves of 64x64, 4 stages
 };
 
 struct TileChoice {
@@ -824,12 +825,13 @@ static int choose_splits(long tiles, double per_stage, int m, int kg, int n) {
 
 // Pick the tile that finishes first on 256 CUs.
 //  - Enough 128x128 tiles to fill the chip: a launch runs in rounds of 256
-//    workgroups, so its time is ~ rounds x (time of one tile). A 256x256 tile
-//    does 4x the work of a 128x128 one at ~1.25x its efficiency (half the
-//    LDS-staging bytes per op), hence the costs 4 * ceil(tiles256 / 256) and
-//    1.25 * ceil(tiles128 / 256); the smaller wins (e.g. 8192x1024x3072 runs
-//    384 big tiles, 2 rounds with one half empty, or 1536 small ones in 6
-//    full rounds).
+//    workgroups, so its time is ~ rounds x (time of one tile). Per round, in
+//    units of a 128x128 tile's time, measured on MI355X: 256x256 costs 4.0
+//    (4x the work at ~1.25x the efficiency: half the LDS-staging bytes per
+//    op), 256x128 on 8 waves 2.2, 128x128 1.25. The cheapest of
+//    4.0 * ceil(t256/256), 2.2 * ceil(t256x128/256) and 1.25 * ceil(t128/256)
+//    wins (e.g. 8192x1024x3072: 2 rounds of 256x256, one half empty, 8.0; 3
+//    rounds of 256x128, 6.6; 6 rounds of 128x128, 7.5).
 //  - Fewer 128x128 tiles than CUs: smaller tiles put more CUs to work. A lone
 //    tile's time is set by how fast one CU streams its operands, so halving a
 //    tile side nearly halves its time. Measured on the configs[2] shapes at
@@ -839,13 +841,16 @@ static int choose_splits(long tiles, double per_stage, int m, int kg, int n) {
 static TileChoice choose_tiles(int m, int kg, int n) {
     constexpr long CUS = 256;
     const long t256 = (long)((m + 255) / 256) * ((n + 255) / 256);
+    const long t2x1 = (long)((m + 255) / 256) * ((n + 127) / 128);
     const long t128 = (long)((m + 127) / 128) * ((n + 127) / 128);
     const long t64 = (long)((m + 63) / 64) * ((n + 63) / 64);
     const long stages = (long)kg * 4 / 64;
     const double c256 = 4.0 * (double)((t256 + CUS - 1) / CUS);
+    const double c2x1 = 2.2 * (double)((t2x1 + CUS - 1) / CUS);
     const double c128 = 1.25 * (double)((t128 + CUS - 1) / CUS);
     TileChoice tc{TILE_128, 1};
-    if (c256 <= c128) tc.cfg = TILE_256;
+    if (c256 <= c2x1 && c256 <= c128) tc.cfg = TILE_256;
+    else if (c2x1 < c128) tc.cfg = TILE_256x128;
     else if (t128 >= CUS) tc.cfg = TILE_128;
     else if (t128 >= CUS / 2) tc.cfg = TILE_64x128;
     else tc.cfg = (t64 <= CUS && stages >= 32) ? TILE_64_DEEP : TILE_64;
@@ -901,6 +906,7 @@ static hipError_t go_small(hipStream_t s, int cfg, const GemmArgs& a) {
         case TILE_64x128: return go_dma<64, 128, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
         case TILE_64: return go_dma<64, 64, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
         case TILE_64_DEEP: return go_dma<64, 64, 2, 2, 8, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
+        case TILE_256x128: return go_dma<256, 128, 4, 2, 4, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
         default: return go_dma<128, 128, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
     }
 }
