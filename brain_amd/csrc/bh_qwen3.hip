@@ -572,6 +572,186 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     }
 }
 
+// Prefill attention over query blocks: one workgroup per (sequence, block
+// of QB consecutive rows of that sequence, chunk of 32 keys; kv head), QB*G =
+// 32 query vectors (row i, head g). The chunk's K and V go through LDS once
+// for all 32 queries (attn_split_kernel reloads them per row). Like the split
+// kernel it writes, per (row, head, chunk), the chunk's softmax statistics
+// (max m, sum l) and its unnormalized weighted sum of V; attn_combine_quant
+// merges the chunks. A query's numbers depend only on its own row and the
+// chunk, not on the rows it shares a block with, so any chunking of the
+// prompt gives the same bits.
+constexpr int PQ = 32;  // query vectors per prefill workgroup
+template <bool KV8, int HD>
+__global__ __launch_bounds__(RT) void attn_prefill_kernel(AttnArgs p, int rows_per_seq) {
+    extern __shared__ __attribute__((aligned(16))) float pf_dyn[];
+    constexpr int hd = HD, hd4 = hd >> 2, ks = hd + 4;  // K rows padded for the LDS banks
+    constexpr int NP = PQ * hd / 4 / RT;                // float4 pieces per thread (Q, K, V alike)
+    static_assert(NP >= 1 && NP * RT * 4 == PQ * hd && KCH * hd4 == NP * RT, "whole pieces per thread");
+    constexpr int ow = hd >> 3;                         // head_dim slice per thread in P.V
+    const int G = p.nh / p.nkv, QB = PQ / G;
+    const int nqb = (rows_per_seq + QB - 1) / QB;
+    const int sp = blockIdx.x % p.splits, bq = blockIdx.x / p.splits;
+    const int b = bq / nqb, qb = bq - b * nqb, kh = blockIdx.y, tid = threadIdx.x;
+    const int i0 = qb * QB, nrow = min(QB, rows_per_seq - i0);
+    const int r0 = b * rows_per_seq + i0;  // first row of the block
+    const int j0 = sp * KCH;
+    // Rows are consecutive positions: the last row holds the largest.
+    const int maxpos = (int)p.pos[r0 + nrow - 1];
+    if (j0 > maxpos) return;
+    const int nk = min(KCH, maxpos + 1 - j0);
+    float* Qs = pf_dyn;         // [PQ][hd]
+    float* Ks = Qs + PQ * hd;   // [32][hd + 4]
+    float* Vs = Ks + KCH * ks;  // [32][hd]
+    __shared__ float Ps[PQ][KCH + 1];
+    __shared__ float mls[PQ][2];
+    __shared__ int posq[PQ];
+    __shared__ float ksc[KCH], vsc[KCH];
+    const size_t seq = p.seq[r0];
+    const size_t base = seq * p.max_seq * p.hkv + (size_t)kh * hd;
+    // Every global read is issued before the first use.
+    float4 qv[NP], kf[KV8 ? 1 : NP], vf[KV8 ? 1 : NP];
+    uint32_t k8[KV8 ? NP : 1], v8[KV8 ? NP : 1];
+#pragma unroll
+    for (int u = 0; u < NP; ++u) {
+        const int idx = tid + u * RT, q = idx / hd4, c = (idx - q * hd4) * 4, i = q / G, g = q - i * G;
+        qv[u] = i < nrow ? *reinterpret_cast<const float4*>(p.q + (size_t)(r0 + i) * p.hq + (size_t)(kh * G + g) * hd + c)
+                         : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int k = idx / hd4;  // the same piece index over the K / V chunk
+        const bool live = k < nk;
+        const size_t o = base + (size_t)(j0 + k) * p.hkv + c;
+        if constexpr (KV8) {
+            k8[u] = live ? *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.kc) + o) : 0u;
+            v8[u] = live ? *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.vc) + o) : 0u;
+        } else {
+            kf[u] = live ? *reinterpret_cast<const float4*>(static_cast<const float*>(p.kc) + o) : make_float4(0.f, 0.f, 0.f, 0.f);
+            vf[u] = live ? *reinterpret_cast<const float4*>(static_cast<const float*>(p.vc) + o) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    float scl = 0.0f;
+    if constexpr (KV8) {
+        const int k = tid < KCH ? tid : tid - KCH;
+        if (tid < 2 * KCH && k < nk) scl = (tid < KCH ? p.ks : p.vs)[(seq * p.max_seq + j0 + k) * p.nkv + kh];
+    }
+    if (tid < PQ) {
+        const int i = tid / G;
+        posq[tid] = i < nrow ? (int)p.pos[r0 + i] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < NP; ++u) {
+        const int idx = tid + u * RT, q = idx / hd4, c = (idx - q * hd4) * 4;
+        *reinterpret_cast<float4*>(Qs + q * hd + c) = qv[u];
+        if constexpr (KV8) {
+            *reinterpret_cast<float4*>(Ks + q * ks + c) = i8x4(k8[u]);
+            *reinterpret_cast<float4*>(Vs + q * hd + c) = i8x4(v8[u]);
+        } else {
+            *reinterpret_cast<float4*>(Ks + q * ks + c) = kf[u];
+            *reinterpret_cast<float4*>(Vs + q * hd + c) = vf[u];
+        }
+    }
+    if constexpr (KV8) {
+        if (tid < KCH) ksc[tid] = scl;
+        else if (tid < 2 * KCH) vsc[tid - KCH] = scl;
+    }
+    __syncthreads();
+    // Scores: thread -> queries 2*(t>>4)+{0,1} x keys 2*(t&15)+{0,1}, each dot
+    // product in head_dim order, then (KV8: x kscale) x 1/sqrt(hd).
+    {
+        const int q0 = 2 * (tid >> 4), k0 = 2 * (tid & 15);
+        float s00 = 0.f, s01 = 0.f, s10 = 0.f, s11 = 0.f;
+        const float* qa = Qs + q0 * hd;
+        const float* qb2 = qa + hd;
+        const float* ka = Ks + k0 * ks;
+        const float* kb = ka + ks;
+#pragma unroll 8
+        for (int c = 0; c < hd; c += 4) {
+            const float4 a0 = *reinterpret_cast<const float4*>(qa + c), a1 = *reinterpret_cast<const float4*>(qb2 + c);
+            const float4 b0 = *reinterpret_cast<const float4*>(ka + c), b1 = *reinterpret_cast<const float4*>(kb + c);
+            s00 += a0.x * b0.x + a0.y * b0.y + a0.z * b0.z + a0.w * b0.w;
+            s01 += a0.x * b1.x + a0.y * b1.y + a0.z * b1.z + a0.w * b1.w;
+            s10 += a1.x * b0.x + a1.y * b0.y + a1.z * b0.z + a1.w * b0.w;
+            s11 += a1.x * b1.x + a1.y * b1.y + a1.z * b1.z + a1.w * b1.w;
+        }
+        const float sv[2][2] = {{s00, s01}, {s10, s11}};
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const int q = q0 + a, k = k0 + c;
+                float v = sv[a][c];
+                if (KV8) v = v * ksc[k];
+                v = v * p.scale;
+                const bool live = k < nk && posq[q] >= 0 && j0 + k <= posq[q];
+                Ps[q][k] = live ? v : -INFINITY;
+            }
+    }
+    __syncthreads();
+    // The chunk's statistics: 8 lanes per query, 4 keys each; max and sum
+    // over the 8 lanes by xor shuffles (a fixed order per query).
+    {
+        const int q = tid >> 3, k4 = (tid & 7) * 4;
+        float sv[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            sv[c] = Ps[q][k4 + c];
+            mx = fmaxf(mx, sv[c]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+        float sum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            sv[c] = sv[c] == -INFINITY ? 0.0f : expf(sv[c] - mx);
+            sum += sv[c];
+        }
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        sum += __shfl_xor(sum, 4, 64);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) Ps[q][k4 + c] = sv[c];
+        if ((tid & 7) == 0) {
+            mls[q][0] = mx;
+            mls[q][1] = sum;
+        }
+    }
+    __syncthreads();
+    // o = sum_k p_k v_k over the chunk's keys in order.
+    const int oq = tid >> 3, od = (tid & 7) * ow;
+    const int i = oq / G, g = oq - i * G;
+    if (i >= nrow || j0 > posq[oq]) return;  // no key of this chunk is visible to the query
+    float O[ow];
+#pragma unroll
+    for (int u = 0; u < ow; ++u) O[u] = 0.0f;
+#pragma unroll 4
+    for (int k = 0; k < nk; ++k) {
+        const float pk = Ps[oq][k];
+        float vk[ow];
+#pragma unroll
+        for (int u = 0; u < ow; u += 4) {
+            const float4 x = *reinterpret_cast<const float4*>(Vs + k * hd + od + u);
+            vk[u] = x.x; vk[u + 1] = x.y; vk[u + 2] = x.z; vk[u + 3] = x.w;
+        }
+        if constexpr (KV8) {
+            const float vs = vsc[k];
+#pragma unroll
+            for (int u = 0; u < ow; ++u) O[u] += pk * vk[u] * vs;
+        } else {
+#pragma unroll
+            for (int u = 0; u < ow; ++u) O[u] += pk * vk[u];
+        }
+    }
+    const size_t slot = ((size_t)(r0 + i) * p.nh + kh * G + g) * p.splits + sp;
+#pragma unroll
+    for (int u = 0; u < ow; u += 4)
+        *reinterpret_cast<float4*>(p.part_o + slot * hd + od + u) = make_float4(O[u], O[u + 1], O[u + 2], O[u + 3]);
+    if ((tid & 7) == 0) {
+        p.part_ml[2 * slot] = mls[oq][0];
+        p.part_ml[2 * slot + 1] = mls[oq][1];
+    }
+}
+
 // Merge the key chunks of every head of row r: M = max m_s,
 // L = sum l_s e^(m_s - M), ctx = sum o_s e^(m_s - M) / L; then quantize the
 // whole context row for the output projection (quant_pack semantics).
@@ -816,10 +996,11 @@ int launch_swiglu_quant(bh_qwen3* e, int rows) {
 int launch_combine_quant(bh_qwen3* e, int rows, int splits) {
     const int hq = (int)e->hq, groups = (hq / 4 + RT - 1) / RT;
     const int nh = (int)e->c.n_heads, hd = (int)e->c.head_dim;
-    if (groups <= 1) attn_combine_quant_kernel<1><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, e->cur_pos, nh, hd, hq, splits, e->sx, e->xq);
-    else if (groups <= 2) attn_combine_quant_kernel<2><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, e->cur_pos, nh, hd, hq, splits, e->sx, e->xq);
-    else if (groups <= 4) attn_combine_quant_kernel<4><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, e->cur_pos, nh, hd, hq, splits, e->sx, e->xq);
-    else attn_combine_quant_kernel<8><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, e->cur_pos, nh, hd, hq, splits, e->sx, e->xq);
+    const uint32_t* pos = e->cur_pos;
+    if (groups <= 1) attn_combine_quant_kernel<1><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, pos, nh, hd, hq, splits, e->sx, e->xq);
+    else if (groups <= 2) attn_combine_quant_kernel<2><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, pos, nh, hd, hq, splits, e->sx, e->xq);
+    else if (groups <= 4) attn_combine_quant_kernel<4><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, pos, nh, hd, hq, splits, e->sx, e->xq);
+    else attn_combine_quant_kernel<8><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, pos, nh, hd, hq, splits, e->sx, e->xq);
     BH_HIP(hipGetLastError(), "attention combine launch");
     return BH_OK;
 }
@@ -836,8 +1017,11 @@ bool fused_ok(bh_qwen3* e, int rows, int k, int n) {
 
 // `splits`: key chunks of KCH covering the longest row of this launch (the
 // workspace stride; chunks past a row's position exit immediately).
+// `rows_per_seq` > 0: the rows are whole runs of consecutive positions, one
+// run of that many rows per sequence (a prefill chunk), which the
+// query-block attention kernel needs.
 int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, const uint32_t* seq, int n_out,
-             const int* out_map, bool decode, int splits) {
+             const int* out_map, bool decode, int splits, int rows_per_seq = 0) {
     e->cur_pos = pos;
     const bh_qwen3_config& c = e->c;
     const int d = (int)c.d_model, ff = (int)c.d_ff, hd = (int)c.head_dim;
@@ -845,6 +1029,11 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
     float* nxt = e->res2;
     const int nh = (int)c.n_heads, nkv = (int)c.n_kv_heads;
     const float scale = 1.0f / sqrtf((float)hd);
+    // Query-block prefill attention: whole per-sequence runs, 32 query vectors
+    // a workgroup (G divides 32), head_dim 64 or 128 (the kernel is built for
+    // those; its LDS image stays within 64 KB).
+    const bool qblock = !decode && rows_per_seq > 0 && rows % rows_per_seq == 0 && PQ % (nh / nkv) == 0 &&
+                        (hd == 64 || hd == 128);
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         const bh_qwen3::Layer& Ly = e->L[l];
         void* kc = static_cast<uint8_t*>(e->kc) + l * e->layer_kv * e->kv_elem;
@@ -900,8 +1089,21 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
             if (c.kv_int8) qk_rope_append_kernel<true><<<dim3(rows, nh + 2 * nkv), 64, 0, e->stream>>>(ra);
             else qk_rope_append_kernel<false><<<dim3(rows, nh + 2 * nkv), 64, 0, e->stream>>>(ra);
             BH_HIP(hipGetLastError(), "qk_rope_append launch");
-            if (c.kv_int8) attn_split_kernel<true><<<agrid, RT, alds_pre, e->stream>>>(aa);
-            else attn_split_kernel<false><<<agrid, RT, alds_pre, e->stream>>>(aa);
+            if (qblock) {
+                const int nqb = (rows_per_seq + PQ / (nh / nkv) - 1) / (PQ / (nh / nkv));
+                const dim3 pgrid(rows / rows_per_seq * nqb * splits, nkv);
+                const size_t plds = ((size_t)PQ * hd + (size_t)KCH * (hd + 4) + (size_t)KCH * hd) * 4;
+                if (hd == 128) {
+                    if (c.kv_int8) attn_prefill_kernel<true, 128><<<pgrid, RT, plds, e->stream>>>(aa, rows_per_seq);
+                    else attn_prefill_kernel<false, 128><<<pgrid, RT, plds, e->stream>>>(aa, rows_per_seq);
+                } else {
+                    if (c.kv_int8) attn_prefill_kernel<true, 64><<<pgrid, RT, plds, e->stream>>>(aa, rows_per_seq);
+                    else attn_prefill_kernel<false, 64><<<pgrid, RT, plds, e->stream>>>(aa, rows_per_seq);
+                }
+            } else {
+                if (c.kv_int8) attn_split_kernel<true><<<agrid, RT, alds_pre, e->stream>>>(aa);
+                else attn_split_kernel<false><<<agrid, RT, alds_pre, e->stream>>>(aa);
+            }
             BH_HIP(hipGetLastError(), "attention launch");
         }
         // (Merging inside the output projection's prologue measured 4x slower
@@ -1323,7 +1525,7 @@ int bh_qwen3_prefill(bh_qwen3* e, const uint32_t* tokens, uint32_t batch, uint32
         BH_HIP(hipMemcpyAsync(e->seq_rows, seq.data(), rows * 4, hipMemcpyHostToDevice, e->stream), "upload");
         if (last) BH_HIP(hipMemcpyAsync(e->row_map, map.data(), batch * 4, hipMemcpyHostToDevice, e->stream), "upload");
         BH_TRY(run_rows(e, (int)rows, e->tok_rows, e->pos_rows, e->seq_rows, last ? (int)batch : 0, e->row_map, false,
-                        (int)((p0 + cc + KCH - 1) / KCH)));
+                        (int)((p0 + cc + KCH - 1) / KCH), (int)cc));
         BH_TRY(sync(e));  // the host vectors are reused by the next chunk
     }
     std::vector<uint32_t> pdec(batch, len);
