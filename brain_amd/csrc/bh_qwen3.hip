@@ -395,7 +395,9 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     // more workgroups fit on a CU.
     extern __shared__ __attribute__((aligned(16))) float attn_dyn[];
     const int r = blockIdx.x, kh = blockIdx.y, sp = blockIdx.z, tid = threadIdx.x;
-
+    // Decode (ROPE) rows are sequences 0..rows-1 in order, so the sequence
+    // needs no load there; elsewhere its load goes out with the position's.
+    const size_t sq = ROPE ? (size_t)r : (size_t)p.seq[r];
     const int t = (int)p.pos[r] + 1;
     const int j0 = sp * KCH;
     if (j0 >= t) return;
@@ -407,8 +409,8 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     float* vls = nv + p.hd;
     const bool last = ROPE && j0 + n == t;  // this chunk ends at the new key
     const int nc = last ? n - 1 : n;        // keys read from the cache
-    const size_t tok0 = (size_t)p.seq[r] * p.max_seq + j0;  // cache slot of this chunk's first key
-    const size_t base = (size_t)p.seq[r] * p.max_seq * p.hkv + (size_t)kh * p.hd;
+    const size_t tok0 = sq * p.max_seq + j0;  // cache slot of this chunk's first key
+    const size_t base = sq * p.max_seq * p.hkv + (size_t)kh * p.hd;
 
     // Every cache read of the chunk is issued first, so its latency overlaps
     // the query rotation: this lane's K pieces (8 lanes per key, float4
@@ -464,7 +466,7 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
             } else {
                 const bool is_k = h == G;
                 rope_head(ro, row + ro.hq + (is_k ? 0 : ro.hkv) + kh * p.hd, ro.kn, is_k, pos, lane, y0, y1);
-                const float sc = kv_append<KV8>(ro, is_k, kh, (size_t)p.seq[r] * p.max_seq + pos, lane, y0, y1);
+                const float sc = kv_append<KV8>(ro, is_k, kh, sq * p.max_seq + pos, lane, y0, y1);
                 dst = is_k ? nk : nv;
                 if (lane == 0) newsc[is_k ? 0 : 1] = sc;
             }
