@@ -54,7 +54,8 @@ hipError_t launch_gemm_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
 // Split-K workspace, one per (device, stream): the S partial slabs of a
 // split GEMM. Every split kernel overwrites the slabs it uses before the
 // reduction reads them, so the buffer is never cleared. Calls on one stream
-// are ordered, so they never share it concurrently.
+// are ordered, so they never share it concurrently; a graph captured on the
+// stream replays in that stream's order too.
 struct SplitWs {
     int device;
     hipStream_t stream;
@@ -83,12 +84,12 @@ int* splitk_workspace(hipStream_t st, size_t ints, hipError_t* err) {
             *err = hipErrorStreamCaptureUnsupported;
             return nullptr;
         }
-        // Growing: wait for this stream's queued users of the old buffer.
-        if ((*err = hipStreamSynchronize(st)) != hipSuccess) return nullptr;
-        if (w->ws) (void)hipFree(w->ws);
-        w->ws = nullptr;
-        w->ints = 0;
-        if ((*err = hipMalloc(&w->ws, ints * 4)) != hipSuccess) return nullptr;
+        // Growing. The old buffer is kept, not freed, until the process ends:
+        // a HIP graph captured earlier may still launch kernels that use it.
+        // (Sizes only grow and each is capped, so this retains little.)
+        int* nb = nullptr;
+        if ((*err = hipMalloc(&nb, ints * 4)) != hipSuccess) return nullptr;
+        w->ws = nb;
         w->ints = ints;
     }
     return w->ws;

@@ -43,3 +43,38 @@ def test_graph_replays_match_eager(gpu):
         for d, e in zip(data, eager):
             assert torch.equal(d["out"].view(torch.int16), e.view(torch.int16)), f"replay {rep} differs"
 
+
+
+def test_graph_survives_workspace_growth(gpu):
+    """A graph that captured a split-K GEMM keeps working after a larger
+    split-K GEMM on the same stream grew the workspace (the old buffer the
+    graph uses must stay valid)."""
+    def case(m, k, n, seed):
+        x = torch.from_numpy(o.synth_acts(m, k, seed)).to(gpu)
+        wq, sw = o.synth_weights(n, k, seed + 1)
+        return dict(x=x, wq=torch.from_numpy(wq.view(np.int32)).to(gpu), sw=torch.from_numpy(sw).to(gpu),
+                    sx=torch.empty(m, device=gpu), xq=torch.empty(m, k // 4, dtype=torch.int32, device=gpu),
+                    out=torch.empty(m, n, dtype=torch.float32, device=gpu))
+
+    small, big = case(128, 3072, 1024, 40), case(300, 4096, 520, 50)   # both take the split-K path
+
+    def run(d):
+        ops.linear_i8(d["x"], d["wq"], d["sw"], None, torch.float32, sx=d["sx"], xq=d["xq"], out=d["out"])
+
+    cap = torch.cuda.Stream()
+    with torch.cuda.stream(cap):
+        run(small)
+    torch.cuda.synchronize()
+    eager = small["out"].clone()
+    ops.reserve_workspace(128, 3072, 1024, cap)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap):
+        run(small)
+    with torch.cuda.stream(cap):
+        run(big)                      # grows the workspace of `cap`
+    torch.cuda.synchronize()
+    for _ in range(3):
+        small["out"].fill_(0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(small["out"], eager)
