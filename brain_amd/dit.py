@@ -82,15 +82,19 @@ class DitInt8Stack:
             self.layer(i)
 
     def capture(self):
-        """Record one step (all layers) in a HIP graph on a side stream."""
+        """Record one step (all layers) in a HIP graph on a side stream. The
+        split-K workspace of that stream is sized first (a linear whose GEMM
+        splits K cannot allocate it during capture)."""
         s = torch.cuda.Stream()
+        for _, k, n in LINEARS:
+            ops.reserve_workspace(self.m, k, n, s)
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             self.step()  # warm (first-touch) outside the capture
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
+        with torch.cuda.graph(self.graph, stream=s):
             self.step()
         torch.cuda.synchronize()
 

@@ -179,6 +179,12 @@ def test_gemm_split_k(gpu, m, k, n):
     run_and_check(gpu, m, k, n, "dyn", seed=m + 5 * k + n, bias=True)
 
 
+def test_gemm_split_k_big_tiles(gpu):
+    # The DiT down projection: 150 tiles of 256x128 over 160 K stages, taken
+    # as 256x256 tiles split 3 ways over K.
+    run_and_check(gpu, 1152, 10240, 3840, "dyn", seed=77, bias=True, sample=300)
+
+
 def test_static_scale_matmul_split_k(gpu):
     m, k, n = 64, 4096, 256
     xq = o.quant_pack(o.synth_acts(m, k, 3), np.full(m, 0.02, np.float32))
