@@ -14,8 +14,10 @@ from HBM, not the Infinity Cache.
              it runs on, vs 8 TB/s
 Also reported: the prefill GEMM sweep (configs[2], each shape timed as one HIP
 graph of back-to-back launches) in TOPS vs the 5.0 POPS int8
-dense MFMA peak, an MFMA roof probe, and the CPU baseline (the restated
-backend-cpu decode path, OpenMP, timed on this host on a bounded sample).
+dense MFMA peak, an MFMA roof probe, and the CPU baselines timed on this host
+on bounded samples: the restated backend-cpu decode path (OpenMP) for the
+decode sweep, and for prefill (which backend-cpu has no int8 path for) that
+GEMV in 32-row chunks plus an OpenMP tiled i32 GEMM.
 """
 import argparse
 import json
@@ -440,6 +442,36 @@ def cpu_baseline(budget_s):
                 step_ms=round(t * 1e3, 2))
 
 
+def prefill_cpu_baseline(budget_s):
+    """Prefill on the host, where backend-cpu has no int8 path
+    (crates/gpu-core/tests/bench_matmul.rs:243-247): the restated decode GEMV
+    applied in 32-row chunks ("reference-CPU-equivalent (GEMV-chunked)") and an
+    OpenMP tiled i32 GEMM (a stronger host reference), on a bounded row sample
+    of the configs[2] shape 512x1024x3072, median of repeated runs."""
+    from oracle import oracle as o
+
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    k, n = 1024, 3072
+    wq, sw = o.synth_weights(n, k, 77)
+    out = {}
+    for name, rows, fn in (("gemv_chunked", 64, lambda xq, sx: [o.cpu_gemv_packed(xq[r:r + 32], wq, sx[r:r + 32], sw, threads)
+                                                             for r in range(0, xq.shape[0], 32)]),
+                           ("tiled_i32", 256, lambda xq, sx: o.cpu_gemm_tiled(xq, wq, sx, sw, threads))):
+        x = o.synth_acts(rows, k, 5)
+        sx = o.max_abs_row(x)
+        xq = o.quant_pack(x, sx)
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - t_start < budget_s / 2 and len(times) < 15):
+            t0 = time.perf_counter()
+            fn(xq, sx)
+            times.append(time.perf_counter() - t0)
+        t = sorted(times)[len(times) // 2]
+        out[name] = dict(value=round(2.0 * rows * n * k / t / 1e12, 4), unit="TOPS", cores=threads, kind="port",
+                         sample=f"{rows} of the 512 rows of 512x1024x3072, {len(times)} runs, median {t * 1e3:.1f} ms")
+    return out
+
+
 def _big_weights(n, k):
     import numpy as np
 
@@ -489,6 +521,7 @@ def main():
         return
     roof = mfma_roof(torch, lib, dev)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    pcpu = None if args.no_cpu or "prefill" not in res else prefill_cpu_baseline(min(args.cpu_seconds, 10.0))
 
     d = res["decode"]
     value = d["step_bytes"] / (d["step_ms"] * 1e-3) / 1e9
@@ -529,6 +562,11 @@ def main():
     }
     if "prefill" in res:
         line["prefill"] = res["prefill"]
+        if pcpu is not None:
+            line["prefill_cpu_baseline"] = pcpu
+            g = [r for r in res["prefill"]["shapes"] if (r["m"], r["k"], r["n"]) == (512, 1024, 3072)]
+            if g:
+                line["prefill_gpu_vs_cpu_tiled"] = round(g[0]["tops"] / 1e3 / pcpu["tiled_i32"]["value"], 1)
     if "qwen3" in res:
         line["qwen3_e2e"] = res["qwen3"]
     if "dit" in res:

@@ -191,6 +191,32 @@ void or_cpu_gemv_packed(const uint32_t* xq, const uint32_t* wq, const float* sx,
     (void)threads;
 }
 
+void or_cpu_gemm_i8_tiled(const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
+                          int64_t m, int64_t kg, int64_t n, int threads, float* out) {
+    const int64_t k = kg * 4;
+    const int64_t TM = 4, TN = 4;
+    const int64_t tiles_n = (n + TN - 1) / TN, tiles = ((m + TM - 1) / TM) * tiles_n;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 4) num_threads(threads)
+#endif
+    for (int64_t t = 0; t < tiles; ++t) {
+        const int64_t r0 = (t / tiles_n) * TM, c0 = (t % tiles_n) * TN;
+        for (int64_t r = r0; r < r0 + TM && r < m; ++r) {
+            const int8_t* xr = (const int8_t*)(xq + r * kg);
+            for (int64_t c = c0; c < c0 + TN && c < n; ++c) {
+                const int8_t* wr = (const int8_t*)(wq + c * kg);
+                int32_t acc = 0;
+#ifdef _OPENMP
+#pragma omp simd reduction(+ : acc)
+#endif
+                for (int64_t i = 0; i < k; ++i) acc += (int32_t)xr[i] * (int32_t)wr[i];
+                out[r * n + c] = (float)acc * sx[r] * sw[c];
+            }
+        }
+    }
+    (void)threads;
+}
+
 void or_cpu_linear_gemv(const float* x, const uint32_t* wq, const float* sw,
                         int64_t m, int64_t k, int64_t n, int threads,
                         float* sx, uint32_t* xq, float* out) {

@@ -96,6 +96,11 @@ void or_cpu_linear_gemv(const float* x, const uint32_t* wq, const float* sw,
 /* Same restated GEMV applied to an already-quantized activation. */
 void or_cpu_gemv_packed(const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
                         int64_t m, int64_t kg, int64_t n, int threads, float* out);
+/* A stronger host reference for prefill, which backend-cpu has no int8 path
+ * for (crates/gpu-core/tests/bench_matmul.rs:243-247): OpenMP over 4x4 output
+ * tiles, each dot product an i32 sum over K (SIMD), then (f32(acc)*sx)*sw. */
+void or_cpu_gemm_i8_tiled(const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
+                          int64_t m, int64_t kg, int64_t n, int threads, float* out);
 
 #ifdef __cplusplus
 }

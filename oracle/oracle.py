@@ -52,6 +52,7 @@ def lib():
             "or_f32_to_bf16_array": (None, [C.c_void_p, C.c_void_p, C.c_size_t]),
             "or_cpu_linear_gemv": (None, [vp, vp, vp, i64, i64, i64, i32, vp, vp, vp]),
             "or_cpu_gemv_packed": (None, [vp, vp, vp, vp, i64, i64, i64, i32, vp]),
+            "or_cpu_gemm_i8_tiled": (None, [vp, vp, vp, vp, i64, i64, i64, i32, vp]),
             "or_argmax_row": (u32, [vp, u32]),
             "or_quantize_weight_q4": (None, [vp, i64, i64, vp, vp]),
             "or_dequantize_weight_q4": (None, [vp, vp, i64, i64, vp]),
@@ -229,6 +230,19 @@ def cpu_gemv_packed(xq, wq, sx, sw, threads):
     n = wq.shape[0]
     out = np.zeros((m, n), np.float32)
     lib().or_cpu_gemv_packed(_p(xq), _p(wq), _p(sx), _p(sw), m, kg, n, threads, _p(out))
+    return out
+
+
+def cpu_gemm_tiled(xq, wq, sx, sw, threads):
+    """OpenMP tiled i32 GEMM on the host (prefill CPU reference)."""
+    xq = _c(xq, np.uint32)
+    wq = _c(wq, np.uint32)
+    sx = _c(sx, np.float32)
+    sw = _c(sw, np.float32)
+    m, kg = xq.shape
+    n = wq.shape[0]
+    out = np.zeros((m, n), np.float32)
+    lib().or_cpu_gemm_i8_tiled(_p(xq), _p(wq), _p(sx), _p(sw), m, kg, n, threads, _p(out))
     return out
 
 

@@ -271,3 +271,22 @@ def test_cpu_baseline_gemv_matches_oracle():
     want = o.matmul_i8(xq, wq, sx, sw)
     assert (o.cpu_linear_gemv(x, wq, sw, 4) == want).all()
     assert (o.cpu_gemv_packed(xq, wq, sx, sw, 2) == want).all()
+
+
+def test_cpu_tiled_gemm_matches_oracle():
+    """The prefill host reference equals the pinned matmul bit for bit, on
+    ragged tiles and on arbitrary bytes (including -128, which quant_pack
+    never emits) against the int64 brute force."""
+    x = o.synth_acts(37, 520, 3)
+    wq, sw = o.synth_weights(50, 520, 4)
+    sx = o.max_abs_row(x)
+    xq = o.quant_pack(x, sx)
+    want = o.matmul_i8(xq, wq, sx, sw)
+    assert (o.cpu_gemm_tiled(xq, wq, sx, sw, 3).view(np.uint32) == want.view(np.uint32)).all()
+    rng = np.random.default_rng(9)
+    xr = rng.integers(0, 2**32, (9, 64), dtype=np.uint64).astype(np.uint32)
+    wr = rng.integers(0, 2**32, (7, 64), dtype=np.uint64).astype(np.uint32)
+    sxr = rng.uniform(0.001, 0.1, 9).astype(np.float32)
+    swr = rng.uniform(0.001, 0.1, 7).astype(np.float32)
+    got = o.cpu_gemm_tiled(xr, wr, sxr, swr, 2)
+    assert (got.view(np.uint32) == o.epilogue(o.acc_exact(xr, wr), sxr, swr).view(np.uint32)).all()
