@@ -8,7 +8,7 @@ total), so a weight is re-read only after >256 MB of other traffic and comes
 from HBM, not the Infinity Cache.
 
   value    = algorithmic bytes of the 16 linears / wall time per step (GB/s),
-             bytes per linear = N*K + 4N + 4*M*K + 2*M*N (BASELINE.md section 3)
+             bytes per linear = N*K + 4N + 4*M*K + 2*M*N
   roofline = the GEMV kernel alone: its algorithmic bytes (N*K + 4N + M*K + 2*M*N)
              / its average launch duration, timed with HIP events on the stream
              it runs on, vs 8 TB/s
@@ -484,7 +484,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the int8 linear shards over output channels with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(the int8 linear shards over output channels with no exchange)", file=sys.stderr)
         sys.exit(2)
     import torch
 

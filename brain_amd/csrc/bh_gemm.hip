@@ -834,7 +834,7 @@ static int choose_splits(long tiles, double per_stage, int m, int kg, int n) {
 //    rounds of 256x128, 6.6; 6 rounds of 128x128, 7.5).
 //  - Fewer 128x128 tiles than CUs: smaller tiles put more CUs to work. A lone
 //    tile's time is set by how fast one CU streams its operands, so halving a
-//    tile side nearly halves its time. Measured on the configs[2] shapes at
+//    tile side nearly halves its time. Measured on the prefill sweep shapes at
 //    M=128..2048: 128-255 tiles of 128x128 run fastest as 64x128 tiles, fewer
 //    as 64x64 tiles, and 64x64 tiles on at most one round of CUs with 32+
 //    K stages run fastest with 8 stages in flight.
