@@ -302,7 +302,7 @@ def bench_w4a8(reps=20):
             fn()
         torch.cuda.synchronize()
         gr = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gr):
+        with torch.cuda.graph(gr, stream=s):  # the stream whose workspace the warm call sized
             for _ in range(reps):
                 fn()
         gr.replay()

@@ -37,6 +37,7 @@ hipError_t launch_gemm_i8_static(hipStream_t s, const uint32_t* xq, const uint32
                                  float* out, int m, int kg, int n);
 
 size_t gemm_workspace_ints(int m, int kg, int n);
+size_t gemm_q4_workspace_ints(int m, int k, int n);
 hipError_t launch_gemv_i8_gated(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                                 const float* sw, const float* gate, int gate_stride, int gate_col, float* out, int m,
                                 int kg, int n);
@@ -59,22 +60,23 @@ hipError_t launch_gemm_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
 struct SplitWs {
     int device;
     hipStream_t stream;
+    int slot;  // 0: split-K slabs, 1: W4A8 weights expanded to int8
     int* ws;
     size_t ints;
 };
 static std::mutex g_ws_mu;
 static std::vector<SplitWs> g_ws;
 
-int* splitk_workspace(hipStream_t st, size_t ints, hipError_t* err) {
+int* splitk_workspace(hipStream_t st, size_t ints, hipError_t* err, int slot) {
     int dev = 0;
     *err = hipGetDevice(&dev);
     if (*err != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> g(g_ws_mu);
     SplitWs* w = nullptr;
     for (auto& x : g_ws)
-        if (x.device == dev && x.stream == st) w = &x;
+        if (x.device == dev && x.stream == st && x.slot == slot) w = &x;
     if (!w) {
-        g_ws.push_back(SplitWs{dev, st, nullptr, 0});
+        g_ws.push_back(SplitWs{dev, st, slot, nullptr, 0});
         w = &g_ws.back();
     }
     if (w->ints < ints) {
@@ -277,14 +279,19 @@ int bh_matmul_i8_dyn(void* stream, const uint32_t* xq, const uint32_t* wq, const
 int bh_reserve_workspace(void* stream, uint32_t m, uint32_t kg, uint32_t n) {
     if ((uint64_t)kg * 4 > I32MAX || m > I32MAX || n > I32MAX)
         return fail(BH_ERR_INVALID, "bh_reserve_workspace: m=%u kg=%u n=%u out of range", m, kg, n);
-    const size_t ints = gemm_workspace_ints((int)m, (int)kg, (int)n);
-    if (!ints) return BH_OK;
-    hipError_t err = hipSuccess;
-    if (!splitk_workspace((hipStream_t)stream, ints, &err)) {
-        if (err == hipErrorStreamCaptureUnsupported)
-            return fail(BH_ERR_INVALID, "bh_reserve_workspace: stream is capturing; reserve before capture");
-        return fail(err == hipErrorOutOfMemory ? BH_ERR_NOMEM : BH_ERR_HIP, "bh_reserve_workspace: %s",
-                    hipGetErrorString(err));
+    // Both workspaces a GEMM of this shape may take: the split-K slabs of the
+    // int8 GEMM, and for W4A8 (K = 4*kg) the weights expanded to int8.
+    const size_t need[2] = {gemm_workspace_ints((int)m, (int)kg, (int)n),
+                            gemm_q4_workspace_ints((int)m, (int)kg * 4, (int)n)};
+    for (int slot = 0; slot < 2; ++slot) {
+        if (!need[slot]) continue;
+        hipError_t err = hipSuccess;
+        if (!splitk_workspace((hipStream_t)stream, need[slot], &err, slot)) {
+            if (err == hipErrorStreamCaptureUnsupported)
+                return fail(BH_ERR_INVALID, "bh_reserve_workspace: stream is capturing; reserve before capture");
+            return fail(err == hipErrorOutOfMemory ? BH_ERR_NOMEM : BH_ERR_HIP, "bh_reserve_workspace: %s",
+                        hipGetErrorString(err));
+        }
     }
     return BH_OK;
 }

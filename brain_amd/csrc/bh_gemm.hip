@@ -957,7 +957,7 @@ static inline bool gemm_aligned(const void* xq, const void* wq, int kg) {
 
 // Split-K workspace of the stream: at least `ints` i32 (grown outside graph
 // capture only; hipErrorStreamCaptureUnsupported otherwise).
-int* splitk_workspace(hipStream_t s, size_t ints, hipError_t* err);
+int* splitk_workspace(hipStream_t s, size_t ints, hipError_t* err, int slot = 0);
 
 // Workspace elements the GEMM needs for this shape (0 = no split-K).
 size_t gemm_workspace_ints(int m, int kg, int n) {
@@ -1020,9 +1020,30 @@ hipError_t launch_gemm_i8_static(hipStream_t s, const uint32_t* xq, const uint32
     return run_gemm<OUT_F32, false, true>(s, al, al && ((kg * 4) % 128 == 0), choose_tiles(m, kg, n), a);
 }
 
-// W4A8 prefill GEMM (matmul_q4_dyn, crates/kernels/wgsl/matmul_q4_dyn.wgsl):
-// the register-staged kernel with int4 B unpacked on the way into LDS. k is
-// the raw K (k % 8 == 0); the activation keeps its int8 [M, K/4] layout.
+// W4A8 prefill GEMM (matmul_q4_dyn, crates/kernels/wgsl/matmul_q4_dyn.wgsl).
+// k is the raw K (k % 8 == 0); the activation keeps its int8 [M, K/4] layout.
+//  - M >= Q4_EXPAND_M and K % 32 == 0: the int4 weights are expanded once to
+//    int8 ([N, K/4], the same values sign-extended) in a per-stream
+//    workspace, and the int8 GEMM runs on them. The accumulators are the same
+//    integers, so the output is bit-identical; the expansion moves 1.5*N*K
+//    bytes, small beside the GEMM at these M.
+//  - otherwise the register-staged kernel with int4 B unpacked on the way
+//    into LDS.
+constexpr int Q4_EXPAND_M = 256;
+
+__global__ __launch_bounds__(256) void expand_q4_kernel(const v4i* w4, v4i* w8, int64_t pieces) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < pieces; i += (int64_t)gridDim.x * 256) {
+        v4i lo, hi;
+        unpack_q4x4(w4[i], lo, hi);
+        w8[2 * i] = lo;
+        w8[2 * i + 1] = hi;
+    }
+}
+
+size_t gemm_q4_workspace_ints(int m, int k, int n) {
+    return (m >= Q4_EXPAND_M && k % 32 == 0) ? (size_t)n * (k / 4) : 0;
+}
+
 template <int OUT, bool HAS_BIAS>
 static hipError_t go_q4(hipStream_t s, bool aligned, const GemmArgs& a) {
     TileChoice tc = choose_tiles(a.m, a.kg, a.n);
@@ -1032,9 +1053,20 @@ static hipError_t go_q4(hipStream_t s, bool aligned, const GemmArgs& a) {
 
 hipError_t launch_gemm_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int k, int n) {
-    GemmArgs a{xq, wq, sx, sw, bias, out, m, k / 4, n, 0.f, 0.f, 1, nullptr};
     // Aligned 16-byte loads need 16-byte rows in both operands: K % 32 == 0.
     const bool al = (k % 32) == 0 && ((reinterpret_cast<uintptr_t>(xq) | reinterpret_cast<uintptr_t>(wq)) & 15u) == 0;
+    const size_t ints = gemm_q4_workspace_ints(m, k, n);
+    if (al && ints) {
+        hipError_t err = hipSuccess;
+        int* w8 = splitk_workspace(s, ints, &err, 1);
+        if (!w8) return err == hipSuccess ? hipErrorOutOfMemory : err;
+        const int64_t pieces = (int64_t)n * k / 32;
+        const unsigned grid = (unsigned)std::min<int64_t>((pieces + 255) / 256, 256 * 8);
+        expand_q4_kernel<<<grid, 256, 0, s>>>(reinterpret_cast<const v4i*>(wq), reinterpret_cast<v4i*>(w8), pieces);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+        return launch_gemm_i8(s, xq, reinterpret_cast<const uint32_t*>(w8), sx, sw, bias, out, out_dtype, m, k / 4, n);
+    }
+    GemmArgs a{xq, wq, sx, sw, bias, out, m, k / 4, n, 0.f, 0.f, 1, nullptr};
     switch (out_dtype) {
         case OUT_I32: return go_q4<OUT_I32, false>(s, al, a);
         case OUT_F32: return bias ? go_q4<OUT_F32, true>(s, al, a) : go_q4<OUT_F32, false>(s, al, a);

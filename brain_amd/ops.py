@@ -145,8 +145,9 @@ def f32_to_bf16(x):
 
 
 def reserve_workspace(m, k, n, stream=None):
-    """Pre-size the split-K workspace of `stream` (default: current) for an
-    [m,k] x [n,k] GEMM; required before capturing such a GEMM in a graph."""
+    """Pre-size the workspaces of `stream` (default: current) that an
+    [m,k] x [n,k] GEMM may take (split-K slabs; for W4A8 the int4 weights
+    expanded to int8); required before capturing such a GEMM in a graph."""
     sp = (stream or torch.cuda.current_stream()).cuda_stream
     check(load().bh_reserve_workspace(sp, m, k // 4, n))
 

@@ -71,9 +71,33 @@ def test_q4_dyn_prefill_shapes(gpu, m, k, n):
     check(gpu, m, k, n, "dyn", seed=m + k + n, sample=None if m * n <= 512 * 3072 else 300)
 
 
-@pytest.mark.parametrize("m,k,n", [(33, 8, 1), (40, 24, 130), (129, 200, 257), (1, 4096, 5)])
+# From M=256 with K % 32 == 0 the int4 weights are expanded to int8 and the
+# int8 GEMM runs (here also splitting K: 256x4096x130); below, or with K % 32
+# != 0, the register-staged int4 kernel.
+@pytest.mark.parametrize("m,k,n", [(33, 8, 1), (40, 24, 130), (129, 200, 257), (1, 4096, 5), (300, 200, 64),
+                                   (256, 4096, 130), (255, 1024, 96)])
 def test_q4_dyn_edges(gpu, m, k, n):
     check(gpu, m, k, n, "dyn", seed=m + k + n)
+
+
+def test_q4_expanded_gemm_in_a_graph(gpu):
+    """The expansion + int8 GEMM recorded in a HIP graph (its workspaces sized
+    first with bh_reserve_workspace, kg = K/4) replays to the eager bits."""
+    m, k, n = 512, 2048, 384
+    xq, w4, sx, sw, _ = make(m, k, n, 8)
+    d = [dev_u32(xq, gpu), dev_u32(w4, gpu), torch.from_numpy(sx).to(gpu), torch.from_numpy(sw).to(gpu)]
+    out = torch.empty(m, n, device=gpu)
+    eager = ops.matmul_q4(*d, None, torch.float32, "dyn").clone()
+    cap = torch.cuda.Stream()
+    ops.reserve_workspace(m, k, n, cap)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap):
+        ops.matmul_q4(*d, None, torch.float32, "dyn", out=out)
+    for _ in range(3):
+        out.fill_(0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
 
 
 def test_q4_steps_through_the_backend(gpu):
