@@ -338,7 +338,7 @@ __device__ __forceinline__ void wait_ahead(int ahead) {
 }
 
 template <int BM, int BN, int WM, int WN, int STAGES, int DK, int OUT, bool HAS_BIAS, bool STATIC, bool SPLITK,
-          bool ILV_ENABLE = false>
+          bool ILV_ENABLE = false, bool PP = false>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the LDS-DMA builtins exist only in the device pass
     using C = DmaCfg<BM, BN, WM, WN, STAGES, DK>;
@@ -492,6 +492,63 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
         }
     };
 
+    if constexpr (PP) {
+        // Ping-pong: the 8 waves form two groups of 4 (one wave of each per
+        // SIMD) that run one phase apart, so on every SIMD one wave multiplies
+        // while the other reads LDS and issues DMA. Each stage takes two
+        // phases per wave, L (wait for the stage, read all its fragments into
+        // registers, issue the DMA of stage +3 into the buffer the stage
+        // before freed) and C (the stage's MFMAs), each closed by a
+        // workgroup barrier. Group 1 starts one barrier late and group 0 ends
+        // one barrier later, so both pass the same number of barriers.
+        //   Stage s is needed by group 0 at its L(s): its own DMA waits there;
+        // group 1 waits for its share of stage s during L(s-1), which ends
+        // before group 0's L(s); for stage 0 every wave waits before a common
+        // first barrier.
+        //   The DMA of L(s) overwrites stage s-1's buffer: group 0 read it in
+        // L(s-1), two phases earlier, group 1 in the phase just before.
+        static_assert(WM * WN == 8 && STAGES == 4, "ping-pong: 8 waves, 4 stages");
+        // Wave-uniform in a scalar register, so the group branches are real
+        // branches: a barrier under an exec mask would still execute.
+        const int grp = __builtin_amdgcn_readfirstlane(wave) >> 2;
+        v4i pa[C::KSTEPS][C::FM], pb[C::KSTEPS][C::FN];
+        // Stage 0 complete (every wave's share) before group 0's first L.
+        if (nk > 0) wait_ahead<C::LOADS, STAGES - 2>(min(nk - 1, STAGES - 2));
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        if (grp == 1) {
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        for (int it = 0; it < nk; ++it) {
+            if (grp == 0) wait_ahead<C::LOADS, STAGES - 2>(min(nk - 1 - it, STAGES - 2));
+            else wait_ahead<C::LOADS, STAGES - 3>(min(nk - 2 - it, STAGES - 3));
+            const uint8_t* A = lds + (it % STAGES) * C::STAGE;
+#pragma unroll
+            for (int ks = 0; ks < C::KSTEPS; ++ks) read_frags(A, ks, pa[ks], pb[ks]);
+            if (it + STAGES - 1 < nk) issue(kt0 + it + STAGES - 1, (it + STAGES - 1) % STAGES);
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the fragments are in registers
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int ks = 0; ks < C::KSTEPS; ++ks)
+#pragma unroll
+                for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < C::FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pb[ks][j], pa[ks][i], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (grp == 0) {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    } else {
     v4i fa[2][C::FM], fb[2][C::FN];
     if (nk > 0) {
         wait_ahead<C::LOADS, STAGES - 2>(min(nk - 1, STAGES - 2));
@@ -545,6 +602,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
 #pragma unroll
             for (int j = 0; j < C::FN; ++j) fb[0][j] = fb[1][j];
         }
+    }
+
     }
 
     // Lane l, register e of fragment (i,j): row rbase + 32i, columns
@@ -897,22 +956,24 @@ static hipError_t go(hipStream_t s, bool aligned, const GemmArgs& a) {
 }
 
 template <int BM, int BN, int WM, int WN, int STAGES, int DK, int OUT, bool HAS_BIAS, bool STATIC, bool SPLITK,
-          bool ILV = false>
+          bool ILV = false, bool PP = false>
 static hipError_t go_dma(hipStream_t s, const GemmArgs& a) {
     const long tiles = (long)((a.m + BM - 1) / BM) * ((a.n + BN - 1) / BN);
     const unsigned grid = (unsigned)(tiles * (SPLITK ? a.splits : 1));
-    gemm_i8_dma_kernel<BM, BN, WM, WN, STAGES, DK, OUT, HAS_BIAS, STATIC, SPLITK, ILV><<<grid, WM * WN * 64, 0, s>>>(a);
+    gemm_i8_dma_kernel<BM, BN, WM, WN, STAGES, DK, OUT, HAS_BIAS, STATIC, SPLITK, ILV, PP><<<grid, WM * WN * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
 // Alternative large-tile DMA configurations for measurement (BH_GEMM_BIG):
 // 0: 256x256, 8 waves (128x64 each: 2 waves per SIMD, ~200 VGPRs), DK=64,
-//    4 stages, DMA issue interleaved with the MFMAs (default; measured 5-10%
-//    above the 4-wave form on the large shapes)
+//    4 stages, the two wave groups in ping-pong (default; 2-3% above 5 on the
+//    large shapes)
 // 1: 256x128, 4 waves (128x64 each), DK=128, 3 stages
-// 2: the default without the DMA interleave
+// 2: 256x256, 8 waves, every wave reading and multiplying, no DMA interleave
 // 3: 256x256, 4 waves (128x128 each), no interleave
 // 4: 256x256, 4 waves (128x128 each), DMA interleave
+// 5: 256x256, 8 waves, DMA issue interleaved between the MFMAs (5-10% above
+//    the 4-wave forms)
 static int big_cfg() {
     static int v = env_int("BH_GEMM_BIG", 0);
     return v;
@@ -941,7 +1002,8 @@ static hipError_t go_cfg(hipStream_t s, bool aligned, bool dma, const TileChoice
                 case 2: return go_dma<256, 256, 2, 4, 4, 64, OUT, HAS_BIAS, STATIC, false>(s, a);
                 case 3: return go_dma<256, 256, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, false, false>(s, a);
                 case 4: return go_dma<256, 256, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, false, true>(s, a);
-                default: return go_dma<256, 256, 2, 4, 4, 64, OUT, HAS_BIAS, STATIC, false, true>(s, a);
+                case 5: return go_dma<256, 256, 2, 4, 4, 64, OUT, HAS_BIAS, STATIC, false, true>(s, a);
+                default: return go_dma<256, 256, 2, 4, 4, 64, OUT, HAS_BIAS, STATIC, false, false, true>(s, a);
             }
         }
         return go_small<OUT, HAS_BIAS, STATIC, false>(s, tc.cfg, a);
@@ -982,7 +1044,7 @@ static hipError_t run_gemm(hipStream_t s, bool al, bool dma, const TileChoice& t
     if (!a.ws) return err == hipSuccess ? hipErrorOutOfMemory : err;
     a.splits = tc.splits;
     if (dma && tc.cfg == TILE_256)
-        err = go_dma<256, 256, 2, 4, 4, 64, OUT_I32, false, false, true, true>(s, a);
+        err = go_dma<256, 256, 2, 4, 4, 64, OUT_I32, false, false, true, false, true>(s, a);
     else if (dma)
         err = go_small<OUT_I32, false, false, true>(s, tc.cfg, a);
     else
