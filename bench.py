@@ -566,7 +566,7 @@ def main():
             line["prefill_cpu_baseline"] = pcpu
             g = [r for r in res["prefill"]["shapes"] if (r["m"], r["k"], r["n"]) == (512, 1024, 3072)]
             if g:
-                line["prefill_gpu_vs_cpu_tiled"] = round(g[0]["tops"] / 1e3 / pcpu["tiled_i32"]["value"], 1)
+                line["prefill_gpu_vs_cpu_tiled"] = round(g[0]["tops"] / pcpu["tiled_i32"]["value"], 1)
     if "qwen3" in res:
         line["qwen3_e2e"] = res["qwen3"]
     if "dit" in res:
