@@ -93,6 +93,34 @@ def test_engine_matches_oracle(gpu, cfg_over):
     compare(cfg, w, prompts, steps=6)
 
 
+@pytest.mark.parametrize("kv_int8", [0, 1])
+def test_engine_long_context_matches_oracle(gpu, kv_int8):
+    """Positions past 512: the merge of more than 16 key chunks takes its
+    batched two-pass form (same operations in the same order as the one-batch
+    form), and the prompt runs as two prefill chunks. Over 530 positions
+    every sequence meets int8 rounding flips (measured ~5e-3 rel-L2, the same
+    as a flipped sequence at 100 positions), so this checks the noise bound
+    and the clear-margin tokens only."""
+    cfg = dict(SMALL, kv_int8=kv_int8)
+    w = scaled_weights(cfg, seed=17)
+    prompts = np.random.default_rng(6).integers(0, cfg["vocab"], size=(3, 530))
+    steps = 3
+    toks_o, logits_o = o.qwen3_generate(cfg, w, prompts, steps, int8=True)
+    e = engine_for(cfg, w, 3, 530 + steps + 1, 640)
+    got = [(e.prefill(prompts), e.logits())]
+    for _ in range(steps):
+        got.append((e.decode(1)[0], e.logits()))
+    for s_, (tk, lg) in enumerate(got):
+        per_seq = [rel_l2(lg[b], logits_o[s_][b]) for b in range(3)]
+        assert max(per_seq) < 2e-2, (s_, per_seq)
+        top2 = np.sort(logits_o[s_], axis=-1)[:, -2:]
+        clear = (top2[:, 1] - top2[:, 0]) > 2e-2 * np.abs(logits_o[s_]).max()
+        assert (tk[clear] == toks_o[s_][clear]).all(), (s_, tk, toks_o[s_])
+        if not (tk == toks_o[s_]).all():
+            break
+    e.close()
+
+
 def test_engine_chunked_prefill_matches_oracle(gpu):
     """max_rows = 8 with batch 2 splits the prompt into 4-position chunks."""
     cfg = SMALL
