@@ -143,7 +143,8 @@ def test_gemv_decode_sweep_full(gpu, m, k, n):
 
 
 @pytest.mark.parametrize("m,k,n", [(17, 1024, 300), (32, 512, 257), (2, 8, 3), (6, 24, 13), (5, 36, 33),
-                                   (1, 4, 1), (31, 132, 70), (3, 2048 + 64, 100)])
+                                   (1, 4, 1), (31, 132, 70), (3, 2048 + 64, 100),
+                                   (20, 1032, 16390), (9, 64, 16401), (32, 200, 16384)])
 def test_gemv_edges(gpu, m, k, n):
     run_and_check(gpu, m, k, n, "gemv", seed=m + k + n, bias=True)
 
