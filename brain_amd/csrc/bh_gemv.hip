@@ -113,6 +113,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
         const int grp = wave >> 2, gt = threadIdx.x & 255;
         const int d = kbytes, d4 = d >> 2;
         const bool first = blockIdx.x == 0;
+        // The norm weights (the same for every row) go out with the first
+        // loads, not behind the reduction and the residual stores.
+        float4 wv[GMAX];
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+            const int i = gt + 256 * g;
+            wv[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (XMODE == 3)
+                if (i < d4) wv[g] = reinterpret_cast<const float4*>(a.pre_w)[i];
+        }
         for (int r0 = 0; r0 < m; r0 += NG) {
             const int r = r0 + grp;
             const bool live = r < m;
@@ -150,13 +160,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
 #pragma unroll
                 for (int w = 1; w < 4; ++w) tot += gred[grp * 4 + w];
                 const float inv = 1.0f / sqrtf(tot / (float)d + a.eps);
-                const float4* w4 = reinterpret_cast<const float4*>(a.pre_w);
 #pragma unroll
                 for (int g = 0; g < GMAX; ++g) {
                     const int i = gt + 256 * g;
                     if (!live || i >= d4) continue;
-                    const float4 wv = w4[i];
-                    v[g] = make_float4(v[g].x * inv * wv.x, v[g].y * inv * wv.y, v[g].z * inv * wv.z, v[g].w * inv * wv.w);
+                    v[g] = make_float4(v[g].x * inv * wv[g].x, v[g].y * inv * wv[g].y, v[g].z * inv * wv[g].z,
+                                       v[g].w * inv * wv[g].w);
                 }
                 __syncthreads();  // gred is reused for the max
             }

@@ -237,7 +237,8 @@ __device__ __forceinline__ uint8_t kv8_code(float v, float scale) {
 __device__ __forceinline__ void rope_head(const RopeArgs& p, const float* src, const float* nw, bool rot, uint32_t pos,
                                           int lane, float (&y0)[2], float (&y1)[2]) {
     const int half = p.hd >> 1;
-    float ss = 0.0f;
+    const bool norm = rot && p.qk_norm;
+    float ss = 0.0f, w0[2] = {0.0f, 0.0f}, w1[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int m = lane + 64 * u;
@@ -245,6 +246,11 @@ __device__ __forceinline__ void rope_head(const RopeArgs& p, const float* src, c
         if (m < half) {
             y0[u] = src[m];
             y1[u] = src[m + half];
+            // The norm weights go out with the row, not after the reduction.
+            if (norm) {
+                w0[u] = nw[m];
+                w1[u] = nw[m + half];
+            }
             ss += y0[u] * y0[u] + y1[u] * y1[u];
         }
     }
@@ -260,8 +266,8 @@ __device__ __forceinline__ void rope_head(const RopeArgs& p, const float* src, c
         if (m >= half) continue;
         float a = y0[u], b = y1[u];
         if (p.qk_norm) {
-            a = a * inv * nw[m];
-            b = b * inv * nw[m + half];
+            a = a * inv * w0[u];
+            b = b * inv * w1[u];
         }
         const float angle = (float)pos * powf(p.theta, -(float)(2 * m) / (float)p.hd);
         const float c = cosf(angle), s = sinf(angle);
