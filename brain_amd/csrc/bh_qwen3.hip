@@ -221,7 +221,21 @@ struct RopeArgs {
     const uint32_t* seq;
     int nh, nkv, hd, hq, hkv, max_seq, qk_norm;
     float eps, theta;
+    const float2* cs;  // [max_seq][hd/2] (cos, sin) of the rotation angles, rope_table_kernel
 };
+
+// The rotation of pair m at position pos, angle pos * theta^(-2m/hd)
+// (rope_paged.wgsl:27-38), as (cos, sin): evaluated once per engine for every
+// position the cache holds, so decode reads it with the row instead of
+// spending the transcendental latency on every step.
+__global__ __launch_bounds__(256) void rope_table_kernel(float2* cs, int max_seq, int hd, float theta) {
+    const int half = hd >> 1;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)max_seq * half) return;
+    const int pos = (int)(i / half), m = (int)(i - (int64_t)pos * half);
+    const float angle = (float)pos * powf(theta, -(float)(2 * m) / (float)hd);
+    cs[i] = make_float2(cosf(angle), sinf(angle));
+}
 
 // One int8 KV code: clamp(round_even(v / scale), -127, 127)
 // (paged_kv_append_i8_clipped_batched.wgsl).
@@ -239,6 +253,7 @@ __device__ __forceinline__ void rope_head(const RopeArgs& p, const float* src, c
     const int half = p.hd >> 1;
     const bool norm = rot && p.qk_norm;
     float ss = 0.0f, w0[2] = {0.0f, 0.0f}, w1[2] = {0.0f, 0.0f};
+    float2 cs[2] = {make_float2(1.0f, 0.0f), make_float2(1.0f, 0.0f)};
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int m = lane + 64 * u;
@@ -246,11 +261,13 @@ __device__ __forceinline__ void rope_head(const RopeArgs& p, const float* src, c
         if (m < half) {
             y0[u] = src[m];
             y1[u] = src[m + half];
-            // The norm weights go out with the row, not after the reduction.
+            // The norm weights and the rotation go out with the row, not
+            // after the reduction.
             if (norm) {
                 w0[u] = nw[m];
                 w1[u] = nw[m + half];
             }
+            if (rot) cs[u] = p.cs[(size_t)pos * half + m];
             ss += y0[u] * y0[u] + y1[u] * y1[u];
         }
     }
@@ -269,8 +286,7 @@ __device__ __forceinline__ void rope_head(const RopeArgs& p, const float* src, c
             a = a * inv * w0[u];
             b = b * inv * w1[u];
         }
-        const float angle = (float)pos * powf(p.theta, -(float)(2 * m) / (float)p.hd);
-        const float c = cosf(angle), s = sinf(angle);
+        const float c = cs[u].x, s = cs[u].y;
         y0[u] = a * c - b * s;
         y1[u] = b * c + a * s;
     }
@@ -900,6 +916,7 @@ struct bh_qwen3 {
     void *kc = nullptr, *vc = nullptr;  // f32 or int8 elements
     float *kscale = nullptr, *vscale = nullptr;  // KV8: [L][max_batch][max_seq][nkv]
     float *kclip = nullptr, *vclip = nullptr;    // KV8: [L][nkv], FLT_MAX = no clipping
+    float2* rope_cs = nullptr;                   // [max_seq][hd/2] rotation (cos, sin)
     size_t layer_kv = 0;  // elements per layer per cache
     size_t kv_elem = 4;   // bytes per cache element
 
@@ -1081,7 +1098,7 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
         std::swap(cur, nxt);
         RopeArgs ra{e->qkv, e->q, kc, vc, ksl, vsl, e->kclip + (size_t)l * nkv, e->vclip + (size_t)l * nkv, Ly.qn,
                     Ly.kn, pos, seq, nh, nkv, hd, (int)e->hq, (int)e->hkv, (int)e->max_seq, (int)c.qk_norm,
-                    c.rms_eps, c.rope_theta};
+                    c.rms_eps, c.rope_theta, e->rope_cs};
         AttnArgs aa{e->q, kc, vc, ksl, vsl, pos, seq, e->part_o, e->part_ml, nh, nkv, hd, (int)e->hq,
                     (int)e->hkv, (int)e->max_seq, splits, scale, ra};
         const dim3 agrid(rows, nkv, splits);
@@ -1329,6 +1346,7 @@ int bh_qwen3_create(const bh_qwen3_config* cfg, uint32_t max_batch, uint32_t max
         (rc = dalloc(e, &e->vscale, c.kv_int8 ? (uint64_t)c.n_layers * max_batch * max_seq * c.n_kv_heads : 1)) ||
         (rc = dalloc(e, &e->kclip, (uint64_t)c.n_layers * c.n_kv_heads)) ||
         (rc = dalloc(e, &e->vclip, (uint64_t)c.n_layers * c.n_kv_heads)) ||
+        (rc = dalloc(e, &e->rope_cs, (uint64_t)max_seq * (c.head_dim / 2))) ||
         (rc = dalloc(e, &e->res, R * d)) || (rc = dalloc(e, &e->res2, R * d)) || (rc = dalloc(e, &e->qkv, R * e->W)) || (rc = dalloc(e, &e->q, R * hq)) ||
         (rc = dalloc(e, &e->part_o, R * c.n_heads * e->max_splits * c.head_dim)) || (rc = dalloc(e, &e->part_ml, R * c.n_heads * e->max_splits * 2)) || (rc = dalloc(e, &e->proj, R * d)) || (rc = dalloc(e, &e->gu, R * 2 * ff)) ||
         (rc = dalloc(e, &e->sx, R)) || (rc = dalloc(e, &e->xq, R * e->xq_words)) ||
@@ -1339,6 +1357,13 @@ int bh_qwen3_create(const bh_qwen3_config* cfg, uint32_t max_batch, uint32_t max
         (rc = dalloc(e, &e->pos_dec, max_batch)) || (rc = dalloc(e, &e->seq_dec, max_batch)) ||
         (rc = dalloc(e, &e->hist, (uint64_t)max_seq * max_batch)) || (rc = dalloc(e, &e->ctl, 2)))
         return bail(rc);
+    {
+        const int64_t nrot = (int64_t)max_seq * (c.head_dim / 2);
+        rope_table_kernel<<<(unsigned)((nrot + 255) / 256), 256, 0, e->stream>>>(e->rope_cs, (int)max_seq,
+                                                                               (int)c.head_dim, c.rope_theta);
+        if (hipGetLastError() != hipSuccess || hipStreamSynchronize(e->stream) != hipSuccess)
+            return bail(fail(BH_ERR_HIP, "bh_qwen3_create: rotation table"));
+    }
     std::vector<float> clip((size_t)c.n_layers * c.n_kv_heads, FLT_MAX);
     if (hipMemcpy(e->kclip, clip.data(), clip.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(e->vclip, clip.data(), clip.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
