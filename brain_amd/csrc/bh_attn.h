@@ -6,6 +6,7 @@
 namespace bh {
 
 constexpr int ATTN_KCH = 32;  // keys per attention workgroup (one split)
+constexpr int ATTN_SB = 16;   // chunks merged in one batch of loads
 
 // Merge of the key chunks of one head, for the four context elements
 // d..d+3: M = max m_s, L = sum l_s e^(m_s - M), ctx = sum o_s e^(m_s - M) / L
@@ -15,7 +16,7 @@ constexpr int ATTN_KCH = 32;  // keys per attention workgroup (one split)
 // rows loop over batches (max first, then the sums), with the same result.
 __device__ __forceinline__ float4 attn_combine4(const float* part_o, const float* part_ml, size_t hs, int ns, int d,
                                                 int hd) {
-    constexpr int SB = 16;
+    constexpr int SB = ATTN_SB;
     if (ns <= SB) {
         float mv[SB], lv[SB];
         float4 ov[SB];
@@ -74,14 +75,45 @@ __device__ __forceinline__ float4 attn_combine4(const float* part_o, const float
     return make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
 }
 
-// Context element group i (4 elements) of row r: head i*4/hd, chunks
-// holding positions 0..pos.
-__device__ __forceinline__ float4 attn_combine_row4(const float* part_o, const float* part_ml, int r, uint32_t pos,
-                                                    int nh, int hd, int splits, int i) {
-    const int e = i * 4, h = e / hd, d = e - h * hd;
-    const size_t hs = ((size_t)r * nh + h) * splits;
-    const int ns = ((int)pos + ATTN_KCH) / ATTN_KCH;
-    return attn_combine4(part_o, part_ml, hs, ns, d, hd);
+// The first batch of one head's merge (chunk slots hs..hs+SB-1 below
+// `splits`, all in bounds), loaded before the row's position is known so the
+// loads overlap the position's; attn_combine_first4 masks the slots past the
+// row's chunk count.
+struct AttnFirst4 {
+    float mv[ATTN_SB], lv[ATTN_SB];
+    float4 ov[ATTN_SB];
+};
+__device__ __forceinline__ void attn_load_first4(const float* part_o, const float* part_ml, size_t hs, int splits, int d,
+                                                 int hd, AttnFirst4& b) {
+#pragma unroll
+    for (int j = 0; j < ATTN_SB; ++j) {
+        const bool ld = j < splits;
+        b.mv[j] = ld ? part_ml[2 * (hs + j)] : -INFINITY;
+        b.lv[j] = ld ? part_ml[2 * (hs + j) + 1] : 0.0f;
+        b.ov[j] = ld ? *reinterpret_cast<const float4*>(part_o + (hs + j) * hd + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+// attn_combine4 over ns chunks from a preloaded first batch: the same
+// operations in the same order (the one-batch form when ns <= SB, else the
+// batched form, which reloads).
+__device__ __forceinline__ float4 attn_combine_first4(const float* part_o, const float* part_ml, size_t hs, int ns,
+                                                      int d, int hd, const AttnFirst4& b) {
+    if (ns > ATTN_SB) return attn_combine4(part_o, part_ml, hs, ns, d, hd);
+    float M = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < ATTN_SB; ++j) M = fmaxf(M, j < ns ? b.mv[j] : -INFINITY);
+    float L = 0.0f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < ATTN_SB; ++j) {
+        if (j >= ns) continue;
+        const float w = expf(b.mv[j] - M);
+        L += b.lv[j] * w;
+        o = make_float4(o.x + b.ov[j].x * w, o.y + b.ov[j].y * w, o.z + b.ov[j].z * w, o.w + b.ov[j].w * w);
+    }
+    const float inv = 1.0f / L;
+    return make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
 }
 
 }  // namespace bh

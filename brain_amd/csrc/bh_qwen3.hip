@@ -420,59 +420,99 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     // Decode (ROPE) rows are sequences 0..rows-1 in order, so the sequence
     // needs no load there; elsewhere its load goes out with the position's.
     const size_t sq = ROPE ? (size_t)r : (size_t)p.seq[r];
-    const int t = (int)p.pos[r] + 1;
     const int j0 = sp * KCH;
-    if (j0 >= t) return;
-    const int n = min(KCH, t - j0);
     const int G = p.nh / p.nkv;
     float* qs = attn_dyn;
     float* nk = qs + G * p.hd;
     float* nv = nk + p.hd;
     float* vls = nv + p.hd;
-    const bool last = ROPE && j0 + n == t;  // this chunk ends at the new key
-    const int nc = last ? n - 1 : n;        // keys read from the cache
     const size_t tok0 = sq * p.max_seq + j0;  // cache slot of this chunk's first key
     const size_t base = sq * p.max_seq * p.hkv + (size_t)kh * p.hd;
 
     // Every cache read of the chunk is issued first, so its latency overlaps
     // the query rotation: this lane's K pieces (8 lanes per key, float4
     // along head_dim, at most 8 pieces for head_dim <= 256), the V rows
-    // (4 elements per piece) and the KV8 scales.
+    // (4 elements per piece) and the KV8 scales, for the first `lim` keys.
     const int kk = tid >> 3, l8 = tid & 7;
     constexpr int KP = 256 / 32;
     float4 kv[KP];
-    const size_t kro = base + (size_t)(j0 + kk) * p.hkv;
-#pragma unroll
-    for (int u = 0; u < KP; ++u) {
-        const int c = l8 * 4 + 32 * u;
-        kv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (kk < nc && c < p.hd)
-            kv[u] = KV8 ? i8x4(*reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.kc) + kro + c))
-                        : *reinterpret_cast<const float4*>(static_cast<const float*>(p.kc) + kro + c);
-    }
-    // V is staged through LDS on the decode path only: prefill launches
-    // thousands of these workgroups, and the staging registers cost them
-    // occupancy (measured slower there).
+    uint32_t k8[KV8 ? KP : 1];
+    // V is staged into LDS on the decode path only (prefill launches
+    // thousands of these workgroups and reads V from the cache). The staging
+    // is a direct global->LDS load (no registers): piece q (4 elements) of
+    // the chunk, key q / (hd/4), lands at byte 16q (f32) or 4q (int8 codes)
+    // of vls, i.e. row-major [KCH][hd], so one wave instruction fills 64
+    // consecutive pieces. Completion is awaited with an explicit vmcnt wait
+    // before the barrier that publishes vls.
     constexpr bool VST = ROPE;
     constexpr int VPT = VST ? KCH * 256 / 4 / RT : 0;
     const int hd4 = p.hd >> 2;
     const size_t vbo = base + (size_t)j0 * p.hkv;
-    float4 vf[KV8 || !VST ? 1 : VPT];
-    uint32_t v8[KV8 && VST ? VPT : 1];
-#pragma unroll
-    for (int u = 0; u < VPT; ++u) {
-        const int q = tid + u * RT;
-        if (q >= nc * hd4) break;
-        const int k = q / hd4, c = (q - k * hd4) * 4;
-        if constexpr (KV8) v8[u] = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.vc) + vbo + (size_t)k * p.hkv + c);
-        else vf[u] = *reinterpret_cast<const float4*>(static_cast<const float*>(p.vc) + vbo + (size_t)k * p.hkv + c);
-    }
+    const uint32_t vls_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)vls;
     float scl = 0.0f;  // KV8: ksc[tid] (tid < KCH) or vsc[tid - KCH]
-    if constexpr (KV8) {
-        const int k = tid < KCH ? tid : tid - KCH;
-        if (tid < 2 * KCH && k < nc) scl = (tid < KCH ? p.ks : p.vs)[(tok0 + k) * p.nkv + kh];
+    // The loads are unconditional, at indices clamped into the first `lim`
+    // (>= 1) keys, so none sits behind a branch: a load under a condition
+    // has its value moved at the join, which waits for it before the next
+    // load goes out. Lanes past `lim` get a repeat of a valid key, masked
+    // (K) or never used (V, scales).
+    auto load_chunk = [&](int lim) {
+        const size_t kro = base + (size_t)(j0 + min(kk, lim - 1)) * p.hkv;
+#pragma unroll
+        for (int u = 0; u < KP; ++u) {
+            // Pieces past head_dim repeat its last piece (masked below).
+            const int c = min(l8 * 4 + 32 * u, p.hd - 4);
+            if constexpr (KV8) k8[u] = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.kc) + kro + c);
+            else kv[u] = *reinterpret_cast<const float4*>(static_cast<const float*>(p.kc) + kro + c);
+        }
+#pragma unroll
+        for (int u = 0; u < VPT; ++u) {
+            const int q0 = tid + u * RT;
+            if (q0 - (tid & 63) >= KCH * hd4) break;  // whole waves past the chunk (uniform per wave)
+            if (q0 >= KCH * hd4) continue;
+            const int q = min(q0, lim * hd4 - 1);  // pieces past `lim` keys repeat a valid one (never read)
+            const int k = q / hd4, c = (q - k * hd4) * 4;
+            const uint32_t dst = __builtin_amdgcn_readfirstlane(vls_lds + (uint32_t)(q0 - (tid & 63)) * (KV8 ? 4u : 16u));
+            if constexpr (KV8) {
+                const uint8_t* src = static_cast<const uint8_t*>(p.vc) + vbo + (size_t)k * p.hkv + c;
+                asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+                             :
+                             : "v"(src), "s"(dst)
+                             : "memory", "m0");
+            } else {
+                const float* src = static_cast<const float*>(p.vc) + vbo + (size_t)k * p.hkv + c;
+                asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                             :
+                             : "v"(src), "s"(dst)
+                             : "memory", "m0");
+            }
+        }
+        if constexpr (KV8) {
+            const int k = min(tid < KCH ? tid : tid - KCH, lim - 1);
+            scl = (tid < KCH ? p.ks : p.vs)[(tok0 + k) * p.nkv + kh];
+        }
+    };
+    // Decode (ROPE): the chunk's addresses do not depend on the row's
+    // position, so its reads go out before the position arrives, over every
+    // key slot of the chunk inside the cache.
+    if constexpr (ROPE) {
+        load_chunk(min(KCH, p.max_seq - j0));
+        // Keeps the loads above the early exit below (the compiler would
+        // otherwise sink them past it, behind the position's load).
+        asm volatile("" ::: "memory");
     }
-
+    const int t = (int)p.pos[r] + 1;
+    if (j0 >= t) return;
+    const int n = min(KCH, t - j0);
+    const bool last = ROPE && j0 + n == t;  // this chunk ends at the new key
+    const int nc = last ? n - 1 : n;        // keys read from the cache
+    if constexpr (!ROPE) load_chunk(nc);
+    // Keys past the cached ones contribute zeros.
+#pragma unroll
+    for (int u = 0; u < KP; ++u) {
+        const int c = l8 * 4 + 32 * u;
+        if constexpr (KV8) kv[u] = i8x4(k8[u]);
+        if (kk >= nc || c >= p.hd) kv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     if constexpr (ROPE) {
         const int wave = tid >> 6, lane = tid & 63, half = p.hd >> 1;
         const RopeArgs& ro = p.ro;
@@ -503,14 +543,8 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     } else {
         for (int i = tid; i < G * p.hd; i += RT) qs[i] = p.q[(size_t)r * p.hq + (size_t)kh * G * p.hd + i];
     }
-#pragma unroll
-    for (int u = 0; u < VPT; ++u) {
-        const int q = tid + u * RT;
-        if (q >= nc * hd4) break;
-        const int k = q / hd4, c = (q - k * hd4) * 4;
-        if constexpr (KV8) *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(vls) + k * p.hd + c) = v8[u];
-        else *reinterpret_cast<float4*>(vls + k * p.hd + c) = vf[u];
-    }
+    // The V staging loads (and every other load of this wave) have landed.
+    if constexpr (VST) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();  // qs, nk, nv, newsc, vls
     if constexpr (KV8) {
         if (tid < KCH) ksc[tid] = tid < n ? (tid < nc ? scl : newsc[0]) : 0.0f;
@@ -786,11 +820,25 @@ __global__ __launch_bounds__(RT) void attn_combine_quant_kernel(const float* par
     __shared__ float red[RT / 64];
     const int r = blockIdx.x;
     const int q4 = hq >> 2;
+    // Every partial load of the row goes out before the row's position (the
+    // number of live chunks) is read.
     float4 y[GQ];
+    AttnFirst4 fb[GQ];
+    size_t hs[GQ];
+    int dd[GQ];
 #pragma unroll
     for (int g = 0; g < GQ; ++g) {
         const int i = threadIdx.x + g * RT;
-        y[g] = i < q4 ? attn_combine_row4(part_o, part_ml, r, pos[r], nh, hd, splits, i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int e = (i < q4 ? i : 0) * 4, h = e / hd;
+        dd[g] = e - h * hd;
+        hs[g] = ((size_t)r * nh + h) * splits;
+        attn_load_first4(part_o, part_ml, hs[g], i < q4 ? splits : 0, dd[g], hd, fb[g]);
+    }
+    const int ns = ((int)pos[r] + ATTN_KCH) / ATTN_KCH;
+#pragma unroll
+    for (int g = 0; g < GQ; ++g) {
+        const int i = threadIdx.x + g * RT;
+        y[g] = i < q4 ? attn_combine_first4(part_o, part_ml, hs[g], ns, dd[g], hd, fb[g]) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     quant_row<GQ>(y, q4, red, sx + r, xq + (size_t)r * q4);
 }
