@@ -820,25 +820,43 @@ __global__ __launch_bounds__(RT) void attn_combine_quant_kernel(const float* par
     __shared__ float red[RT / 64];
     const int r = blockIdx.x;
     const int q4 = hq >> 2;
-    // Every partial load of the row goes out before the row's position (the
-    // number of live chunks) is read.
+    // The partial loads of up to two groups go out before the row's position
+    // (the number of live chunks) is read; wider rows (more than 2048
+    // context elements) take their groups one at a time, as the registers
+    // of more preloaded groups would spill.
+    constexpr int PRE = GQ <= 2 ? GQ : 1;
     float4 y[GQ];
-    AttnFirst4 fb[GQ];
-    size_t hs[GQ];
-    int dd[GQ];
-#pragma unroll
-    for (int g = 0; g < GQ; ++g) {
+    AttnFirst4 fb[PRE];
+    auto group = [&](int g, size_t& hs, int& d) {
         const int i = threadIdx.x + g * RT;
         const int e = (i < q4 ? i : 0) * 4, h = e / hd;
-        dd[g] = e - h * hd;
-        hs[g] = ((size_t)r * nh + h) * splits;
-        attn_load_first4(part_o, part_ml, hs[g], i < q4 ? splits : 0, dd[g], hd, fb[g]);
-    }
-    const int ns = ((int)pos[r] + ATTN_KCH) / ATTN_KCH;
+        d = e - h * hd;
+        hs = ((size_t)r * nh + h) * splits;
+        return i < q4;
+    };
+    if constexpr (PRE == GQ) {
+        size_t hs[GQ];
+        int dd[GQ];
+        bool live[GQ];
 #pragma unroll
-    for (int g = 0; g < GQ; ++g) {
-        const int i = threadIdx.x + g * RT;
-        y[g] = i < q4 ? attn_combine_first4(part_o, part_ml, hs[g], ns, dd[g], hd, fb[g]) : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int g = 0; g < GQ; ++g) {
+            live[g] = group(g, hs[g], dd[g]);
+            attn_load_first4(part_o, part_ml, hs[g], live[g] ? splits : 0, dd[g], hd, fb[g]);
+        }
+        const int ns = ((int)pos[r] + ATTN_KCH) / ATTN_KCH;
+#pragma unroll
+        for (int g = 0; g < GQ; ++g)
+            y[g] = live[g] ? attn_combine_first4(part_o, part_ml, hs[g], ns, dd[g], hd, fb[g]) : make_float4(0.f, 0.f, 0.f, 0.f);
+    } else {
+        const int ns = ((int)pos[r] + ATTN_KCH) / ATTN_KCH;
+#pragma unroll
+        for (int g = 0; g < GQ; ++g) {
+            size_t hs;
+            int d;
+            const bool live = group(g, hs, d);
+            attn_load_first4(part_o, part_ml, hs, live ? splits : 0, d, hd, fb[0]);
+            y[g] = live ? attn_combine_first4(part_o, part_ml, hs, ns, d, hd, fb[0]) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
     }
     quant_row<GQ>(y, q4, red, sx + r, xq + (size_t)r * q4);
 }
