@@ -27,9 +27,7 @@
 
 namespace bh {
 
-constexpr int GV_THREADS = 256;
 constexpr int GV_WAVES = 4;
-constexpr int GV_MAXC = 16;  // max 64-byte chunks a wave holds in registers per pass
 
 struct GemvArgs {
     const uint32_t* xq;
