@@ -89,6 +89,7 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     for (int w = 1; w < RT / 64; ++w) s += red[w];
     return s;
 }
+template <int NT = RT>
 __device__ __forceinline__ float block_max(float v, float* red) {
     v = wave_max(v);
     __syncthreads();
@@ -96,7 +97,7 @@ __device__ __forceinline__ float block_max(float v, float* red) {
     __syncthreads();
     float s = red[0];
 #pragma unroll
-    for (int w = 1; w < RT / 64; ++w) s = fmaxf(s, red[w]);
+    for (int w = 1; w < NT / 64; ++w) s = fmaxf(s, red[w]);
     return s;
 }
 
@@ -105,18 +106,20 @@ __device__ __forceinline__ float absmax4(float4 v) { return fmaxf(fmaxf(fabsf(v.
 
 // Per-token quantization of a row held in registers (G float4 per thread):
 // sx = max(max|y|, 1e-8)/127, q = clamp(rne(y * (1/sx))) as quant_pack.
-template <int G>
+// NT: threads of the block (the row's max is exact in any order, so the
+// result does not depend on it).
+template <int G, int NT = RT>
 __device__ __forceinline__ void quant_row(const float4 (&y)[G], int d4, float* red, float* sx, uint32_t* xq) {
     float am = 0.0f;
 #pragma unroll
     for (int g = 0; g < G; ++g)
-        if (threadIdx.x + g * RT < d4) am = fmaxf(am, absmax4(y[g]));
-    am = block_max(am, red);
+        if (threadIdx.x + g * NT < d4) am = fmaxf(am, absmax4(y[g]));
+    am = block_max<NT>(am, red);
     const float s = fmaxf(am, 1e-8f) / 127.0f;
     const float inv = 1.0f / s;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const int i = threadIdx.x + g * RT;
+        const int i = threadIdx.x + g * NT;
         if (i < d4) xq[i] = quant_word(y[g], inv);
     }
     if (threadIdx.x == 0) *sx = s;
@@ -813,11 +816,11 @@ __global__ __launch_bounds__(RT) void attn_prefill_kernel(AttnArgs p, int rows_p
 // Merge the key chunks of every head of row r: M = max m_s,
 // L = sum l_s e^(m_s - M), ctx = sum o_s e^(m_s - M) / L; then quantize the
 // whole context row for the output projection (quant_pack semantics).
-template <int GQ>
-__global__ __launch_bounds__(RT) void attn_combine_quant_kernel(const float* part_o, const float* part_ml,
+template <int GQ, int NT = RT>
+__global__ __launch_bounds__(NT) void attn_combine_quant_kernel(const float* part_o, const float* part_ml,
                                                                 const uint32_t* pos, int nh, int hd, int hq,
                                                                 int splits, float* sx, uint32_t* xq) {
-    __shared__ float red[RT / 64];
+    __shared__ float red[NT / 64];
     const int r = blockIdx.x;
     const int q4 = hq >> 2;
     // The partial loads of up to two groups go out before the row's position
@@ -828,7 +831,7 @@ __global__ __launch_bounds__(RT) void attn_combine_quant_kernel(const float* par
     float4 y[GQ];
     AttnFirst4 fb[PRE];
     auto group = [&](int g, size_t& hs, int& d) {
-        const int i = threadIdx.x + g * RT;
+        const int i = threadIdx.x + g * NT;
         const int e = (i < q4 ? i : 0) * 4, h = e / hd;
         d = e - h * hd;
         hs = ((size_t)r * nh + h) * splits;
@@ -858,7 +861,7 @@ __global__ __launch_bounds__(RT) void attn_combine_quant_kernel(const float* par
             y[g] = live ? attn_combine_first4(part_o, part_ml, hs, ns, d, hd, fb[0]) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     }
-    quant_row<GQ>(y, q4, red, sx + r, xq + (size_t)r * q4);
+    quant_row<GQ, NT>(y, q4, red, sx + r, xq + (size_t)r * q4);
 }
 
 // Greedy argmax, stage 1: chunk c of row b -> (value, index) with the
@@ -1089,7 +1092,7 @@ int launch_combine_quant(bh_qwen3* e, int rows, int splits) {
     const int nh = (int)e->c.n_heads, hd = (int)e->c.head_dim;
     const uint32_t* pos = e->cur_pos;
     if (groups <= 1) attn_combine_quant_kernel<1><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, pos, nh, hd, hq, splits, e->sx, e->xq);
-    else if (groups <= 2) attn_combine_quant_kernel<2><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, pos, nh, hd, hq, splits, e->sx, e->xq);
+    else if (groups <= 2) attn_combine_quant_kernel<1, 2 * RT><<<rows, 2 * RT, 0, e->stream>>>(e->part_o, e->part_ml, pos, nh, hd, hq, splits, e->sx, e->xq);
     else if (groups <= 4) attn_combine_quant_kernel<4><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, pos, nh, hd, hq, splits, e->sx, e->xq);
     else attn_combine_quant_kernel<8><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, pos, nh, hd, hq, splits, e->sx, e->xq);
     BH_HIP(hipGetLastError(), "attention combine launch");
