@@ -188,9 +188,9 @@ __global__ __launch_bounds__(RT) void norm_quant_kernel(NormQuantArgs p) {
 
 // silu_mul.wgsl (h = g / (1 + exp(-g)) * u) over the stacked gate|up output,
 // then the row's int8 quant.
-template <int G>
-__global__ __launch_bounds__(RT) void swiglu_quant_kernel(const float* gu, int ff, float* sx, uint32_t* xq, int xq_words) {
-    __shared__ float red[RT / 64];
+template <int G, int NT = RT>
+__global__ __launch_bounds__(NT) void swiglu_quant_kernel(const float* gu, int ff, float* sx, uint32_t* xq, int xq_words) {
+    __shared__ float red[NT / 64];
     const int r = blockIdx.x;
     const int d4 = ff >> 2;
     const float4* g4 = reinterpret_cast<const float4*>(gu + (size_t)r * 2 * ff);
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(RT) void swiglu_quant_kernel(const float* gu, int f
     float4 h[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const int i = threadIdx.x + g * RT;
+        const int i = threadIdx.x + g * NT;
         h[g] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (i < d4) {
             const float4 a = g4[i], b = u4[i];
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(RT) void swiglu_quant_kernel(const float* gu, int f
                                a.z / (1.0f + expf(-a.z)) * b.z, a.w / (1.0f + expf(-a.w)) * b.w);
         }
     }
-    quant_row<G>(h, d4, red, sx + r, xq + (size_t)r * xq_words);
+    quant_row<G, NT>(h, d4, red, sx + r, xq + (size_t)r * xq_words);
 }
 
 struct RopeArgs {
@@ -1077,7 +1077,7 @@ int launch_swiglu_quant(bh_qwen3* e, int rows) {
     const int groups = (ff / 4 + RT - 1) / RT;
     if (groups <= 1) swiglu_quant_kernel<1><<<rows, RT, 0, e->stream>>>(e->gu, ff, e->sx, e->xq, ff / 4);
     else if (groups <= 2) swiglu_quant_kernel<2><<<rows, RT, 0, e->stream>>>(e->gu, ff, e->sx, e->xq, ff / 4);
-    else if (groups <= 4) swiglu_quant_kernel<4><<<rows, RT, 0, e->stream>>>(e->gu, ff, e->sx, e->xq, ff / 4);
+    else if (groups <= 4) swiglu_quant_kernel<1, 4 * RT><<<rows, 4 * RT, 0, e->stream>>>(e->gu, ff, e->sx, e->xq, ff / 4);
     else swiglu_quant_kernel<8><<<rows, RT, 0, e->stream>>>(e->gu, ff, e->sx, e->xq, ff / 4);
     BH_HIP(hipGetLastError(), "swiglu_quant launch");
     return BH_OK;
