@@ -100,6 +100,48 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
 
     float* sxs = reinterpret_cast<float*>(xs + MT * 16 * xstride);  // XMODE 2-4: row scales
     if constexpr (XMODE == 3 || XMODE == 4) {
+      if (XMODE == 4 && m == 1) {
+        // One row (batch-1 decode): the whole workgroup shares it, one float4
+        // of the SwiGLU output per thread (K <= 4096 and NW >= 4 waves give at
+        // most four), instead of one group of 256 threads taking them all.
+        // Elementwise the same arithmetic, and the row max is exact in any
+        // order, so the codes and the scale are the ones below.
+        constexpr int NTH = NW * 64, GX = (1024 + NTH - 1) / NTH;
+        __shared__ float pm[NW];
+        const int d = kbytes, d4 = d >> 2;
+        const float4* g4 = reinterpret_cast<const float4*>(a.pre_a);
+        const float4* u4 = g4 + d4;
+        float4 h[GX];
+        float am = 0.0f;
+#pragma unroll
+        for (int gi = 0; gi < GX; ++gi) {
+            const int i = threadIdx.x + NTH * gi;
+            h[gi] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (i < d4) {
+                const float4 gv = g4[i], uv = u4[i];
+                h[gi] = make_float4(gv.x / (1.0f + expf(-gv.x)) * uv.x, gv.y / (1.0f + expf(-gv.y)) * uv.y,
+                                    gv.z / (1.0f + expf(-gv.z)) * uv.z, gv.w / (1.0f + expf(-gv.w)) * uv.w);
+                am = fmaxf(am, fmaxf(fmaxf(fabsf(h[gi].x), fabsf(h[gi].y)), fmaxf(fabsf(h[gi].z), fabsf(h[gi].w))));
+            }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+        if (lane == 0) pm[wave] = am;
+        __syncthreads();
+        float rm = pm[0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) rm = fmaxf(rm, pm[w]);
+        const float sxv = fmaxf(rm, 1e-8f) / 127.0f;
+        const float invq = 1.0f / sxv;
+#pragma unroll
+        for (int gi = 0; gi < GX; ++gi) {
+            const int i = threadIdx.x + NTH * gi;
+            if (i < d4) *reinterpret_cast<uint32_t*>(xs + 4 * i) = quant_word(h[gi], invq);
+        }
+        if (threadIdx.x < 4) *reinterpret_cast<uint32_t*>(xs + d + 4 * threadIdx.x) = 0u;  // pad past K
+        if (threadIdx.x == 0) sxs[0] = sxv;
+        __syncthreads();
+      } else {
         // Rows in groups of 256 threads (NW/4 rows per round). The sum of
         // squares uses exactly the reduction of the decoder's separate
         // norm_quant kernel -- thread t accumulates float4 groups t, t+256, ...
@@ -192,6 +234,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
             }
             __syncthreads();  // gred is reused by the next round
         }
+      }
     } else if constexpr (XMODE == 2) {
         // Each row is split across wpr = NW/m waves (1 when m >= NW): partial
         // maxima meet in LDS, then every wave quantizes its share of the row.

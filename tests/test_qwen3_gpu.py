@@ -253,8 +253,9 @@ def test_kv_int8_chunking_graph_and_clip(gpu):
 @pytest.mark.parametrize("batch,kv_int8", [(1, 0), (3, 0), (6, 0), (2, 1), (6, 1)])
 def test_fused_decode_is_bit_identical_to_unfused(gpu, batch, kv_int8):
     """Decode with the producers inside their consumers (rotation + cache
-    append inside attention; merge, RMSNorm and SwiGLU inside the following
-    GEMV's prologue; up to 4 rows) against every producer as its own kernel:
+    append inside attention; RMSNorm and SwiGLU inside the following GEMV's
+    prologue, up to 4 rows, one row taking the SwiGLU path that spreads the
+    row over the whole workgroup) against every producer as its own kernel:
     tokens, logits and the KV cache contents they leave must agree exactly.
     Batch 6 keeps the separate GEMV producers but still fuses the rotation."""
     cfg = dict(SMALL, kv_int8=kv_int8)
