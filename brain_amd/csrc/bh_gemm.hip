@@ -887,10 +887,12 @@ static int choose_splits(long tiles, double per_stage, int m, int kg, int n) {
 //    workgroups, so its time is ~ rounds x (time of one tile). Per round, in
 //    units of a 128x128 tile's time, measured on MI355X: 256x256 costs 4.0
 //    (4x the work at ~1.25x the efficiency: half the LDS-staging bytes per
-//    op), 256x128 on 8 waves 2.2, 128x128 1.25. The cheapest of
-//    4.0 * ceil(t256/256), 2.2 * ceil(t256x128/256) and 1.25 * ceil(t128/256)
+//    op), 256x128 on 8 waves 2.2, 128x128 1.4. The cheapest of
+//    4.0 * ceil(t256/256), 2.2 * ceil(t256x128/256) and 1.4 * ceil(t128/256)
 //    wins (e.g. 8192x1024x3072: 2 rounds of 256x256, one half empty, 8.0; 3
-//    rounds of 256x128, 6.6; 6 rounds of 128x128, 7.5).
+//    rounds of 256x128, 6.6; 6 rounds of 128x128, 8.4; 1152x3840x10240: one
+//    round of 256x256, 4.0, measured 54 us, against 3 rounds of 128x128, 4.2,
+//    measured 71 us).
 //  - Fewer 128x128 tiles than CUs: smaller tiles put more CUs to work. A lone
 //    tile's time is set by how fast one CU streams its operands, so halving a
 //    tile side nearly halves its time. Measured on the prefill sweep shapes at
@@ -906,7 +908,7 @@ static TileChoice choose_tiles(int m, int kg, int n) {
     const long stages = (long)kg * 4 / 64;
     const double c256 = 4.0 * (double)((t256 + CUS - 1) / CUS);
     const double c2x1 = 2.2 * (double)((t2x1 + CUS - 1) / CUS);
-    const double c128 = 1.25 * (double)((t128 + CUS - 1) / CUS);
+    const double c128 = 1.4 * (double)((t128 + CUS - 1) / CUS);
     TileChoice tc{TILE_128, 1};
     if (c256 <= c2x1 && c256 <= c128) tc.cfg = TILE_256;
     else if (c2x1 < c128) tc.cfg = TILE_256x128;
