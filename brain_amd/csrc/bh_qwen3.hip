@@ -504,7 +504,13 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
         asm volatile("" ::: "memory");
     }
     const int t = (int)p.pos[r] + 1;
-    if (j0 >= t) return;
+    if (j0 >= t) {
+        // A chunk past the row: nothing to do, but its V staging loads still
+        // write this workgroup's LDS, so they land before the workgroup ends
+        // and its LDS can go to another.
+        if constexpr (VST) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        return;
+    }
     const int n = min(KCH, t - j0);
     const bool last = ROPE && j0 + n == t;  // this chunk ends at the new key
     const int nc = last ? n - 1 : n;        // keys read from the cache
