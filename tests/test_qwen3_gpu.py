@@ -274,13 +274,16 @@ def test_fused_decode_is_bit_identical_to_unfused(gpu, batch, kv_int8):
     b.close()
 
 
-def test_qwen3_0_6b_fused_decode_matches_unfused(gpu):
-    """The fused decode kernels at the config-3 shapes (head_dim 128, K=2048
-    merge prologue, 16 waves per GEMV workgroup) against the separate ones."""
-    prompts = np.random.default_rng(5).integers(0, QWEN3_0_6B["vocab"], size=(2, 40))
+@pytest.mark.parametrize("batch", [1, 2, 8])
+def test_qwen3_0_6b_fused_decode_matches_unfused(gpu, batch):
+    """The fused decode kernels at the config-3 shapes (head_dim 128, a
+    2048-wide merge on 512 threads, 16 waves per GEMV workgroup; batch 1 takes
+    the one-row SwiGLU prologue, batch 8 the separate producers on 1024-thread
+    SwiGLU rows) against the separate ones."""
+    prompts = np.random.default_rng(5).integers(0, QWEN3_0_6B["vocab"], size=(batch, 40))
     out = []
     for unfused in (False, True):
-        e = Qwen3Engine(QWEN3_0_6B, 2, 64, max_rows=128)
+        e = Qwen3Engine(QWEN3_0_6B, batch, 64, max_rows=8 * 64)
         e.init_random(11)
         out.append((e.generate(prompts, 6, eager=unfused, unfused=unfused), e.logits()))
         e.close()
