@@ -45,7 +45,9 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on CPU-baseline work")
-    ap.add_argument("--only", default="", help="profiling aid: 'decode', 'gemv', 'prefill', 'qwen3', 'dit', 'w4a8' or 'copy' only")
+    ap.add_argument("--only", default="", help="profiling aid: 'decode', 'gemv', 'prefill', 'quant', 'qwen3', 'dit', "
+                    "'w4a8' or 'copy' only")
+    ap.add_argument("--no-quant", action="store_true")
     ap.add_argument("--no-qwen3", action="store_true")
     ap.add_argument("--no-dit", action="store_true")
     ap.add_argument("--no-w4a8", action="store_true")
@@ -328,6 +330,73 @@ def bench_w4a8(reps=20):
     return out
 
 
+def bench_quant(reps=20):
+    """Per-token activation quantization at the configs[2] activation shapes
+    (max_abs_rows.wgsl + quant_pack.wgsl, HBM-bound): the single-pass
+    bh_quantize_rows (reads the f32 row once) and the reference's two passes
+    (bh_max_abs_rows, then bh_quant_pack: the row is read twice), plus the
+    bf16 rows of the DiT stack. One HIP graph per shape of at least `reps`
+    launches cycling over input copies that together exceed the 256 MB
+    Infinity Cache, so every launch reads its rows from HBM. GB/s over the
+    algorithmic bytes: f32 reads 4MK per pass, the int8 codes MK, the scales
+    4M per write or read."""
+    import torch
+    from brain_amd import ops
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    out = {"f32": [], "bf16": []}
+
+    def timed(fns):
+        n = max(reps, len(fns))
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for fn in fns:
+                fn()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=s):
+            for i in range(n):
+                fns[i % len(fns)]()
+        gr.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        gr.replay()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n
+
+    def ncopies(nbytes):
+        return max(2, min(256, -(-(640 << 20) // nbytes)))
+
+    for m in (512, 2048, 8192):
+        for k in (1024, 3072, 4096):
+            copies = ncopies(4 * m * k)
+            xs = [torch.randn(m, k, device=dev, generator=g) for _ in range(copies)]
+            sx = torch.empty(m, device=dev)
+            xq = torch.empty(m, k // 4, dtype=torch.int32, device=dev)
+            one = timed([lambda x=x: ops.quantize_rows(x, sx, xq) for x in xs])
+            two = timed([lambda x=x: (ops.max_abs_rows(x, sx), ops.quant_pack(x, sx, xq)) for x in xs])
+            b1 = 4 * m * k + m * k + 4 * m
+            b2 = 8 * m * k + m * k + 12 * m
+            out["f32"].append({"m": m, "k": k, "one_pass_us": round(one * 1e6, 2),
+                               "one_pass_gbs": round(b1 / one / 1e9, 1),
+                               "one_pass_frac": round(b1 / one / 1e9 / HBM_PEAK_GBS, 3),
+                               "two_pass_us": round(two * 1e6, 2), "two_pass_gbs": round(b2 / two / 1e9, 1)})
+            del xs
+    for m, k in ((1152, 3840), (1152, 10240)):
+        copies = ncopies(2 * m * k)
+        xs = [torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16) for _ in range(copies)]
+        sx = torch.empty(m, device=dev)
+        xq = torch.empty(m, k // 4, dtype=torch.int32, device=dev)
+        dt = timed([lambda x=x: ops.quantize_rows_bf16(x, sx, xq) for x in xs])
+        b = 2 * m * k + m * k + 4 * m
+        out["bf16"].append({"m": m, "k": k, "us": round(dt * 1e6, 2), "gbs": round(b / dt / 1e9, 1),
+                            "frac": round(b / dt / 1e9 / HBM_PEAK_GBS, 3)})
+        del xs
+    return out
+
+
 def qwen3_weight_bytes(c):
     """int8 weight + scale bytes one decode step streams (every linear + the head)."""
     d, ff, hq, hkv = c["d_model"], c["d_ff"], c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
@@ -510,6 +579,8 @@ def main():
         del sets
     if args.only in ("", "prefill") and not args.no_prefill:
         res["prefill"] = bench_prefill(torch, lib, dev, gen, args.prefill_reps)
+    if args.only in ("", "quant") and not args.no_quant:
+        res["quant"] = bench_quant()
     if args.only in ("", "qwen3") and not args.no_qwen3:
         res["qwen3"] = bench_qwen3(cpu=not args.no_cpu)
     if args.only in ("", "dit") and not args.no_dit:
@@ -567,6 +638,8 @@ def main():
             g = [r for r in res["prefill"]["shapes"] if (r["m"], r["k"], r["n"]) == (512, 1024, 3072)]
             if g:
                 line["prefill_gpu_vs_cpu_tiled"] = round(g[0]["tops"] / pcpu["tiled_i32"]["value"], 1)
+    if "quant" in res:
+        line["activation_quant"] = res["quant"]
     if "qwen3" in res:
         line["qwen3_e2e"] = res["qwen3"]
     if "dit" in res:

@@ -63,7 +63,8 @@ def test_f32_to_bf16_matches_reference_rule(gpu):
 
 
 # ---------------------------------------------------------------- quantization
-QUANT_SHAPES = [(1, 4), (1, 1024), (3, 8), (4, 36), (16, 1024), (7, 3072), (64, 4096), (513, 1024), (5, 10240)]
+QUANT_SHAPES = [(1, 4), (1, 1024), (3, 8), (4, 36), (16, 1024), (7, 3072), (64, 4096), (513, 1024), (5, 10240),
+                (1027, 1024), (2048, 504), (1024, 4)]
 
 
 @pytest.mark.parametrize("m,k", QUANT_SHAPES)
