@@ -394,6 +394,41 @@ def bench_quant(reps=20):
         out["bf16"].append({"m": m, "k": k, "us": round(dt * 1e6, 2), "gbs": round(b / dt / 1e9, 1),
                             "frac": round(b / dt / 1e9 / HBM_PEAK_GBS, 3)})
         del xs
+    # Weight quantization (model::int8::quantize_weight, load time): the device
+    # kernel over f32 [N, K] (4NK + NK + 4N bytes) and the host quantizer the
+    # reference runs at load (rayon over rows), here row-parallel C++.
+    import ctypes
+    import numpy as np
+    from brain_amd import _lib
+    out["weights"] = []
+    for n, k in ((11008, 4096), (151936, 1024)):
+        w = torch.randn(n, k, device=dev, generator=g)
+        packed = torch.empty(n, k // 4, dtype=torch.int32, device=dev)
+        sw = torch.empty(n, device=dev)
+        lib = _lib.load()
+        fn = lambda: _lib.check(lib.bh_quantize_weight_device(ops._stream(), w.data_ptr(), n, k,
+                                                              packed.data_ptr(), sw.data_ptr()))
+        dt = timed([fn])
+        b = 5 * n * k + 4 * n
+        row = {"n": n, "k": k, "device_us": round(dt * 1e6, 1), "device_gbs": round(b / dt / 1e9, 1),
+               "device_frac": round(b / dt / 1e9 / HBM_PEAK_GBS, 3)}
+        if n == 11008:
+            wh = w.cpu().numpy()
+            ph = np.empty((n, k // 4), np.uint32)
+            sh = np.empty(n, np.float32)
+            args = (wh.ctypes.data_as(ctypes.c_void_p), n, k, ph.ctypes.data_as(ctypes.c_void_p),
+                    sh.ctypes.data_as(ctypes.c_void_p))
+            _lib.check(lib.bh_quantize_weight(*args))
+            t0 = time.perf_counter()
+            for _ in range(3):
+                _lib.check(lib.bh_quantize_weight(*args))
+            ht = (time.perf_counter() - t0) / 3
+            row.update({"host_ms": round(ht * 1e3, 1), "host_gbs": round(b / ht / 1e9, 1),
+                        "host_threads": min(int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count(),
+                                            os.cpu_count())})
+            assert (ph.view(np.int32) == packed.cpu().numpy()).all(), "host and device weight codes differ"
+        out["weights"].append(row)
+        del w, packed
     return out
 
 

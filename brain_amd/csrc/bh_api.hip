@@ -552,9 +552,20 @@ int bh_tune_load(const char* path) {
 }
 
 // ---------------------------------------------------------------- host quantizer
-static void parallel_rows(uint64_t n, const std::function<void(uint64_t, uint64_t)>& fn) {
+// Host threads for row-parallel work: OMP_NUM_THREADS when set (the CPU share
+// a job is given), else the hardware's thread count.
+static unsigned host_threads() {
     unsigned hw = std::thread::hardware_concurrency();
-    uint64_t nt = std::min<uint64_t>(hw ? hw : 1, std::max<uint64_t>(1, n / 16));
+    if (const char* e = getenv("OMP_NUM_THREADS")) {
+        const int v = atoi(e);
+        if (v > 0) return hw ? std::min<unsigned>((unsigned)v, hw) : (unsigned)v;
+    }
+    return hw ? hw : 1;
+}
+
+static void parallel_rows(uint64_t n, const std::function<void(uint64_t, uint64_t)>& fn) {
+    const unsigned hw = host_threads();
+    uint64_t nt = std::min<uint64_t>(hw, std::max<uint64_t>(1, n / 16));
     if (nt <= 1) {
         fn(0, n);
         return;

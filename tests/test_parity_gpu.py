@@ -299,7 +299,8 @@ def test_linear_fused_quant(gpu, m, k, n):
     assert (gotb[:, cols] == wantb).all()
 
 
-@pytest.mark.parametrize("n,k", [(1, 64), (3, 8), (17, 24), (64, 4096), (129, 128), (300, 1000)])
+@pytest.mark.parametrize("n,k", [(1, 64), (3, 8), (17, 24), (64, 4096), (129, 128), (300, 1000), (5, 2052),
+                                 (6, 1500), (33, 4100)])
 def test_device_weight_quantizer(gpu, n, k):
     rng = np.random.default_rng(n + k)
     w = (rng.standard_normal((n, k)) * rng.uniform(0.1, 10, (n, 1))).astype(np.float32)
