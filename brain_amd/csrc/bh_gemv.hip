@@ -23,6 +23,7 @@
 //   - fused epilogue: dequant, bias, bf16 RNE.
 #include <cstdlib>
 
+#include "bh_attn.h"
 #include "bh_common.h"
 
 namespace bh {
@@ -56,6 +57,13 @@ struct GemvArgs {
     const float* pre_w;
     float* res_out;
     float eps;
+    // XMODE 5 (the decoder's attention merge fused into the output
+    // projection): the per-chunk partials and row positions of the split
+    // attention; x = merge(part_o, part_ml) of row r over its chunks.
+    const float* part_o = nullptr;
+    const float* part_ml = nullptr;
+    const uint32_t* pos = nullptr;
+    int nh = 0, hd = 0, splits = 0;
 };
 
 // XMODE: 0 = packed activation read from global memory, 1 = staged into
@@ -274,6 +282,61 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
                 }
             }
             __syncthreads();  // pmax is reused by the next round
+        }
+    } else if constexpr (XMODE == 5) {
+        // Rows one at a time, the whole workgroup on each: every thread merges
+        // one 4-element context group (the partial loads go out before the
+        // row's position is read), then the row's int8 quantization. The same
+        // operations as the separate merge kernel (attn_combine_first4, the
+        // row max exact in any order), so the codes and scales are its own.
+        // K <= 2048 (launch_gemv_i8_merge): one group per thread from 8 waves,
+        // which keeps a thread's 16 preloaded chunk slots in registers.
+        constexpr int NTH = NW * 64, GX = (512 + NTH - 1) / NTH;
+        __shared__ float pm[NW];
+        const int q4 = kbytes >> 2;
+        for (int r = 0; r < m; ++r) {
+            AttnFirst4 fb[GX];
+            size_t hs[GX];
+            int dd[GX];
+            bool live[GX];
+#pragma unroll
+            for (int gi = 0; gi < GX; ++gi) {
+                const int i = threadIdx.x + NTH * gi;
+                live[gi] = i < q4;
+                const int e = (live[gi] ? i : 0) * 4, h = e / a.hd;
+                dd[gi] = e - h * a.hd;
+                hs[gi] = ((size_t)r * a.nh + h) * a.splits;
+                attn_load_first4(a.part_o, a.part_ml, hs[gi], live[gi] ? a.splits : 0, dd[gi], a.hd, fb[gi]);
+            }
+            const int ns = ((int)a.pos[r] + ATTN_KCH) / ATTN_KCH;
+            float4 y[GX];
+            float am = 0.0f;
+#pragma unroll
+            for (int gi = 0; gi < GX; ++gi) {
+                y[gi] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (live[gi]) {
+                    y[gi] = attn_combine_first4(a.part_o, a.part_ml, hs[gi], ns, dd[gi], a.hd, fb[gi]);
+                    am = fmaxf(am, fmaxf(fmaxf(fabsf(y[gi].x), fabsf(y[gi].y)), fmaxf(fabsf(y[gi].z), fabsf(y[gi].w))));
+                }
+            }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+            if (lane == 0) pm[wave] = am;
+            __syncthreads();
+            float rm = pm[0];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) rm = fmaxf(rm, pm[w]);
+            const float sxv = fmaxf(rm, 1e-8f) / 127.0f;
+            const float invq = 1.0f / sxv;
+            uint8_t* xr8 = xs + r * xstride;
+#pragma unroll
+            for (int gi = 0; gi < GX; ++gi) {
+                const int i = threadIdx.x + NTH * gi;
+                if (live[gi]) *reinterpret_cast<uint32_t*>(xr8 + 4 * i) = quant_word(y[gi], invq);
+            }
+            if (threadIdx.x < 4) *reinterpret_cast<uint32_t*>(xr8 + kbytes + 4 * threadIdx.x) = 0u;  // pad past K
+            if (threadIdx.x == 0) sxs[r] = sxv;
+            __syncthreads();  // pm is reused by the next row; xs and sxs are complete
         }
     } else if constexpr (XLDS) {
         const int pieces = kbytes >> 4;
@@ -533,6 +596,27 @@ hipError_t launch_gemv_i8_pre(hipStream_t s, int mode, const uint32_t* pre_tok, 
     }
     if (nchunks >= 32) return gv_go<1, OUT_F32, false, true, 4, 1, 16, 4>(s, a);
     return gv_go<1, OUT_F32, false, true, 4, 1, 8, 4>(s, a);
+}
+
+// XMODE 5: out = (merge of the attention partials, quantized) . W^T, f32, for
+// m <= 4 rows, K = nh * hd <= 2048, on 8 waves (512 threads, one 4-element
+// context group each).
+hipError_t launch_gemv_i8_merge(hipStream_t s, const float* part_o, const float* part_ml, const uint32_t* pos, int nh,
+                                int hd, int splits, const uint32_t* wq, const float* sw, float* out, int m, int kg,
+                                int n) {
+    const int kbytes = kg * 4;
+    if (m < 1 || m > 4 || kbytes % 16 != 0 || kbytes > 2048 || kbytes != nh * hd ||
+        (reinterpret_cast<uintptr_t>(wq) & 15u) != 0)
+        return hipErrorNotSupported;
+    GemvArgs a{nullptr, wq, nullptr, sw, nullptr, out, m, kg, n, nullptr, 0, 0, nullptr, nullptr, nullptr,
+               nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0.0f};
+    a.part_o = part_o;
+    a.part_ml = part_ml;
+    a.pos = pos;
+    a.nh = nh;
+    a.hd = hd;
+    a.splits = splits;
+    return gv_go<1, OUT_F32, false, true, 4, 1, 8, 5>(s, a);
 }
 
 }  // namespace bh

@@ -57,6 +57,9 @@ hipError_t launch_gemm_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
 hipError_t launch_gemv_i8_pre(hipStream_t s, int mode, const uint32_t* pre_tok, const float* pre_emb,
                               const float* pre_a, const float* pre_b, const float* pre_w, float* res_out, float eps,
                               const uint32_t* wq, const float* sw, float* out, int m, int kg, int n);
+hipError_t launch_gemv_i8_merge(hipStream_t s, const float* part_o, const float* part_ml, const uint32_t* pos, int nh,
+                                int hd, int splits, const uint32_t* wq, const float* sw, float* out, int m, int kg,
+                                int n);
 
 int tuned_variant(uint32_t m, uint32_t n, uint32_t k);
 
@@ -1206,11 +1209,19 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
             }
             BH_HIP(hipGetLastError(), "attention launch");
         }
-        // (Merging inside the output projection's prologue measured 4x slower
-        // than this separate launch: every GEMV workgroup re-read all the
-        // partials of the row.)
-        BH_TRY(launch_combine_quant(e, rows, splits));
-        BH_TRY(launch_linear(e, Ly.wo, Ly.so, e->proj, rows, (int)e->hq, d));
+        // Up to 4 rows, the merge runs inside the output projection's
+        // prologue: every GEMV workgroup re-reads the row's partials (tens of
+        // KB from L2), one 4-element context group per thread with the loads
+        // issued before the position read, which costs less than a launch.
+        if (fuse && fused_ok(e, rows, (int)e->hq, d) && e->hq <= 2048) {
+            // The merge of the chunks inside the output projection's prologue.
+            BH_HIP(launch_gemv_i8_merge(e->stream, e->part_o, e->part_ml, e->cur_pos, nh, hd, splits, Ly.wo, Ly.so,
+                                        e->proj, rows, (int)e->hq / 4, d),
+                   "fused merge + output projection launch");
+        } else {
+            BH_TRY(launch_combine_quant(e, rows, splits));
+            BH_TRY(launch_linear(e, Ly.wo, Ly.so, e->proj, rows, (int)e->hq, d));
+        }
         if (fuse) {
             BH_HIP(launch_gemv_i8_pre(e->stream, 3, nullptr, nullptr, cur, e->proj, Ly.ln2, nxt, c.rms_eps, Ly.wgu,
                                       Ly.sgu, e->gu, rows, d / 4, 2 * ff),
