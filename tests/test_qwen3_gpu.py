@@ -83,6 +83,35 @@ def compare(cfg, w, prompts, steps, max_rows=None):
     e.close()
 
 
+@pytest.mark.parametrize("batch,plen", [(1, 1), (1, 3), (2, 2), (4, 1)])
+def test_engine_short_prompt_matches_oracle(gpu, batch, plen):
+    """Prompts of at most 4 rows in all: the prefill itself takes the fused
+    producers (RMSNorm, SwiGLU and the attention merge inside the GEMV
+    prologues), which the decode-only comparisons do not reach."""
+    w = scaled_weights(SMALL, seed=41 + plen)
+    prompts = np.random.default_rng(plen + 10 * batch).integers(0, SMALL["vocab"], size=(batch, plen))
+    steps = 5
+    toks_o, logits_o = o.qwen3_generate(SMALL, w, prompts, steps, int8=True)
+    e = engine_for(SMALL, w, batch, plen + steps + 1)
+    got = [(e.prefill(prompts), e.logits())]
+    for _ in range(steps):
+        got.append((e.decode(1)[0], e.logits()))
+    e.close()
+    # One sequence can meet an int8 rounding flip (~5e-3 rel-L2, as with
+    # longer prompts); most steps must still be exact.
+    exact = 0
+    for s_, (tk, lg) in enumerate(got):
+        worst = max(rel_l2(lg[b], logits_o[s_][b]) for b in range(batch))
+        assert worst < 2e-2, (s_, worst)
+        exact += worst < 1e-4
+        top2 = np.sort(logits_o[s_], axis=-1)[:, -2:]
+        clear = (top2[:, 1] - top2[:, 0]) > 2e-2 * np.abs(logits_o[s_]).max()
+        assert (tk[clear] == toks_o[s_][clear]).all(), (s_, tk, toks_o[s_])
+        if not (tk == toks_o[s_]).all():
+            break
+    assert exact >= 3, exact
+
+
 @pytest.mark.parametrize("cfg_over", [{}, dict(tie_embeddings=0), dict(qk_norm=0, n_kv_heads=4), dict(kv_int8=1),
                                       dict(kv_int8=1, n_kv_heads=1, tie_embeddings=0)],
                          ids=["tied", "untied", "mha_no_qknorm", "kv_int8", "kv_int8_mqa"])
