@@ -1209,11 +1209,13 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
             }
             BH_HIP(hipGetLastError(), "attention launch");
         }
-        // Up to 4 rows, the merge runs inside the output projection's
-        // prologue: every GEMV workgroup re-reads the row's partials (tens of
-        // KB from L2), one 4-element context group per thread with the loads
-        // issued before the position read, which costs less than a launch.
-        if (fuse && fused_ok(e, rows, (int)e->hq, d) && e->hq <= 2048) {
+        // One row (batch-1 decode): the merge runs inside the output
+        // projection's prologue. Every GEMV workgroup re-reads the row's
+        // partials (tens of KB from L2), one 4-element context group per
+        // thread with the loads issued before the position read, which costs
+        // less than a launch. With more rows each workgroup merges them one
+        // after another (measured slower from 2 rows: batch 4 1.19 -> 1.43 ms).
+        if (fuse && rows == 1 && fused_ok(e, rows, (int)e->hq, d) && e->hq <= 2048) {
             // The merge of the chunks inside the output projection's prologue.
             BH_HIP(launch_gemv_i8_merge(e->stream, e->part_o, e->part_ml, e->cur_pos, nh, hd, splits, Ly.wo, Ly.so,
                                         e->proj, rows, (int)e->hq / 4, d),

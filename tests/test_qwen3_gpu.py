@@ -86,8 +86,8 @@ def compare(cfg, w, prompts, steps, max_rows=None):
 @pytest.mark.parametrize("batch,plen", [(1, 1), (1, 3), (2, 2), (4, 1)])
 def test_engine_short_prompt_matches_oracle(gpu, batch, plen):
     """Prompts of at most 4 rows in all: the prefill itself takes the fused
-    producers (RMSNorm, SwiGLU and the attention merge inside the GEMV
-    prologues), which the decode-only comparisons do not reach."""
+    producers (RMSNorm and SwiGLU inside the GEMV prologues; for one row also
+    the attention merge), which the decode-only comparisons do not reach."""
     w = scaled_weights(SMALL, seed=41 + plen)
     prompts = np.random.default_rng(plen + 10 * batch).integers(0, SMALL["vocab"], size=(batch, plen))
     steps = 5
@@ -283,8 +283,9 @@ def test_kv_int8_chunking_graph_and_clip(gpu):
 def test_fused_decode_is_bit_identical_to_unfused(gpu, batch, kv_int8):
     """Decode with the producers inside their consumers (rotation + cache
     append inside attention; RMSNorm and SwiGLU inside the following GEMV's
-    prologue, up to 4 rows, one row taking the SwiGLU path that spreads the
-    row over the whole workgroup) against every producer as its own kernel:
+    prologue, up to 4 rows; one row also takes the SwiGLU path that spreads
+    the row over the whole workgroup and the attention merge inside the output
+    projection) against every producer as its own kernel:
     tokens, logits and the KV cache contents they leave must agree exactly.
     Batch 6 keeps the separate GEMV producers but still fuses the rotation."""
     cfg = dict(SMALL, kv_int8=kv_int8)
