@@ -185,10 +185,14 @@ __global__ __launch_bounds__(QT) void quantize_rows_bf16_kernel(const uint16_t* 
     const uint4* xr = reinterpret_cast<const uint4*>(x + (int64_t)row * k);
     uint4 v[NV];
     float a = 0.0f;
+    // Every load of the row first, at clamped indices (k8 >= 1), so none
+    // waits at a branch join; then the masks and the max.
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = xr[min((int)(threadIdx.x + i * QT), k8 - 1)];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int g = threadIdx.x + i * QT;
-        v[i] = g < k8 ? xr[g] : make_uint4(0u, 0u, 0u, 0u);
+        if (g >= k8) v[i] = make_uint4(0u, 0u, 0u, 0u);
         const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) a = fmaxf(a, fmaxf(fabsf(bf16_lo(w[j])), fabsf(bf16_hi(w[j]))));
@@ -335,7 +339,7 @@ hipError_t launch_quant_pack(hipStream_t s, const float* x, const float* sx, int
 hipError_t launch_quantize_rows_bf16(hipStream_t s, const uint16_t* x, int m, int k, float* sx, uint32_t* xq) {
     if (m <= 0) return hipSuccess;
     const int k8 = k / 8;
-    if (k % 8 == 0 && al16(x) && k8 <= 8 * QT) {
+    if (k % 8 == 0 && al16(x) && k8 >= 1 && k8 <= 8 * QT) {
         if (k8 <= QT) quantize_rows_bf16_kernel<1><<<m, QT, 0, s>>>(x, m, k, sx, xq);
         else if (k8 <= 2 * QT) quantize_rows_bf16_kernel<2><<<m, QT, 0, s>>>(x, m, k, sx, xq);
         else if (k8 <= 4 * QT) quantize_rows_bf16_kernel<4><<<m, QT, 0, s>>>(x, m, k, sx, xq);
