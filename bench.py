@@ -402,13 +402,17 @@ def bench_quant(reps=20):
     from brain_amd import _lib
     out["weights"] = []
     for n, k in ((11008, 4096), (151936, 1024)):
-        w = torch.randn(n, k, device=dev, generator=g)
+        # Copies that together exceed the Infinity Cache, as above.
+        ws = [torch.randn(n, k, device=dev, generator=g) for _ in range(ncopies(4 * n * k))]
+        w = ws[0]
         packed = torch.empty(n, k // 4, dtype=torch.int32, device=dev)
         sw = torch.empty(n, device=dev)
         lib = _lib.load()
-        fn = lambda: _lib.check(lib.bh_quantize_weight_device(ops._stream(), w.data_ptr(), n, k,
-                                                              packed.data_ptr(), sw.data_ptr()))
-        dt = timed([fn])
+        dt = timed([lambda wi=wi: _lib.check(lib.bh_quantize_weight_device(ops._stream(), wi.data_ptr(), n, k,
+                                                                            packed.data_ptr(), sw.data_ptr()))
+                    for wi in ws])
+        _lib.check(lib.bh_quantize_weight_device(ops._stream(), w.data_ptr(), n, k, packed.data_ptr(), sw.data_ptr()))
+        torch.cuda.synchronize()
         b = 5 * n * k + 4 * n
         row = {"n": n, "k": k, "device_us": round(dt * 1e6, 1), "device_gbs": round(b / dt / 1e9, 1),
                "device_frac": round(b / dt / 1e9 / HBM_PEAK_GBS, 3)}
@@ -428,7 +432,7 @@ def bench_quant(reps=20):
                                             os.cpu_count())})
             assert (ph.view(np.int32) == packed.cpu().numpy()).all(), "host and device weight codes differ"
         out["weights"].append(row)
-        del w, packed
+        del w, ws, packed
     return out
 
 
