@@ -22,9 +22,16 @@
 //     issued before the activation staging so the two overlap;
 //   - fused epilogue: dequant, bias, bf16 RNE.
 #include <cstdlib>
+#include <type_traits>
 
 #include "bh_attn.h"
 #include "bh_common.h"
+
+// Phase timestamps for latency studies: a timing build defines BH_STAMP(i)
+// to record s_memrealtime at the marked points; the library leaves it empty.
+#ifndef BH_STAMP
+#define BH_STAMP(i)
+#endif
 
 namespace bh {
 
@@ -77,6 +84,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t xs[];  // [MT*16][kbytes+16] when XLDS
     __shared__ int red[KSPLIT > 1 ? NW : 1][CG * MT * 4][64];
 
+    BH_STAMP(0);
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int slot = wave / KSPLIT;   // which column group of this workgroup
@@ -379,16 +387,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
     for (int c = 0; c < CG; ++c)
 #pragma unroll
         for (int t = 0; t < MT; ++t) acc[c][t] = v4i{0, 0, 0, 0};
-#pragma unroll 1
-    for (int j0 = 0; j0 < my_chunks; j0 += U) {
-        if (j0 > 0) {
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                if (j0 + u < my_chunks)
-#pragma unroll
-                    for (int c = 0; c < CG; ++c)
-                        wf[u][c] = load_k16<ALIGNED>(wp[c], (ks + KSPLIT * (j0 + u)) * 64 + ksub, kbytes);
-        }
+    // One batch of U chunks: activation fragments, then the MFMAs. The first
+    // batch is peeled out of the loop so that its activation loads issue
+    // right behind the weight loads already in flight: inside the loop the
+    // compiler waits for every outstanding load at the loop header, which
+    // made the activation a second memory round trip.
+    auto batch = [&](int j0) {
         v4i xf[U][MT];
 #pragma unroll
         for (int u = 0; u < U; ++u)
@@ -403,7 +407,20 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
 #pragma unroll
                     for (int t = 0; t < MT; ++t)
                         acc[c][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xf[u][t], wf[u][c], acc[c][t], 0, 0, 0);
+    };
+    BH_STAMP(1);
+    batch(0);
+#pragma unroll 1
+    for (int j0 = U; j0 < my_chunks; j0 += U) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (j0 + u < my_chunks)
+#pragma unroll
+                for (int c = 0; c < CG; ++c)
+                    wf[u][c] = load_k16<ALIGNED>(wp[c], (ks + KSPLIT * (j0 + u)) * 64 + ksub, kbytes);
+        batch(j0);
     }
+    BH_STAMP(2);
 
     // Lane l, register i of a 16x16 i32 result holds row 4*(l/16)+i, column l%16.
     auto emit = [&](int c, int ri, int s) {
@@ -435,6 +452,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) red[wave][(c * MT + t) * 4 + i][lane] = acc[c][t][i];
         __syncthreads();
+        BH_STAMP(3);
         for (int q = ks; q < CG * MT * 4; q += KSPLIT) {
             const int c = q / (MT * 4), ri = q % (MT * 4);
             if (g0 + c >= ngroups) continue;
@@ -443,6 +461,165 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
             for (int w = 0; w < KSPLIT; ++w) s += red[slot * KSPLIT + w][q][lane];
             emit(c, ri, s);
         }
+    }
+    BH_STAMP(4);
+}
+
+// Wide N (the LM head: thousands of 16-column groups), m <= 16: a resident
+// grid streams W. Each wave owns every nwaves-th column group (an equal share)
+// and covers the whole K of each, so there is no cross-wave sum and no
+// barrier after the prologue. The packed activation is staged in LDS once
+// per workgroup (its loads go out ahead of the first weights), so the
+// L2 serves m*K bytes per workgroup instead of per column group. A wave keeps
+// the weight loads of its next work item in flight while it multiplies the
+// current one (two register sets, alternating), and the column scale of an
+// item is loaded ahead of its weights, so no wait in the loop drains the
+// memory pipe. Work items are (column group, batch of U = 16 64-byte K
+// chunks); K (= KB bytes) is a compile-time multiple of 1024.
+template <int OUT, bool HAS_BIAS, int KB>
+__global__ __launch_bounds__(256) void gemv_i8_stream_kernel(GemvArgs a, int groups_per_wave) {
+    constexpr int U = 16, kbytes = KB, nbatch = KB / 1024;
+    __shared__ __attribute__((aligned(16))) uint8_t xs[16 * (KB + 16)];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int m = a.m, n = a.n;
+    const int ngroups = (n + 15) >> 4;
+    constexpr int xstride = kbytes + 16;
+    const int ksub = (lane >> 4) * 16;
+    const int nwaves = gridDim.x * 4;
+    const int gw = blockIdx.x * 4 + wave;
+    // This wave's groups: gw + i * nwaves for i < ng.
+    int ng = gw < ngroups ? (ngroups - 1 - gw) / nwaves + 1 : 0;
+    ng = ng < groups_per_wave ? ng : groups_per_wave;
+    const int items = ng * nbatch;
+
+    struct Item {
+        v4i w[U];
+        float sw, bias;
+    };
+    auto load_item = [&](Item& it, int j) {
+        const int i = j / nbatch, b = j - i * nbatch;
+        const int g = gw + i * nwaves;
+        int r = g * 16 + (lane & 15);
+        r = r < n ? r : n - 1;  // clamped rows are loaded but never stored
+        if (b == 0) {
+            it.sw = OUT != OUT_I32 ? a.sw[r] : 0.0f;
+            it.bias = HAS_BIAS ? a.bias[r] : 0.0f;
+        }
+        const uint8_t* rp = reinterpret_cast<const uint8_t*>(a.wq) + (int64_t)r * kbytes + b * U * 64 + ksub;
+#pragma unroll
+        for (int u = 0; u < U; ++u) it.w[u] = *reinterpret_cast<const v4i*>(rp + u * 64);
+    };
+
+    // Activation image: 16 rows plus a 16-byte pad per row. Rows >= m repeat
+    // row 0: they only feed accumulator rows that are never stored, and an
+    // unconditional load keeps the compiler from turning it into a branch
+    // (which would make it wait for the weights). Every thread loads its
+    // kbytes/256 pieces first, then its first item's weights, and waits only
+    // for the pieces before the LDS writes.
+    constexpr int pieces = kbytes >> 4, nst = kbytes >> 8;
+    v4i st[nst];
+#pragma unroll
+    for (int i = 0; i < nst; ++i) {
+        const int p = threadIdx.x + 256 * i;
+        const int r = p / pieces, c = p - r * pieces;
+        st[i] = *reinterpret_cast<const v4i*>(reinterpret_cast<const uint8_t*>(a.xq) +
+                                              (int64_t)(r < m ? r : 0) * kbytes + c * 16);
+    }
+    Item ia, ib;
+    load_item(ia, 0);  // unconditional (rows clamped), so the waits below count only the pieces
+#pragma unroll
+    for (int i = 0; i < nst; ++i) {
+        const int p = threadIdx.x + 256 * i;
+        const int r = p / pieces, c = p - r * pieces;
+        *reinterpret_cast<v4i*>(xs + r * xstride + c * 16) = st[i];
+    }
+    if (threadIdx.x < 16) *reinterpret_cast<v4i*>(xs + threadIdx.x * xstride + kbytes) = v4i{0, 0, 0, 0};
+    float sxr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = 4 * (lane >> 4) + i;
+        sxr[i] = (OUT != OUT_I32 && row < m) ? a.sx[row] : 0.0f;
+    }
+    __syncthreads();
+    if (items == 0) return;
+
+    const uint8_t* xrow = xs + (lane & 15) * xstride + ksub;
+    v4i acc = {0, 0, 0, 0};
+    // Results of the last npend groups (slot k = group i_last - k), not yet stored.
+    constexpr int NPEND = 8;
+    using PendT = typename std::conditional<OUT == OUT_I32, int, float>::type;
+    PendT pend[NPEND][4];
+#pragma unroll
+    for (int k = 0; k < NPEND; ++k)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pend[k][q] = 0;  // defined values: the shift below reads every slot
+    int npend = 0;
+    auto flush = [&](int i_last) {
+#pragma unroll
+        for (int k = 0; k < NPEND; ++k) {
+            if (k < npend) {
+                const int col = (gw + (i_last - k) * nwaves) * 16 + (lane & 15);
+                if (col < n) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int row = 4 * (lane >> 4) + q;
+                        if (row < m) {
+                            const int64_t idx = (int64_t)row * n + col;
+                            if constexpr (OUT == OUT_I32) reinterpret_cast<int*>(a.out)[idx] = pend[k][q];
+                            else store_out<OUT>(a.out, idx, pend[k][q]);
+                        }
+                    }
+                }
+            }
+        }
+        npend = 0;
+    };
+    auto consume = [&](const Item& it, int j) {
+        const int i = j / nbatch, b = j - i * nbatch;
+        const uint8_t* xp = xrow + b * U * 64;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const v4i xf = *reinterpret_cast<const v4i*>(xp + u * 64);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(xf, it.w[u], acc, 0, 0, 0);
+        }
+        if (b != nbatch - 1) return;
+        // Park the group's results; the stores go out in bursts of NPEND
+        // groups (at the end of the wave for the LM head). A store in the loop
+        // would sit in the in-order vmcnt queue ahead of the next item's
+        // weights, so the next wait would also wait for its write ack.
+#pragma unroll
+        for (int k = NPEND - 1; k > 0; --k)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) pend[k][q] = pend[k - 1][q];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if constexpr (OUT == OUT_I32) {
+                pend[0][q] = acc[q];
+            } else {
+                float v = dequant(acc[q], sxr[q], it.sw);
+                if constexpr (HAS_BIAS) v = v + it.bias;
+                pend[0][q] = v;
+            }
+        }
+        acc = v4i{0, 0, 0, 0};
+        if (++npend == NPEND || i == ng - 1) flush(i);
+    };
+    // Two register sets: item j in ia (j even) or ib (j odd).
+#pragma unroll 1
+    for (int j = 0;; j += 2) {
+        if (j + 1 >= items) {
+            consume(ia, j);
+            break;
+        }
+        load_item(ib, j + 1);
+        consume(ia, j);
+        if (j + 2 >= items) {
+            consume(ib, j + 1);
+            break;
+        }
+        load_item(ia, j + 2);
+        consume(ib, j + 1);
     }
 }
 
@@ -467,6 +644,35 @@ static hipError_t gv_go(hipStream_t s, const GemvArgs& a) {
     return hipGetLastError();
 }
 
+// The streaming wide-N kernel: as many waves as can be resident (so the
+// whole grid is one round), each owning an equal share of the column groups.
+template <int OUT, bool HAS_BIAS, int KB>
+static hipError_t gv_stream_kb(hipStream_t s, const GemvArgs& a) {
+    // Resident waves (the whole grid is one round).
+    static const int slots = [] {
+        int dev = 0, cus = 0, per_cu = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+            cus = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_i8_stream_kernel<OUT, HAS_BIAS, KB>, 256, 0) !=
+                hipSuccess || per_cu < 1)
+            per_cu = 1;
+        return cus * per_cu * 4;
+    }();
+    const int ngroups = (a.n + 15) / 16;
+    const int gpw = (ngroups + slots - 1) / slots;  // groups per wave
+    const int waves = (ngroups + gpw - 1) / gpw;    // balanced: every wave gpw or gpw-1 groups
+    gemv_i8_stream_kernel<OUT, HAS_BIAS, KB><<<(waves + 3) / 4, 256, 0, s>>>(a, gpw);
+    return hipGetLastError();
+}
+
+// The streaming wide-N kernel, instantiated for K = 1024 bytes (the LM head
+// of the 1024-wide decoder), m <= 16.
+template <int OUT, bool HAS_BIAS>
+static hipError_t gv_stream(hipStream_t s, const GemvArgs& a) {
+    return gv_stream_kb<OUT, HAS_BIAS, 1024>(s, a);
+}
+
 // Launch policy (measured on MI355X with rotating >256 MB weight pools):
 //  - wide N (>= 1024 column groups, e.g. the LM head): each wave covers two
 //    column groups (four above 8 rows), cutting activation (L2) traffic per
@@ -487,6 +693,7 @@ static hipError_t gv_split(hipStream_t s, const GemvArgs& a) {
         case 4: return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 1, 4>(s, a);
         default: break;
     }
+    if (ngroups >= 1024 && MT == 1 && a.kg == 256 && gv_cfg() != 9) return gv_stream<OUT, HAS_BIAS>(s, a);
     // More than 8 rows: four column groups per wave (activation reads a
     // quarter of the weight reads; 4.5% faster on the LM head at m = 16,
     // 15% slower at m = 1).

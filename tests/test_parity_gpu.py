@@ -145,7 +145,9 @@ def test_gemv_decode_sweep_full(gpu, m, k, n):
 
 @pytest.mark.parametrize("m,k,n", [(17, 1024, 300), (32, 512, 257), (2, 8, 3), (6, 24, 13), (5, 36, 33),
                                    (1, 4, 1), (31, 132, 70), (3, 2048 + 64, 100),
-                                   (20, 1032, 16390), (9, 64, 16401), (32, 200, 16384)])
+                                   (20, 1032, 16390), (9, 64, 16401), (32, 200, 16384),
+                                   # the streaming wide-N kernel (K = 1024, >= 1024 column groups)
+                                   (16, 1024, 16390), (3, 1024, 40001), (1, 1024, 16384), (13, 1024, 151936)])
 def test_gemv_edges(gpu, m, k, n):
     run_and_check(gpu, m, k, n, "gemv", seed=m + k + n, bias=True)
 
