@@ -67,6 +67,7 @@ SIGNATURES = {
     "bh_matmul_i8": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
     "bh_matmul_i8_gemv": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
     "bh_matmul_i8_dyn": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
+    "bh_matmul_i8_dyn_noalloc": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
     "bh_reserve_workspace": (i32, [vp, u32, u32, u32]),
     "bh_matmul_i8_static": (i32, [vp, vp, vp, f32, f32, vp, u32, u32, u32]),
     "bh_linear_i8": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),

@@ -37,6 +37,10 @@ hipError_t launch_gemm_i8_static(hipStream_t s, const uint32_t* xq, const uint32
                                  float* out, int m, int kg, int n);
 
 size_t gemm_workspace_ints(int m, int kg, int n);
+hipError_t launch_gemm_i8_noalloc(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
+                                  const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n,
+                                  size_t* need_bytes);
+size_t noalloc_scratch_bytes();
 size_t gemm_q4_workspace_ints(int m, int k, int n);
 hipError_t launch_gemv_i8_gated(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                                 const float* sw, const float* gate, int gate_stride, int gate_col, float* out, int m,
@@ -274,6 +278,26 @@ int bh_matmul_i8_dyn(void* stream, const uint32_t* xq, const uint32_t* wq, const
                     "the stream is capturing; call bh_reserve_workspace on this stream first",
                     m, kg, n);
     return hip_status(e, "gemm_i8 launch");
+}
+
+int bh_matmul_i8_dyn_noalloc(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx,
+                             const float* sw, const float* bias, void* out, int out_dtype, uint32_t m, uint32_t kg,
+                             uint32_t n) {
+    int rc = check_matmul(xq, wq, sx, sw, out, out_dtype, m, kg, n, "bh_matmul_i8_dyn_noalloc");
+    if (rc) return rc;
+    if (m == 0 || n == 0) return BH_OK;
+    const uint64_t tiles = (((uint64_t)m + 127) / 128) * (((uint64_t)n + 127) / 128);
+    if (tiles > I32MAX)
+        return fail(BH_ERR_INVALID, "bh_matmul_i8_dyn_noalloc: %llu tiles", (unsigned long long)tiles);
+    size_t need = 0;
+    hipError_t e = launch_gemm_i8_noalloc((hipStream_t)stream, xq, wq, sx, sw, bias, out, out_dtype, (int)m, (int)kg,
+                                          (int)n, &need);
+    if (e == hipErrorInvalidValue && need > noalloc_scratch_bytes())
+        return fail(BH_ERR_INVALID,
+                    "bh_matmul_i8_dyn_noalloc: m=%u kg=%u n=%u needs %zu bytes of split-K scratch, more than the "
+                    "fixed %zu; use bh_matmul_i8_dyn",
+                    m, kg, n, need, noalloc_scratch_bytes());
+    return hip_status(e, "gemm_i8 launch (no allocation)");
 }
 
 int bh_reserve_workspace(void* stream, uint32_t m, uint32_t kg, uint32_t n) {

@@ -25,6 +25,8 @@
 #include <algorithm>
 #include <cstdlib>
 
+#include <mutex>
+
 #include "bh_common.h"
 
 namespace bh {
@@ -1038,11 +1040,14 @@ hipError_t gemm_reserve(hipStream_t s, int m, int kg, int n) {
 
 // Launches the chosen configuration: one kernel, or for S > 1 the split
 // kernel (raw i32 partials) and the reduction that applies the epilogue.
+// ws_fixed: caller-provided slab memory of at least splits*m*n i32 (the
+// no-allocation entry point); null takes the stream's library workspace.
 template <int OUT, bool HAS_BIAS, bool STATIC>
-static hipError_t run_gemm(hipStream_t s, bool al, bool dma, const TileChoice& tc, GemmArgs a) {
+static hipError_t run_gemm(hipStream_t s, bool al, bool dma, const TileChoice& tc, GemmArgs a,
+                           int* ws_fixed = nullptr) {
     if (tc.splits <= 1) return go_cfg<OUT, HAS_BIAS, STATIC>(s, al, dma, tc, a);
     hipError_t err = hipSuccess;
-    a.ws = splitk_workspace(s, (size_t)tc.splits * a.m * a.n, &err);
+    a.ws = ws_fixed ? ws_fixed : splitk_workspace(s, (size_t)tc.splits * a.m * a.n, &err);
     if (!a.ws) return err == hipSuccess ? hipErrorOutOfMemory : err;
     a.splits = tc.splits;
     if (dma && tc.cfg == TILE_256)
@@ -1075,6 +1080,64 @@ hipError_t launch_gemm_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
     }
     if (bias) return run_gemm<OUT_BF16, true, false>(s, al, dma, tc, a);
     return run_gemm<OUT_BF16, false, false>(s, al, dma, tc, a);
+}
+
+// ---------------------------------------------------------------- no allocation
+// The split-K slabs of bh_matmul_i8_dyn_noalloc live in this fixed device
+// array (one copy per GPU, held until the process ends) instead of the
+// library's grown-on-demand per-stream workspace, so that call never
+// allocates. In host code `scratch` only names the symbol: its device address
+// comes from hipGetSymbolAddress, looked up once per device with that device
+// current, and only that address is ever passed to a kernel.
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(32) << 20;
+static __device__ __align__(256) int scratch[NOALLOC_SCRATCH_BYTES / 4];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static int* g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+// Device address of this device's `scratch` (current device), or null.
+static int* scratch_ptr(hipError_t* err) {
+    int dev = 0;
+    if ((*err = hipGetDevice(&dev)) != hipSuccess) return nullptr;
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) {
+        *err = hipErrorInvalidDevice;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if ((*err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return nullptr;
+        g_scratch_ptr[dev] = static_cast<int*>(p);
+    }
+    return g_scratch_ptr[dev];
+}
+
+size_t noalloc_scratch_bytes() { return NOALLOC_SCRATCH_BYTES; }
+
+// bh_matmul_i8_dyn without allocation: the same kernels and launch choice;
+// the split-K slabs go to the fixed scratch. *need_bytes reports the slab
+// bytes the shape needs (0 when it does not split K); hipErrorInvalidValue
+// when that exceeds the scratch.
+hipError_t launch_gemm_i8_noalloc(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
+                                  const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n,
+                                  size_t* need_bytes) {
+    GemmArgs a{xq, wq, sx, sw, bias, out, m, kg, n, 0.f, 0.f, 1, nullptr};
+    const bool al = gemm_aligned(xq, wq, kg);
+    const bool dma = al && ((kg * 4) % 128 == 0);
+    const TileChoice tc = choose_tiles(m, kg, n);
+    *need_bytes = tc.splits > 1 ? (size_t)tc.splits * m * n * 4 : 0;
+    if (*need_bytes > NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;
+    hipError_t err = hipSuccess;
+    int* ws = scratch_ptr(&err);  // the first call on a device looks the address up
+    if (!ws) return err;
+    if (out_dtype == OUT_I32) return run_gemm<OUT_I32, false, false>(s, al, dma, tc, a, ws);
+    if (out_dtype == OUT_F32) {
+        if (bias) return run_gemm<OUT_F32, true, false>(s, al, dma, tc, a, ws);
+        return run_gemm<OUT_F32, false, false>(s, al, dma, tc, a, ws);
+    }
+    if (bias) return run_gemm<OUT_BF16, true, false>(s, al, dma, tc, a, ws);
+    return run_gemm<OUT_BF16, false, false>(s, al, dma, tc, a, ws);
 }
 
 hipError_t launch_gemm_i8_static(hipStream_t s, const uint32_t* xq, const uint32_t* wq, float ssx, float ssw,

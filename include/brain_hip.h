@@ -101,6 +101,21 @@ int bh_matmul_i8_gemv(void* stream, const uint32_t* xq, const uint32_t* wq, cons
 int bh_matmul_i8_dyn(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
                      const float* bias, void* out, int out_dtype, uint32_t m, uint32_t kg, uint32_t n);
 
+/* bh_matmul_i8_dyn that allocates nothing. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * kernels, launch choice and results as bh_matmul_i8_dyn; when the shape
+ * splits K, the i32 partial slabs go to a fixed 32 MiB device array that the
+ * library holds on each GPU until the process ends (instead of the per-stream
+ * workspace bh_matmul_i8_dyn grows). A shape whose slabs exceed 32 MiB
+ * returns BH_ERR_INVALID. Every call on one GPU shares that array: calls
+ * that overlap on one GPU (two streams) race and must be serialized by the
+ * caller. The slabs are fully overwritten before they are read, so nothing
+ * needs clearing between calls. */
+int bh_matmul_i8_dyn_noalloc(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx,
+                             const float* sw, const float* bias, void* out, int out_dtype, uint32_t m, uint32_t kg,
+                             uint32_t n);
+
 /* Pre-size the library-held split-K workspace of `stream` for a
  * bh_matmul_i8_dyn call of this shape (a no-op for shapes that do not split
  * K). The workspace is allocated per (device, stream) on first need and
