@@ -320,17 +320,30 @@ int bh_reserve_workspace(void* stream, uint32_t m, uint32_t kg, uint32_t n) {
     return BH_OK;
 }
 
+// select::candidates, I8 arm (crates/backend-api/src/select.rs:197, 209,
+// 323-331): above DECODE_REGIME_MAX_ROWS rows, or without workgroup
+// reductions, the tile alone; up to I8_GEMV_MAX_ROWS the GEMV first; in
+// between the tile first. This is the reference's order, unchanged; what
+// runs on MI355X is bh_matmul_i8's launch policy below.
+static const uint32_t DECODE_REGIME_MAX_ROWS = 32;
+static const uint32_t I8_GEMV_MAX_ROWS = 8;
+
 int bh_select_i8(uint32_t m, uint32_t n, uint32_t k, int int8_dot, int workgroup_reductions, int out[2]) {
     (void)n;
     (void)k;
     if (!out) return fail(BH_ERR_INVALID, "bh_select_i8: null out");
     if (!int8_dot) return 0;
-    if (m > (uint32_t)GEMV_MAX_ROWS || !workgroup_reductions) {
+    if (m > DECODE_REGIME_MAX_ROWS || !workgroup_reductions) {
         out[0] = BH_VARIANT_PACKED_INT8;
         return 1;
     }
-    out[0] = BH_VARIANT_WORKGROUP_PER_OUTPUT;
-    out[1] = BH_VARIANT_PACKED_INT8;
+    if (m <= I8_GEMV_MAX_ROWS) {
+        out[0] = BH_VARIANT_WORKGROUP_PER_OUTPUT;
+        out[1] = BH_VARIANT_PACKED_INT8;
+    } else {
+        out[0] = BH_VARIANT_PACKED_INT8;
+        out[1] = BH_VARIANT_WORKGROUP_PER_OUTPUT;
+    }
     return 2;
 }
 
@@ -344,10 +357,15 @@ const char* bh_variant_kernel(int variant) {
 
 int bh_matmul_i8(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
                  const float* bias, void* out, int out_dtype, uint32_t m, uint32_t kg, uint32_t n) {
-    int v[2];
-    bh_select_i8(m, n, kg * 4, 1, 1, v);
-    if (const int t = tuned_variant(m, n, kg * 4)) v[0] = t;
-    if (v[0] == BH_VARIANT_WORKGROUP_PER_OUTPUT)
+    // Launch policy: a measured choice for this shape (bh_tune_i8 /
+    // bh_tune_set) wins; otherwise the MI355X crossover, which is not the
+    // P40 one the reference's candidate order encodes (I8_GEMV_MAX_ROWS = 8):
+    // the MFMA GEMV streams the weights once for up to 32 rows and beat the
+    // tile at every measured m <= 32 of the configs[1] shapes, so every row
+    // count in the decode regime takes the GEMV.
+    int v = tuned_variant(m, n, kg * 4);
+    if (!v) v = m <= DECODE_REGIME_MAX_ROWS ? BH_VARIANT_WORKGROUP_PER_OUTPUT : BH_VARIANT_PACKED_INT8;
+    if (v == BH_VARIANT_WORKGROUP_PER_OUTPUT)
         return bh_matmul_i8_gemv(stream, xq, wq, sx, sw, bias, out, out_dtype, m, kg, n);
     return bh_matmul_i8_dyn(stream, xq, wq, sx, sw, bias, out, out_dtype, m, kg, n);
 }

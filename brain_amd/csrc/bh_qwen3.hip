@@ -1502,6 +1502,19 @@ int bh_qwen3_set_weight_i8(bh_qwen3* e, const char* name, const uint32_t* packed
     return sync(e);
 }
 
+// dequantize_weight (crates/model/src/int8.rs:70-87) on the device:
+// w[r, 4g+b] = f32(int8 byte b of packed[r, g]) * sw[r].
+__global__ void dequantize_rows_kernel(const uint32_t* packed, const float* sw, uint64_t n, uint64_t kg, float* w) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n * kg; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t r = i / kg;
+        const uint32_t word = packed[i];
+        const float s = sw[r];
+        const float4 v = make_float4((float)(int8_t)(uint8_t)word * s, (float)(int8_t)(uint8_t)(word >> 8) * s,
+                                     (float)(int8_t)(uint8_t)(word >> 16) * s, (float)(int8_t)(uint8_t)(word >> 24) * s);
+        reinterpret_cast<float4*>(w)[i] = v;
+    }
+}
+
 static int upload_chunked(bh_qwen3* e, void* dst, const uint8_t* src, size_t bytes) {
     constexpr size_t CH = 64u << 20;
     for (size_t off = 0; off < bytes; off += CH) {
@@ -1526,6 +1539,30 @@ int bh_qwen3_load(bh_qwen3* e, const char* path) {
         if (!st) return fail(BH_ERR_INVALID, "bh_qwen3_load: %s has no tensor '%s'", path, name.c_str());
         uint64_t elems = 1;
         for (uint64_t d : st->shape) elems *= d;
+        if (t.is_emb && st->dtype == bh::ST_U32) {
+            // A quantized embedding, as the reference's importer writes it
+            // (should_quantize takes every rank-2 tensor with k % 4 == 0,
+            // crates/qwen3omnimoe/src/import.rs:349-351, 622-623): the gather
+            // table is its dequantization (crates/model/src/int8.rs:70-87) and
+            // a tied head takes the packed words and scales as they are.
+            const uint64_t d = e->c.d_model, vocab = e->c.vocab;
+            const bh::StTensor* sc = f.find(name + ".scale");
+            if (st->shape.size() != 2 || st->shape[0] != vocab || st->shape[1] * 4 != d)
+                return fail(BH_ERR_INVALID, "bh_qwen3_load: packed '%s' must be U32 [%llu, %llu]", name.c_str(),
+                            (unsigned long long)vocab, (unsigned long long)(d / 4));
+            if (!sc || sc->dtype != bh::ST_F32 || sc->shape.size() != 1 || sc->shape[0] != vocab)
+                return fail(BH_ERR_INVALID, "bh_qwen3_load: '%s.scale' must be F32 [%llu]", name.c_str(),
+                            (unsigned long long)vocab);
+            // Tied: straight into the head's buffers. Untied: staged in tmpw
+            // (vocab*d floats hold the vocab*d code bytes and the vocab scales).
+            uint32_t* pk = e->c.tie_embeddings ? e->head : reinterpret_cast<uint32_t*>(e->tmpw);
+            float* sv = e->c.tie_embeddings ? e->shead : e->tmpw + vocab * d / 4;
+            BH_TRY(upload_chunked(e, pk, f.bytes(*st), vocab * d));
+            BH_TRY(upload_chunked(e, sv, f.bytes(*sc), vocab * 4));
+            dequantize_rows_kernel<<<grid_for(vocab * d / 4), 256, 0, e->stream>>>(pk, sv, vocab, d / 4, e->emb);
+            BH_HIP(hipGetLastError(), "dequantize launch");
+            continue;
+        }
         if (t.f32) {
             if (st->dtype != bh::ST_F32 || elems != t.n)
                 return fail(BH_ERR_INVALID, "bh_qwen3_load: '%s' must be F32 with %llu elements", name.c_str(),

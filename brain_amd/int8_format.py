@@ -6,9 +6,11 @@ F32. This is the reference's importer plan (crates/qwen3omnimoe/src/import.rs:
 349-351 `should_quantize`: rank 2 and k % 4 == 0, with 420-425 writing the
 pair) and its loader contract (crates/model/src/int8.rs:112-187).
 Quantization is the library's host quantizer, bh_quantize_weight, which is
-bit-identical to crates/model/src/int8.rs:33-59. The embedding is never
-quantized, because it is gathered in f32; the tied head is quantized from it
-at load.
+bit-identical to crates/model/src/int8.rs:33-59. As in the reference, the
+embedding is quantized too (its importer test expects embed_tokens as U32
+plus .scale, import.rs:622-623); the engine gathers from its dequantization
+(crates/model/src/int8.rs:70-87) and a tied head uses the packed words as
+they are. `never` names tensors to keep F32 anyway.
 
 The engine reads these files natively (bh_qwen3_load, memory-mapped, chunked
 upload); this module writes them and inspects them.
@@ -19,7 +21,7 @@ import numpy as np
 
 from ._lib import check, load
 
-NEVER_QUANTIZE = ("tok.weight",)
+NEVER_QUANTIZE = ()
 
 DTYPES = {1: "F32", 2: "U32", 3: "I8", 4: "U8", 5: "F16", 6: "BF16", 7: "I32", 0: "other"}
 

@@ -107,7 +107,10 @@ def matmul_i8_static(xq, wq, sx, sw, out=None):
     m, kg = xq.shape
     n = wq.shape[0]
     _dev(xq, wq, out)
+    _need(xq, torch.int32, m * kg, "xq")
+    _need(wq, torch.int32, n * kg, "wq")
     out = torch.empty(m, n, device=xq.device, dtype=torch.float32) if out is None else out
+    _need(out, torch.float32, m * n, "out")
     check(load().bh_matmul_i8_static(_stream(), _ptr(xq), _ptr(wq), float(sx), float(sw), _ptr(out), m, kg, n))
     return out
 
@@ -116,11 +119,23 @@ def linear_i8(x, wq, sw, bias=None, out_dtype=torch.float32, sx=None, xq=None, o
     """Quantize x per token, then the W8A8 matmul (Ops::act + Ops::matmul)."""
     m, k = x.shape
     n = wq.shape[0]
-    _dev(x, wq, sw, bias)
+    if k % 4:
+        raise ValueError(f"linear_i8: k={k} is not a multiple of 4")
+    _dev(x, wq, sw, bias, sx, xq, out)
+    _need(x, torch.float32, m * k, "x")
+    _need(wq, torch.int32, n * (k // 4), "wq")
+    _need(sw, torch.float32, n, "sw")
+    if bias is not None:
+        _need(bias, torch.float32, n, "bias")
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"linear_i8: out_dtype {out_dtype}, expected float32 or bfloat16")
     sx = torch.empty(m, device=x.device, dtype=torch.float32) if sx is None else sx
     xq = torch.empty(m, k // 4, device=x.device, dtype=torch.int32) if xq is None else xq
+    _need(sx, torch.float32, m, "sx")
+    _need(xq, torch.int32, m * (k // 4), "xq")
     code = {torch.float32: BH_OUT_F32, torch.bfloat16: BH_OUT_BF16}[out_dtype]
     out = torch.empty(m, n, device=x.device, dtype=out_dtype) if out is None else out
+    _need(out, out_dtype, m * n, "out")
     check(load().bh_linear_i8(_stream(), _ptr(x), _ptr(wq), _ptr(sw), _ptr(bias), _ptr(sx), _ptr(xq),
                               _ptr(out), code, m, k, n))
     return out
@@ -166,6 +181,10 @@ def matmul_q4(xq, wq4, sx, sw, bias=None, out_dtype=torch.float32, variant="auto
     _dev(xq, wq4, sx, sw, bias, out)
     _need(xq, torch.int32, m * kg, "xq")
     _need(wq4, torch.int32, n * kw, "wq4")
+    _need(sx, torch.float32, m, "sx")
+    _need(sw, torch.float32, n, "sw")
+    if bias is not None:
+        _need(bias, torch.float32, n, "bias")
     code = _CODES[out_dtype]
     out = torch.empty(m, n, device=xq.device, dtype=out_dtype) if out is None else out
     _need(out, out_dtype, m * n, "out")
@@ -174,15 +193,19 @@ def matmul_q4(xq, wq4, sx, sw, bias=None, out_dtype=torch.float32, variant="auto
     return out
 
 
-
 def moe_linear_gated_i8(xq, wq, sx, sw, gate, e_idx, out=None):
     """moe_linear_gated_i8.wgsl: f32 out [m, n], rows with gate[row, e_idx] <= 0 are +0."""
     m, kg = xq.shape
     n = wq.shape[0]
     n_experts = gate.shape[1]
     _dev(xq, wq, sx, sw, gate, out)
+    _need(xq, torch.int32, m * kg, "xq")
+    _need(wq, torch.int32, n * kg, "wq")
+    _need(sx, torch.float32, m, "sx")
+    _need(sw, torch.float32, n, "sw")
     _need(gate, torch.float32, m * n_experts, "gate")
     out = torch.empty(m, n, device=xq.device, dtype=torch.float32) if out is None else out
+    _need(out, torch.float32, m * n, "out")
     check(load().bh_moe_linear_gated_i8(_stream(), _ptr(xq), _ptr(wq), _ptr(sx), _ptr(sw), _ptr(gate), n_experts,
                                         e_idx, _ptr(out), m, kg, n))
     return out

@@ -81,8 +81,9 @@ int bh_quantize_rows(void* stream, const float* x, uint32_t m, uint32_t k, float
  * f32(x). */
 int bh_quantize_rows_bf16(void* stream, const uint16_t* x, uint32_t m, uint32_t k, float* sx, uint32_t* xq);
 
-/* W8A8 matmul, variant chosen by bh_select_i8 (GEMV for m <= 32, MFMA tile
- * otherwise). Replaces the `matmul_i8_dyn` / `matmul_i8_gemv` dispatches,
+/* W8A8 matmul: a tuned variant if bh_tune_i8 / bh_tune_set recorded one for
+ * the shape, else the GEMV for m <= 32 (the MI355X crossover), the MFMA tile
+ * otherwise. Replaces the `matmul_i8_dyn` / `matmul_i8_gemv` dispatches,
  * bindings [xq, wq, sx, sw, out], params [m, kg, n]
  * (crates/kernels/wgsl/matmul_i8_dyn.wgsl:50-280, matmul_i8_gemv.wgsl:39-76)
  * and the selection in crates/model/src/ops.rs:667-730.
@@ -308,8 +309,11 @@ int bh_quant_rows_steps(bh_backend* be, const uint32_t kernels[2], bh_buffer* x,
 int bh_mm8_rows_off(bh_backend* be, uint32_t kind, bh_buffer* xq, bh_buffer* wq, bh_buffer* sx, bh_buffer* sw,
                     bh_buffer* o, uint32_t xr0, uint64_t ooff, uint32_t m, uint32_t k, uint32_t n, bh_dispatch** out);
 
-/* `backend_api::select::candidates` I8 arm (crates/backend-api/src/select.rs:323-331),
- * with this backend's crossover. Variant codes: */
+/* `backend_api::select::candidates` I8 arm (crates/backend-api/src/select.rs:197,209,323-331),
+ * in the reference's order: m > 32 or no workgroup reductions -> tile only; m <= 8 -> GEMV
+ * then tile; 8 < m <= 32 -> tile then GEMV. (bh_matmul_i8 does not follow this order: it
+ * runs a tuned choice if one was measured, else the GEMV for every m <= 32, the MI355X
+ * crossover.) Variant codes: */
 enum { BH_VARIANT_PACKED_INT8 = 1, BH_VARIANT_WORKGROUP_PER_OUTPUT = 2 };
 /* Fills out[0..ret) with candidate variants, best first; returns the count. */
 int bh_select_i8(uint32_t m, uint32_t n, uint32_t k, int int8_dot, int workgroup_reductions, int out[2]);
@@ -354,8 +358,12 @@ int bh_st_describe(const char* path, const char* name, int* dtype, uint64_t* sha
  *    SwiGLU -> int8 down -> residual; then RMSNorm, the int8 head and a
  *    greedy argmax on the device. Activations f32; every linear quantizes its
  *    input per token (max_abs_row + quant_pack semantics) and runs
- *    bh_matmul_i8 with f32 output. The KV cache is f32, one contiguous
- *    [max_seq, kv_dim] slab per (layer, sequence).
+ *    bh_matmul_i8 with f32 output. The KV cache is one contiguous
+ *    [max_seq, kv_dim] slab per (layer, sequence) in one of two modes:
+ *    f32 (kv_int8 = 0), or int8 codes (kv_int8 = 1) with one f32 scale per
+ *    (token, kv head), min(max|x|, clip)/127 (1 when that is 0), where the
+ *    clip ceilings are per (layer, kv head) and default to FLT_MAX (no
+ *    clipping; see bh_qwen3_set_kv_clip).
  * ====================================================================== */
 typedef struct bh_qwen3 bh_qwen3;
 

@@ -47,9 +47,14 @@ def test_selector_i8_arm():
     out = (C.c_int * 2)()
     # no int8_dot -> no int8 candidate (the model falls back to fp32)
     assert lib.bh_select_i8(1, 1024, 1024, 0, 1, out) == 0
-    # decode: GEMV first, tile second
-    assert lib.bh_select_i8(16, 3072, 1024, 1, 1, out) == 2
-    assert list(out) == [_lib.BH_VARIANT_WORKGROUP_PER_OUTPUT, _lib.BH_VARIANT_PACKED_INT8]
+    # the reference's order (select.rs:323-331): GEMV first up to I8_GEMV_MAX_ROWS = 8 ...
+    for m in (1, 4, 8):
+        assert lib.bh_select_i8(m, 3072, 1024, 1, 1, out) == 2
+        assert list(out) == [_lib.BH_VARIANT_WORKGROUP_PER_OUTPUT, _lib.BH_VARIANT_PACKED_INT8]
+    # ... the tile first above it, through DECODE_REGIME_MAX_ROWS = 32
+    for m in (9, 16, 32):
+        assert lib.bh_select_i8(m, 3072, 1024, 1, 1, out) == 2
+        assert list(out) == [_lib.BH_VARIANT_PACKED_INT8, _lib.BH_VARIANT_WORKGROUP_PER_OUTPUT]
     # no workgroup reductions -> tile only (select.rs:324)
     assert lib.bh_select_i8(4, 3072, 1024, 1, 0, out) == 1 and out[0] == _lib.BH_VARIANT_PACKED_INT8
     # prefill

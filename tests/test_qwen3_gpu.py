@@ -233,6 +233,34 @@ def test_int8_checkpoint_load_matches_f32_upload(gpu, tmp_path):
     b.close()
 
 
+@pytest.mark.parametrize("tied", [1, 0])
+def test_int8_checkpoint_with_quantized_embedding(gpu, tmp_path, tied):
+    """The reference's importer also packs the embedding (import.rs:349-351,
+    622-623). Loading such a file gives the engine whose gather table is the
+    dequantized embedding (int8.rs:70-87) and whose head is the file's packed
+    head: the same model as an untied engine built from those f32 tables."""
+    from brain_amd import int8_format as fmt
+    cfg = dict(SMALL, tie_embeddings=tied)
+    w = scaled_weights(cfg, seed=23)
+    path = str(tmp_path / "qe.safetensors")
+    fmt.write_int8_checkpoint(path, w)
+    assert fmt.describe(path, "tok.weight") == ("U32", (cfg["vocab"], cfg["d_model"] // 4))
+    packed, sw = o.quantize_weight(w["tok.weight"])
+    ref_w = dict(w)
+    ref_w["tok.weight"] = o.dequantize_weight(packed, sw, cfg["d_model"])
+    if tied:
+        ref_w["lm_head.weight"] = w["tok.weight"]  # the packed head is quantize(tok) either way
+    ref_cfg = dict(cfg, tie_embeddings=0)
+    prompts = np.random.default_rng(10).integers(0, cfg["vocab"], size=(2, 5))
+    a = engine_for(ref_cfg, ref_w, 2, 16)
+    b = Qwen3Engine(cfg, 2, 16)
+    b.load(path)
+    assert (a.generate(prompts, 4) == b.generate(prompts, 4)).all()
+    assert np.array_equal(a.logits(), b.logits())
+    a.close()
+    b.close()
+
+
 def test_autotune_changes_no_result(gpu):
     """Both candidates are bit-exact, so the measured choice changes speed only."""
     from brain_amd._lib import load as L
