@@ -89,6 +89,27 @@ __device__ __forceinline__ bool gated_off(const GemmArgs& a, int row) {
     return a.gate && a.gate[(int64_t)row * a.gate_stride + a.gate_col] <= 0.0f;
 }
 
+// moe_linear_gated_i8's early exit for unrouted rows
+// (crates/kernels/wgsl/moe_linear_gated_i8.wgsl:66-69), per output tile: when
+// no row of [row0, row0+BM) is routed, the tile stores its +0 outputs and
+// skips the K loop. (A tile with some routed rows multiplies them all; the
+// epilogue zeroes the rest.) Split-K partial tiles never skip: the reduction
+// reads every slab. Block-uniform result; all threads take part.
+template <int BM, int BN, int NT, bool SPLITK>
+__device__ __forceinline__ bool gated_tile_skipped(const GemmArgs& a, int row0, int col0) {
+    if (SPLITK || !a.gate) return false;
+    const int t = threadIdx.x;
+    const bool live = t < BM && row0 + t < a.m && !gated_off(a, row0 + t);
+    if (__syncthreads_or(live)) return false;
+    float* out = reinterpret_cast<float*>(a.out);  // the gated linear's output is f32
+    const int rows = min(BM, a.m - row0), cols = min(BN, a.n - col0);
+    for (int i = t; i < rows * cols; i += NT) {
+        const int r = i / cols, c = i - r * cols;
+        out[(int64_t)(row0 + r) * a.n + col0 + c] = 0.0f;
+    }
+    return true;
+}
+
 // One output element through the epilogue.
 template <int OUT, bool HAS_BIAS, bool STATIC>
 __device__ __forceinline__ void emit(const GemmArgs& a, int row, int col, int acc, float sxm, float swn, float bn) {
@@ -123,6 +144,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_kernel(GemmArgs a) {
     int tm, tn;
     tile_of(tile_id, gridDim.x / S, tiles_m, tiles_n, tm, tn);
     const int row0 = tm * BM, col0 = tn * BN;
+    if (gated_tile_skipped<BM, BN, WM * WN * 64, SPLITK>(a, row0, col0)) return;
     const int kbytes = a.kg * 4;
     const int nk_all = (kbytes + GM_BK - 1) / GM_BK;
     const int kt0 = (int)(((int64_t)nk_all * split) / S);
@@ -355,6 +377,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
     int tm, tn;
     tile_of(tile_id, gridDim.x / S, tiles_m, tiles_n, tm, tn);
     const int row0 = tm * BM, col0 = tn * BN;
+    if (gated_tile_skipped<BM, BN, WM * WN * 64, SPLITK>(a, row0, col0)) return;
     const int kbytes = a.kg * 4;
     const int nk_all = kbytes / DK;
     const int kt0 = (int)(((int64_t)nk_all * split) / S);

@@ -96,6 +96,23 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
     const int xstride = kbytes + 16;
     const int ksub = (lane >> 4) * 16;  // this lane's 16-byte slice of a 64-byte chunk
     const int g0 = (blockIdx.x * SLOTS + slot) * CG;  // first of this wave's CG column groups
+    if constexpr (XMODE == 0) {
+        // moe_linear_gated_i8's early exit (moe_linear_gated_i8.wgsl:66-69)
+        // for the whole launch: with no routed row at all the workgroup
+        // stores its +0 outputs and reads no weights. (Otherwise every row
+        // is multiplied, since the weights are streamed once for all rows,
+        // and the epilogue zeroes the unrouted ones.)
+        if (a.gate) {
+            const bool live = lane < m && !(a.gate[(int64_t)lane * a.gate_stride + a.gate_col] <= 0.0f);
+            if (!__any(live)) {
+                for (int i = threadIdx.x; i < m * SLOTS * CG * 16; i += NW * 64) {
+                    const int r = i / (SLOTS * CG * 16), c = blockIdx.x * SLOTS * CG * 16 + i % (SLOTS * CG * 16);
+                    if (c < n) reinterpret_cast<float*>(a.out)[(int64_t)r * n + c] = 0.0f;
+                }
+                return;
+            }
+        }
+    }
 
     const uint8_t* wp[CG];
 #pragma unroll
@@ -693,7 +710,7 @@ static hipError_t gv_split(hipStream_t s, const GemvArgs& a) {
         case 4: return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 1, 4>(s, a);
         default: break;
     }
-    if (ngroups >= 1024 && MT == 1 && a.kg == 256 && gv_cfg() != 9) return gv_stream<OUT, HAS_BIAS>(s, a);
+    if (ngroups >= 1024 && MT == 1 && a.kg == 256 && !a.gate && gv_cfg() != 9) return gv_stream<OUT, HAS_BIAS>(s, a);
     // More than 8 rows: four column groups per wave (activation reads a
     // quarter of the weight reads; 4.5% faster on the LM head at m = 16,
     // 15% slower at m = 1).

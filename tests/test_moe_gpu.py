@@ -58,3 +58,37 @@ def test_moe_step_through_the_backend(gpu):
     want = o.epilogue(o.acc_exact(xq, wq), sx, sw)
     want[[1, 3]] = 0.0
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,k,n,pattern", [
+    (8, 1024, 768, "none"),          # GEMV: no routed row -> the launch reads no weights
+    (4, 1024, 16390, "some"),        # wide N, K=1024: the gated GEMV keeps the gate
+    (512, 1024, 1536, "blocks"),     # GEMM: whole tiles of unrouted rows skip their K loop
+    (300, 2048, 700, "none"),        # GEMM, nothing routed
+    (200, 4096, 300, "blocks"),      # split-K shape: partial tiles never skip
+])
+def test_moe_unrouted_tiles_skip(gpu, m, k, n, pattern):
+    rng = np.random.default_rng(m * 3 + n)
+    n_experts, e_idx = 4, 2
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    sx = o.max_abs_row(x)
+    xq = o.quant_pack(x, sx)
+    wq, sw = o.quantize_weight(rng.standard_normal((n, k)).astype(np.float32))
+    gate = np.abs(rng.standard_normal((m, n_experts))).astype(np.float32) + 0.1
+    if pattern == "none":
+        gate[:, e_idx] = 0.0
+    elif pattern == "some":
+        gate[1::2, e_idx] = -1.0
+    else:
+        gate[128:384, e_idx] = 0.0
+        gate[7, e_idx] = -0.0
+    out = torch.full((m, n), float("nan"), device=gpu)   # every output must be written
+    got = ops.moe_linear_gated_i8(dev_u32(xq, gpu), dev_u32(wq, gpu), torch.from_numpy(sx).to(gpu),
+                                  torch.from_numpy(sw).to(gpu), torch.from_numpy(gate).to(gpu), e_idx,
+                                  out=out).cpu().numpy()
+    off = gate[:, e_idx] <= 0
+    want = np.zeros((m, n), np.float32)
+    on = np.nonzero(~off)[0]
+    if len(on):
+        want[on] = o.epilogue(o.acc_exact(xq[on], wq), sx[on], sw)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

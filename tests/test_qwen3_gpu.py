@@ -222,7 +222,7 @@ def test_int8_checkpoint_load_matches_f32_upload(gpu, tmp_path):
     cfg = dict(SMALL, tie_embeddings=0)
     w = scaled_weights(cfg, seed=21)
     path = str(tmp_path / "q.safetensors")
-    fmt.write_int8_checkpoint(path, w, keep_f32=("blocks.1.mlp.up.weight",))
+    fmt.write_int8_checkpoint(path, w, never=("tok.weight",), keep_f32=("blocks.1.mlp.up.weight",))
     prompts = np.random.default_rng(8).integers(0, cfg["vocab"], size=(2, 7))
     a = engine_for(cfg, w, 2, 16)
     b = Qwen3Engine(cfg, 2, 16)
