@@ -68,6 +68,9 @@ SIGNATURES = {
     "bh_matmul_i8_gemv": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
     "bh_matmul_i8_dyn": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
     "bh_matmul_i8_dyn_noalloc": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
+    "bh_paged_kv_append_i8": (i32, [vp, vp, vp, vp, vp, vp, u64, vp, u64, u32, u32, u32, u32]),
+    "bh_paged_decode_scores_i8": (i32, [vp, vp, vp, u64, vp, vp, vp, u64, vp] + [u32] * 8 + [f32]),
+    "bh_paged_decode_apply_i8": (i32, [vp, vp, vp, u64, vp, vp, vp, u64, vp] + [u32] * 8),
     "bh_reserve_workspace": (i32, [vp, u32, u32, u32]),
     "bh_matmul_i8_static": (i32, [vp, vp, vp, f32, f32, vp, u32, u32, u32]),
     "bh_linear_i8": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
@@ -83,6 +86,7 @@ SIGNATURES = {
     "bh_qwen3_decode": (i32, [vp, u32, u32, vp]),
     "bh_qwen3_logits": (i32, [vp, vp, u64]),
     "bh_qwen3_lengths": (i32, [vp, vp, u32]),
+    "bh_qwen3_kv_read": (i32, [vp, u32, u32, u32, u32, u32, vp, vp]),
     "bh_qwen3_stream": (vp, [vp]),
     "bh_qwen3_load": (i32, [vp, C.c_char_p]),
     "bh_qwen3_set_kv_clip": (i32, [vp, u32, u32, vp]),

@@ -16,7 +16,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libbrain_hip.so")
-SOURCES = ["bh_api.hip", "bh_quant.hip", "bh_gemv.hip", "bh_gemm.hip", "bh_qwen3.hip", "bh_q4.hip", "bh_st.cpp"]
+SOURCES = ["bh_api.hip", "bh_quant.hip", "bh_gemv.hip", "bh_gemm.hip", "bh_qwen3.hip", "bh_q4.hip", "bh_kv8.hip",
+           "bh_st.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",

@@ -22,6 +22,7 @@
 
 #include "../../include/brain_hip.h"
 #include "bh_common.h"
+#include "bh_kv8.h"
 
 namespace bh {
 hipError_t launch_max_abs_rows(hipStream_t s, const float* x, int m, int k, float* sx);
@@ -452,6 +453,66 @@ int bh_moe_linear_gated_i8(void* stream, const uint32_t* xq, const uint32_t* wq,
     return hip_status(e, "moe_linear_gated_i8 launch");
 }
 
+// ---------------------------------------------------------------- int8 paged KV
+static int check_kv_geom(const char* who, uint32_t kv_stride, uint32_t bs, uint32_t hd) {
+    if (hd == 0 || hd % 4 || hd > 256 || kv_stride == 0 || kv_stride % hd || bs == 0)
+        return fail(BH_ERR_INVALID, "%s: head_dim %u (a multiple of 4, <= 256), kv_stride %u (a multiple of "
+                    "head_dim) and block_size %u (> 0) do not fit", who, hd, kv_stride, bs);
+    return BH_OK;
+}
+
+int bh_paged_kv_append_i8(void* stream, const float* src, const uint32_t* blocks, const uint32_t* offsets,
+                          const float* clip, uint32_t* pool, uint64_t pool_words, float* scales, uint64_t n_scales,
+                          uint32_t batch, uint32_t kv_stride, uint32_t block_size, uint32_t head_dim) {
+    int rc = check_kv_geom("bh_paged_kv_append_i8", kv_stride, block_size, head_dim);
+    if (rc) return rc;
+    if (batch == 0) return BH_OK;
+    if (!src || !blocks || !offsets || !clip || !pool || !scales)
+        return fail(BH_ERR_INVALID, "bh_paged_kv_append_i8: null buffer");
+    if ((uint64_t)batch * (kv_stride / head_dim) > I32MAX)
+        return fail(BH_ERR_INVALID, "bh_paged_kv_append_i8: batch %u x %u heads", batch, kv_stride / head_dim);
+    return hip_status(launch_paged_kv_append_i8((hipStream_t)stream, src, blocks, offsets, clip, pool, pool_words,
+                                                scales, n_scales, batch, kv_stride, block_size, head_dim),
+                      "paged_kv_append_i8 launch");
+}
+
+static int paged_read(void* stream, bool apply, const char* who, const float* in, const uint32_t* pool,
+                      uint64_t pool_words, const uint32_t* bt, const uint32_t* seq_lens, const float* scales,
+                      uint64_t n_scales, float* out, uint32_t batch, uint32_t n_heads, uint32_t group, uint32_t hd,
+                      uint32_t bs, uint32_t kv_stride, uint32_t cap, uint32_t max_bt, float scale) {
+    int rc = check_kv_geom(who, kv_stride, bs, hd);
+    if (rc) return rc;
+    if (group == 0 || (n_heads && (n_heads - 1) / group >= kv_stride / hd))
+        return fail(BH_ERR_INVALID, "%s: %u heads in groups of %u need more than the %u kv heads", who, n_heads,
+                    group, kv_stride / hd);
+    if (batch == 0 || n_heads == 0 || (!apply && cap == 0)) return BH_OK;
+    if (!in || !pool || !bt || !seq_lens || !scales || !out) return fail(BH_ERR_INVALID, "%s: null buffer", who);
+    if ((uint64_t)batch * n_heads * ((apply ? hd : cap) + 63) / 64 > I32MAX)
+        return fail(BH_ERR_INVALID, "%s: grid too large", who);
+    PagedReadArgs a{in, pool, pool_words, bt, seq_lens, scales, n_scales, out, n_heads, group, hd, bs, kv_stride,
+                    cap, max_bt, scale};
+    return hip_status(launch_paged_decode_i8((hipStream_t)stream, apply, a, batch), who);
+}
+
+int bh_paged_decode_scores_i8(void* stream, const float* q, const uint32_t* pool, uint64_t pool_words,
+                              const uint32_t* block_tables, const uint32_t* seq_lens, const float* scales,
+                              uint64_t n_scales, float* scores, uint32_t batch, uint32_t n_heads, uint32_t group,
+                              uint32_t head_dim, uint32_t block_size, uint32_t kv_stride, uint32_t cap,
+                              uint32_t max_bt, float scale) {
+    return paged_read(stream, false, "bh_paged_decode_scores_i8", q, pool, pool_words, block_tables, seq_lens, scales,
+                      n_scales, scores, batch, n_heads, group, head_dim, block_size, kv_stride, cap, max_bt, scale);
+}
+
+int bh_paged_decode_apply_i8(void* stream, const float* probs, const uint32_t* pool, uint64_t pool_words,
+                             const uint32_t* block_tables, const uint32_t* seq_lens, const float* scales,
+                             uint64_t n_scales, float* ctx, uint32_t batch, uint32_t n_heads, uint32_t group,
+                             uint32_t head_dim, uint32_t block_size, uint32_t kv_stride, uint32_t cap,
+                             uint32_t max_bt) {
+    return paged_read(stream, true, "bh_paged_decode_apply_i8", probs, pool, pool_words, block_tables, seq_lens,
+                      scales, n_scales, ctx, batch, n_heads, group, head_dim, block_size, kv_stride, cap, max_bt,
+                      0.0f);
+}
+
 int bh_f32_to_bf16(void* stream, const float* x, uint16_t* out, uint64_t n) {
     if (n == 0) return BH_OK;
     if (!x || !out) return fail(BH_ERR_INVALID, "bh_f32_to_bf16: null buffer");
@@ -725,6 +786,9 @@ enum KernelId : int {
     K_MATMUL_Q4_DYN,
     K_MATMUL_Q4_GEMV,
     K_MOE_LINEAR_GATED_I8,
+    K_PAGED_KV_APPEND_I8,
+    K_PAGED_DECODE_SCORES_I8,
+    K_PAGED_DECODE_APPLY_I8,
 };
 
 struct KernelSpec {
@@ -741,6 +805,12 @@ static const KernelSpec kSpecs[] = {
     {"bias_add", K_BIAS_ADD, 2, 2},            {"roof_dp4a", K_ROOF_DP4A, 2, 4},
     {"matmul_q4_dyn", K_MATMUL_Q4_DYN, 5, 3},   {"matmul_q4_gemv", K_MATMUL_Q4_GEMV, 5, 3},
     {"moe_linear_gated_i8", K_MOE_LINEAR_GATED_I8, 6, 5},
+    // crates/qwen3/src/serve.rs:1267-1270: [src, blocks, offsets, clip, pool, scales] /
+    // [b, kv_stride, block_size, head_dim]; [q|probs, pool, block_tables, seq_lens, scales,
+    // scores|ctx] / [b, n_heads, group, head_dim, block_size, kv_stride, cap, max_bt (, scale)].
+    {"paged_kv_append_i8_clipped_batched", K_PAGED_KV_APPEND_I8, 6, 4},
+    {"paged_decode_scores_i8_batched", K_PAGED_DECODE_SCORES_I8, 6, 9},
+    {"paged_decode_apply_i8_batched", K_PAGED_DECODE_APPLY_I8, 6, 8},
 };
 
 static const KernelSpec* spec_of(const char* name) {
@@ -762,7 +832,8 @@ struct bh_dispatch {
     std::atomic<int> rc{1};
     uint32_t kind = 0;
     std::vector<bh_buffer*> bufs;
-    std::vector<uint64_t> off;  // word offsets
+    std::vector<uint64_t> off;   // word offsets
+    std::vector<uint64_t> span;  // words bound from off (the slice length, or to the end)
     std::vector<uint32_t> params;
 };
 
@@ -842,9 +913,36 @@ static int binding_needs(KernelId id, const std::vector<uint32_t>& p, std::vecto
             need = {a * b, c * b, a, c, a * ne, a * c};
             return BH_OK;
         }
+        case K_PAGED_KV_APPEND_I8: {  // [b, kv_stride, block_size, head_dim]
+            const uint64_t hd = p.size() > 3 ? p[3] : 0;
+            if (hd == 0 || b % hd) return fail(BH_ERR_INVALID, "%s: kv_stride %llu is not a multiple of head_dim %llu",
+                                               name, (unsigned long long)b, (unsigned long long)hd);
+            // the pool and scale slots the tables name are checked on the device
+            need = {a * b, a, a, b / hd, 0, 0};
+            return BH_OK;
+        }
+        case K_PAGED_DECODE_SCORES_I8:
+        case K_PAGED_DECODE_APPLY_I8: {  // [b, n_heads, group, head_dim, block_size, kv_stride, cap, max_bt]
+            const uint64_t hd = p.size() > 3 ? p[3] : 0, cap = p.size() > 6 ? p[6] : 0, mbt = p.size() > 7 ? p[7] : 0;
+            const uint64_t qn = a * b * hd, pn = a * b * cap;
+            need = {id == K_PAGED_DECODE_SCORES_I8 ? qn : pn, 0, a * mbt, a, 0, id == K_PAGED_DECODE_SCORES_I8 ? pn : qn};
+            return BH_OK;
+        }
         case K_BIAS_ADD: need = {a * b, b}; return BH_OK;
         case K_ROOF_DP4A: need = {a, a}; return BH_OK;
         default: return fail(BH_ERR_UNSUPPORTED, "kernel '%s' is not provided by the hip backend", name);
+    }
+}
+
+// Bindings whose extent depends on device-side tables (the paged KV pool and
+// scales): the kernel checks each access against the bound slice, and the
+// alias check takes the whole slice.
+static bool device_checked(KernelId id, uint32_t i) {
+    switch (id) {
+        case K_PAGED_KV_APPEND_I8: return i == 4 || i == 5;
+        case K_PAGED_DECODE_SCORES_I8:
+        case K_PAGED_DECODE_APPLY_I8: return i == 1 || i == 4;
+        default: return false;
     }
 }
 
@@ -859,6 +957,9 @@ static bool is_output(KernelId id, uint32_t i) {
         case K_MATMUL_Q4_DYN:
         case K_MATMUL_Q4_GEMV: return i == 4;
         case K_MOE_LINEAR_GATED_I8: return i == 5;
+        case K_PAGED_KV_APPEND_I8: return i == 4 || i == 5;
+        case K_PAGED_DECODE_SCORES_I8:
+        case K_PAGED_DECODE_APPLY_I8: return i == 5;
         case K_MATMUL_I8: return i == 2;
         case K_BIAS_ADD: return i == 0;
         case K_ROOF_DP4A: return i == 1;
@@ -880,7 +981,7 @@ static int record(bh_backend* be, uint32_t kind, bh_buffer* const* bufs, const u
     std::vector<uint64_t> need;
     int rc = binding_needs(sp->id, pv, need, name);
     if (rc) return rc;
-    std::vector<uint64_t> lo(nbufs), hi(nbufs);
+    std::vector<uint64_t> lo(nbufs), hi(nbufs), spans(nbufs);
     for (uint32_t i = 0; i < nbufs; ++i) {
         if (!bufs[i]) return fail(BH_ERR_INVALID, "%s: binding %u is null", name, i);
         const uint64_t off = offsets ? offsets[2 * i] : 0;
@@ -896,13 +997,14 @@ static int record(bh_backend* be, uint32_t kind, bh_buffer* const* bufs, const u
             return fail(BH_ERR_INVALID, "%s: binding %u needs %llu words, slice has %llu", name, i,
                         (unsigned long long)need[i], (unsigned long long)span);
         lo[i] = off;
-        hi[i] = off + need[i];
+        hi[i] = off + (device_checked(sp->id, i) ? span : need[i]);
+        spans[i] = span;
     }
     // No output may alias another binding's range (crates/gpu-core/src/lib.rs:708).
     for (uint32_t i = 0; i < nbufs; ++i) {
-        if (!is_output(sp->id, i) || need[i] == 0) continue;
+        if (!is_output(sp->id, i) || hi[i] == lo[i]) continue;
         for (uint32_t j = 0; j < nbufs; ++j) {
-            if (j == i || bufs[j] != bufs[i] || need[j] == 0) continue;
+            if (j == i || bufs[j] != bufs[i] || hi[j] == lo[j]) continue;
             if (lo[i] < hi[j] && lo[j] < hi[i])
                 return fail(BH_ERR_INVALID, "%s: output binding %u overlaps binding %u", name, i, j);
         }
@@ -914,6 +1016,7 @@ static int record(bh_backend* be, uint32_t kind, bh_buffer* const* bufs, const u
         bh_buffer_retain(bufs[i]);
         s->bufs.push_back(bufs[i]);
         s->off.push_back(lo[i]);
+        s->span.push_back(spans[i]);
     }
     be->uniform_allocs++;
     be->bind_groups++;
@@ -963,6 +1066,23 @@ static int launch_step(bh_backend* be, const bh_dispatch* s) {
             return bh_matmul_i8_static(st, (const uint32_t*)wptr(s, 0), (const uint32_t*)wptr(s, 1), sx, sw,
                                        (float*)wptr(s, 2), p[0], p[1], p[2]);
         }
+        case K_PAGED_KV_APPEND_I8:
+            return bh_paged_kv_append_i8(st, (const float*)wptr(s, 0), (const uint32_t*)wptr(s, 1),
+                                         (const uint32_t*)wptr(s, 2), (const float*)wptr(s, 3), (uint32_t*)wptr(s, 4),
+                                         s->span[4], (float*)wptr(s, 5), s->span[5], p[0], p[1], p[2], p[3]);
+        case K_PAGED_DECODE_SCORES_I8: {
+            float sc;
+            memcpy(&sc, &p[8], 4);
+            return bh_paged_decode_scores_i8(st, (const float*)wptr(s, 0), (const uint32_t*)wptr(s, 1), s->span[1],
+                                             (const uint32_t*)wptr(s, 2), (const uint32_t*)wptr(s, 3),
+                                             (const float*)wptr(s, 4), s->span[4], (float*)wptr(s, 5), p[0], p[1],
+                                             p[2], p[3], p[4], p[5], p[6], p[7], sc);
+        }
+        case K_PAGED_DECODE_APPLY_I8:
+            return bh_paged_decode_apply_i8(st, (const float*)wptr(s, 0), (const uint32_t*)wptr(s, 1), s->span[1],
+                                            (const uint32_t*)wptr(s, 2), (const uint32_t*)wptr(s, 3),
+                                            (const float*)wptr(s, 4), s->span[4], (float*)wptr(s, 5), p[0], p[1], p[2],
+                                            p[3], p[4], p[5], p[6], p[7]);
         case K_BIAS_ADD: {
             const uint64_t total = (uint64_t)p[0] * p[1];
             if (total == 0) return BH_OK;

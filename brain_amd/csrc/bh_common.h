@@ -42,6 +42,16 @@ __device__ __forceinline__ uint32_t quant_word(float4 v, float inv) {
            (quant_byte(v.w, inv) << 24);
 }
 
+// One int8 KV-cache code (paged_kv_append_i8_clipped_batched.wgsl:72):
+// clamp(i32(round_ties_even(v / scale)), -127, 127), a true division; i32()
+// saturates and maps NaN to 0 as the reference's CPU lowering does
+// (crates/wgsl-cpu/src/lib.rs:1554, fcvt_to_sint_sat).
+__device__ __forceinline__ uint8_t kv8_code(float v, float scale) {
+    const float r = rintf(v / scale);
+    const float q = r != r ? 0.0f : fminf(fmaxf(r, -127.0f), 127.0f);
+    return (uint8_t)(int8_t)(int)q;
+}
+
 // W4A8: one u32 of 8 int4 nibbles (nibble b = K index 8g+b, two's complement,
 // crates/model/src/int4.rs:46-67) -> 8 sign-extended int8 in K order, bytes
 // 0..3 in lo and 4..7 in hi. The even and odd nibbles are masked into bytes;

@@ -245,10 +245,6 @@ __global__ __launch_bounds__(256) void rope_table_kernel(float2* cs, int max_seq
 
 // One int8 KV code: clamp(round_even(v / scale), -127, 127)
 // (paged_kv_append_i8_clipped_batched.wgsl).
-__device__ __forceinline__ uint8_t kv8_code(float v, float scale) {
-    const float q = fminf(fmaxf(rintf(v / scale), -127.0f), 127.0f);
-    return (uint8_t)(int8_t)(int)q;
-}
 
 // One head of the q|k|v row through the per-head RMSNorm and the
 // rotate-half RoPE of rope_paged.wgsl:27-38 (pair (m, m+hd/2), angle
@@ -1747,6 +1743,26 @@ int bh_qwen3_logits(bh_qwen3* e, float* out, uint64_t n) {
     if (!e->batch || n < want) return fail(BH_ERR_INVALID, "bh_qwen3_logits: need %llu floats", (unsigned long long)want);
     (void)hipSetDevice(e->device);
     BH_HIP(hipMemcpyAsync(out, e->logits, want * 4, hipMemcpyDeviceToHost, e->stream), "download");
+    return sync(e);
+}
+
+int bh_qwen3_kv_read(bh_qwen3* e, uint32_t layer, uint32_t seq, uint32_t which, uint32_t pos0, uint32_t npos,
+                     void* data, float* scales) {
+    if (!e || !data || which > 1 || layer >= e->c.n_layers || seq >= e->max_batch ||
+        (uint64_t)pos0 + npos > e->max_seq)
+        return fail(BH_ERR_INVALID, "bh_qwen3_kv_read: bad argument");
+    (void)hipSetDevice(e->device);
+    const size_t tok0 = (size_t)seq * e->max_seq + pos0;
+    const uint8_t* cache = static_cast<const uint8_t*>(which ? e->vc : e->kc) + (size_t)layer * e->layer_kv * e->kv_elem;
+    BH_HIP(hipMemcpyAsync(data, cache + tok0 * e->hkv * e->kv_elem, (size_t)npos * e->hkv * e->kv_elem,
+                          hipMemcpyDeviceToHost, e->stream),
+           "kv read");
+    if (e->c.kv_int8 && scales) {
+        const size_t nkv = e->c.n_kv_heads;
+        const float* sc = (which ? e->vscale : e->kscale) + (size_t)layer * e->max_batch * e->max_seq * nkv;
+        BH_HIP(hipMemcpyAsync(scales, sc + tok0 * nkv, (size_t)npos * nkv * 4, hipMemcpyDeviceToHost, e->stream),
+               "kv scale read");
+    }
     return sync(e);
 }
 

@@ -97,6 +97,18 @@ class Qwen3Engine:
         check(load().bh_qwen3_decode(self._h, steps, flags, out.ctypes.data))
         return out
 
+    def kv(self, layer, seq, which, npos, pos0=0):
+        """The engine's cache for (layer, seq): K (which=0) or V (1) over
+        positions pos0..pos0+npos. f32 [npos, kv_dim], or with kv_int8
+        (int8 codes [npos, kv_dim], scales [npos, n_kv_heads])."""
+        kvd = self.cfg["n_kv_heads"] * self.cfg["head_dim"]
+        int8 = bool(self.cfg.get("kv_int8", 0))
+        data = np.zeros((npos, kvd), np.int8 if int8 else np.float32)
+        sc = np.zeros((npos, self.cfg["n_kv_heads"]), np.float32)
+        check(load().bh_qwen3_kv_read(self._h, layer, seq, which, pos0, npos, data.ctypes.data,
+                                      sc.ctypes.data if int8 else None))
+        return (data, sc) if int8 else data
+
     def logits(self):
         out = np.zeros((self.batch, self.cfg["vocab"]), np.float32)
         check(load().bh_qwen3_logits(self._h, out.ctypes.data, out.size))

@@ -158,13 +158,51 @@ int bh_matmul_q4(void* stream, const uint32_t* xq, const uint32_t* wq4, const fl
 
 /* Sparse-MoE expert linear, int8 (crates/kernels/wgsl/moe_linear_gated_i8.wgsl):
  * out [m,n] f32 = (f32(xq.wq^T) * sx) * sw for rows routed to expert e_idx,
- * +0 for rows with gate[row * n_experts + e_idx] <= 0. The GEMV (m <= 32) or
- * MFMA GEMM computes every row and the epilogue zeroes the unrouted ones.
+ * +0 for rows with gate[row * n_experts + e_idx] <= 0 (moe_linear_gated_i8.wgsl:66-69).
+ * The GEMV (m <= 32) or MFMA GEMM skips the weights of a launch (GEMV) or
+ * output tile (GEMM) with no routed row, multiplies the rest and zeroes the
+ * unrouted rows in the epilogue.
  * Step name "moe_linear_gated_i8": bindings [xq, wq, sx, sw, gate, out],
  * params [m, kg, n, n_experts, e_idx]. */
 int bh_moe_linear_gated_i8(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
                            const float* gate, uint32_t n_experts, uint32_t e_idx, float* out, uint32_t m, uint32_t kg,
                            uint32_t n);
+
+/* The int8 paged KV cache (brain's int8 serving attention, crates/qwen3/src/serve.rs:1262-1270).
+ * pool: int8 codes, 4 per u32 word, kv_stride bytes per slot, slot = physical_block *
+ * block_size + offset; scales: one f32 per (slot, kv head). pool_words / n_scales are
+ * the lengths of those buffers: the slots the device-side tables name are checked
+ * against them, and one outside is skipped (nothing stored or added) where the
+ * reference would access out of bounds. head_dim % 4 == 0, head_dim <= 256,
+ * kv_stride % head_dim == 0. Each f32 result keeps the reference's summation order.
+ *
+ * paged_kv_append_i8_clipped_batched (crates/kernels/wgsl/paged_kv_append_i8_clipped_batched.wgsl:46-77):
+ * for each sequence b and kv head h of src [batch][kv_stride], scale = min(max|x|,
+ * clip[h]) / 127 (1 when that is 0) into scales[slot*n_kv + h], codes clamp(round_even(x /
+ * scale), +-127) into the pool, at slot blocks[b]*block_size + offsets[b]. Step bindings
+ * [src, blocks, offsets, clip, pool, scales], params [batch, kv_stride, block_size, head_dim]. */
+int bh_paged_kv_append_i8(void* stream, const float* src, const uint32_t* blocks, const uint32_t* offsets,
+                          const float* clip, uint32_t* pool, uint64_t pool_words, float* scales, uint64_t n_scales,
+                          uint32_t batch, uint32_t kv_stride, uint32_t block_size, uint32_t head_dim);
+/* paged_decode_scores_i8_batched (crates/kernels/wgsl/paged_decode_scores_i8_batched.wgsl:28-54):
+ * scores[b][h][j] = ((sum_d q[b][h][d] * code) * kscale) * scale for j < seq_lens[b]
+ * (entries past it untouched), kv head h / group, position j at block_tables[b*max_bt +
+ * j/block_size]. Step bindings [q, pool, block_tables, seq_lens, scales, scores], params
+ * [batch, n_heads, group, head_dim, block_size, kv_stride, cap, max_bt, scale_bits]. */
+int bh_paged_decode_scores_i8(void* stream, const float* q, const uint32_t* pool, uint64_t pool_words,
+                              const uint32_t* block_tables, const uint32_t* seq_lens, const float* scales,
+                              uint64_t n_scales, float* scores, uint32_t batch, uint32_t n_heads, uint32_t group,
+                              uint32_t head_dim, uint32_t block_size, uint32_t kv_stride, uint32_t cap,
+                              uint32_t max_bt, float scale);
+/* paged_decode_apply_i8_batched (crates/kernels/wgsl/paged_decode_apply_i8_batched.wgsl:28-53):
+ * ctx[b][h*head_dim + d] = sum over j < seq_lens[b] (in order) of (probs[b][h][j] * code)
+ * * vscale. Step bindings [probs, pool, block_tables, seq_lens, scales, ctx], params
+ * [batch, n_heads, group, head_dim, block_size, kv_stride, cap, max_bt]. */
+int bh_paged_decode_apply_i8(void* stream, const float* probs, const uint32_t* pool, uint64_t pool_words,
+                             const uint32_t* block_tables, const uint32_t* seq_lens, const float* scales,
+                             uint64_t n_scales, float* ctx, uint32_t batch, uint32_t n_heads, uint32_t group,
+                             uint32_t head_dim, uint32_t block_size, uint32_t kv_stride, uint32_t cap,
+                             uint32_t max_bt);
 
 /* f32 -> bf16 bits, round to nearest even, NaN -> (bits >> 16) | 0x0040: the
  * conversion every bf16 output of this library goes through
@@ -421,6 +459,12 @@ int bh_qwen3_decode(bh_qwen3* e, uint32_t steps, uint32_t flags, uint32_t* out);
 int bh_qwen3_logits(bh_qwen3* e, float* out, uint64_t n);
 /* Positions filled so far (prompt + decoded) of each sequence: len[batch]. */
 int bh_qwen3_lengths(bh_qwen3* e, uint32_t* len, uint32_t batch);
+/* Copy the cache of one layer and sequence to the host (which: 0 = K, 1 = V):
+ * positions pos0..pos0+npos, [npos][n_kv_heads*head_dim] f32, or int8 codes
+ * with kv_int8, then (kv_int8, scales not NULL) their scales [npos][n_kv_heads].
+ * A validation aid: the codes and scales are the engine's own. */
+int bh_qwen3_kv_read(bh_qwen3* e, uint32_t layer, uint32_t seq, uint32_t which, uint32_t pos0, uint32_t npos,
+                     void* data, float* scales);
 /* int8 KV: per-kv-head ceilings of layer `layer` for K (which 0) or V (1);
  * the scale is min(max|x|, clip)/127. Default FLT_MAX (no clipping), the
  * reference's uncalibrated sentinel. */

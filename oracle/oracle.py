@@ -60,6 +60,12 @@ def lib():
             "or_qwen3_param_count": (u64, [vp]),
             "or_qwen3_generate": (i32, [vp, vp, i32, vp, u32, u32, u32, vp, vp]),
             "or_qwen3_cpu_decode": (C.c_double, [vp, u64, i32, u32, u32]),
+            "or_qwen3_generate_clip": (i32, [vp, vp, i32, vp, u32, u32, u32, vp, vp, vp, vp]),
+            "or_kv8_code": (C.c_int8, [C.c_float, C.c_float]),
+            "or_paged_kv_append_i8_clipped": (None, [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32]),
+            "or_paged_decode_scores_i8": (None, [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, u32,
+                                                 C.c_float]),
+            "or_paged_decode_apply_i8": (None, [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, u32]),
         }
         for n, (r, a) in sig.items():
             f = getattr(L, n)
@@ -335,8 +341,10 @@ def _qcfg(cfg):
     return c
 
 
-def qwen3_generate(cfg, weights, prompts, steps, int8=True):
-    """or_qwen3_generate: greedy tokens [(steps+1), batch] and logits [(steps+1), batch, vocab]."""
+def qwen3_generate(cfg, weights, prompts, steps, int8=True, kclip=None, vclip=None):
+    """or_qwen3_generate_clip: greedy tokens [(steps+1), batch] and logits
+    [(steps+1), batch, vocab]; kclip/vclip [n_layers, n_kv_heads] are the int8
+    KV clip ceilings (None: FLT_MAX)."""
     c = _qcfg(cfg)
     blob = np.concatenate([weights[n].ravel() for n, _ in qwen3_param_list(cfg)]).astype(np.float32)
     assert blob.size == lib().or_qwen3_param_count(C.byref(c))
@@ -344,8 +352,12 @@ def qwen3_generate(cfg, weights, prompts, steps, int8=True):
     batch, ln = prompts.shape
     toks = np.zeros((steps + 1, batch), np.uint32)
     logits = np.zeros((steps + 1, batch, cfg["vocab"]), np.float32)
-    rc = lib().or_qwen3_generate(C.byref(c), _p(blob), 1 if int8 else 0, _p(prompts), batch, ln, steps,
-                                 _p(toks), _p(logits))
+    kc = None if kclip is None else _c(kclip, np.float32)
+    vc = None if vclip is None else _c(vclip, np.float32)
+    for t in (kc, vc):
+        assert t is None or t.size == cfg["n_layers"] * cfg["n_kv_heads"]
+    rc = lib().or_qwen3_generate_clip(C.byref(c), _p(blob), 1 if int8 else 0, _p(prompts), batch, ln, steps,
+                                      _p(toks), _p(logits), _p(kc), _p(vc))
     assert rc == 0
     return toks, logits
 
@@ -404,3 +416,47 @@ def acc_exact_q4(xq, w4, k, rows=None, cols=None):
     a = unpack_i8(xq if rows is None else np.asarray(xq)[rows]).astype(np.float64)[:, :k]
     b = unpack_q4(w4 if cols is None else np.asarray(w4)[cols], k).astype(np.float64)
     return (a @ b.T).astype(np.int64).astype(np.int32)
+
+
+# ---------------------------------------------------------------- int8 paged KV
+def kv8_code(x, scale):
+    """or_kv8_code: clamp(i32(round_even(x / scale)), -127, 127)."""
+    return int(lib().or_kv8_code(float(x), float(scale)))
+
+
+def paged_kv_append_i8(src, blocks, offsets, clip, pool, scales, block_size, head_dim):
+    """or_paged_kv_append_i8_clipped on (copies of) pool [u32 words] and scales; returns both."""
+    src = _c(src, np.float32)
+    batch, kv_stride = src.shape
+    blocks, offsets, clip = _c(blocks, np.uint32), _c(offsets, np.uint32), _c(clip, np.float32)
+    pool = _c(pool, np.uint32).copy()
+    scales = _c(scales, np.float32).copy()
+    lib().or_paged_kv_append_i8_clipped(_p(src), _p(blocks), _p(offsets), _p(clip), _p(pool), _p(scales), batch,
+                                        kv_stride, block_size, head_dim)
+    return pool, scales
+
+
+def paged_decode_scores_i8(q, pool, block_tables, seq_lens, scales, scores, n_heads, group, head_dim, block_size,
+                           kv_stride, cap, scale):
+    """or_paged_decode_scores_i8; `scores` [batch, n_heads, cap] is copied and
+    returned with the entries below each seq_len overwritten."""
+    block_tables = _c(block_tables, np.uint32)
+    batch, max_bt = block_tables.shape
+    q, pool, seq_lens, scales = _c(q, np.float32), _c(pool, np.uint32), _c(seq_lens, np.uint32), _c(scales, np.float32)
+    out = _c(scores, np.float32).copy()
+    lib().or_paged_decode_scores_i8(_p(q), _p(pool), _p(block_tables), _p(seq_lens), _p(scales), _p(out), batch,
+                                    n_heads, group, head_dim, block_size, kv_stride, cap, max_bt, scale)
+    return out
+
+
+def paged_decode_apply_i8(probs, pool, block_tables, seq_lens, scales, n_heads, group, head_dim, block_size,
+                          kv_stride, cap):
+    """or_paged_decode_apply_i8: ctx [batch, n_heads*head_dim]."""
+    block_tables = _c(block_tables, np.uint32)
+    batch, max_bt = block_tables.shape
+    probs, pool = _c(probs, np.float32), _c(pool, np.uint32)
+    seq_lens, scales = _c(seq_lens, np.uint32), _c(scales, np.float32)
+    ctx = np.zeros((batch, n_heads * head_dim), np.float32)
+    lib().or_paged_decode_apply_i8(_p(probs), _p(pool), _p(block_tables), _p(seq_lens), _p(scales), _p(ctx), batch,
+                                   n_heads, group, head_dim, block_size, kv_stride, cap, max_bt)
+    return ctx

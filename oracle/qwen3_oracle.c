@@ -8,8 +8,9 @@
  * which reads only earlier positions):
  *
  * With kv_int8, K and V are stored as int8 codes with one scale per (token,
- * kv head): scale = max|x|/127 (1 if 0), code = clamp(round_even(x/scale))
- * (paged_kv_append_i8_clipped_batched.wgsl, FLT_MAX clip); scores use
+ * kv head): scale = min(max|x|, clip)/127 (1 if 0), code =
+ * clamp(round_even(x/scale)) (paged_kv_append_i8_clipped_batched.wgsl; the
+ * clip table per (layer, kv head) is FLT_MAX unless given); scores use
  * (q . f32(code)) * kscale * hd^-1/2 and the context (p * f32(code)) * vscale
  * (paged_decode_{scores,apply}_i8_batched.wgsl).
  *
@@ -50,6 +51,7 @@
 
 #include "brain_oracle.h"
 #include "qwen3_oracle.h"
+#include "kv8_oracle.h"
 
 typedef struct {
     const float *ln1, *wq, *wk, *wv, *qn, *kn, *wo, *ln2, *gate, *up, *down;
@@ -147,6 +149,12 @@ uint64_t or_qwen3_param_count(const or_qwen3_config *c) {
 
 int or_qwen3_generate(const or_qwen3_config *c, const float *params, int int8, const uint32_t *prompts,
                       uint32_t batch, uint32_t len, uint32_t steps, uint32_t *out_tokens, float *out_logits) {
+    return or_qwen3_generate_clip(c, params, int8, prompts, batch, len, steps, out_tokens, out_logits, NULL, NULL);
+}
+
+int or_qwen3_generate_clip(const or_qwen3_config *c, const float *params, int int8, const uint32_t *prompts,
+                           uint32_t batch, uint32_t len, uint32_t steps, uint32_t *out_tokens, float *out_logits,
+                           const float *kclip, const float *vclip) {
     const uint32_t d = c->d_model, ff = c->d_ff, hd = c->head_dim, nh = c->n_heads, nkv = c->n_kv_heads;
     const uint32_t hq = nh * hd, hkv = nkv * hd, G = nh / nkv, L = c->n_layers, V = c->vocab;
     if (!len || nh % nkv || hd % 2) return -1;
@@ -223,17 +231,17 @@ int or_qwen3_generate(const or_qwen3_config *c, const float *params, int int8, c
                 memcpy(Vl + (size_t)pos * hkv, v, sizeof(float) * hkv);
                 float *KSl = KS + (size_t)l * T * nkv, *VSl = VS + (size_t)l * T * nkv;
                 if (c->kv_int8) {
+                    /* paged_kv_append_i8_clipped_batched.wgsl:56-77 (or_kv8_code): the
+                     * scale is min(max|x|, clip[l][h]) / 127, 1 when that is 0. */
                     for (uint32_t h = 0; h < nkv; ++h)
                         for (int which = 0; which < 2; ++which) {
                             float *xr = (which ? Vl : Kl) + (size_t)pos * hkv + h * hd;
+                            const float *ct = which ? vclip : kclip;
                             float mxa = 0.0f;
                             for (uint32_t e = 0; e < hd; ++e) mxa = fmaxf(mxa, fabsf(xr[e]));
-                            float sc = fminf(mxa, FLT_MAX) / 127.0f;
+                            float sc = fminf(mxa, ct ? ct[(size_t)l * nkv + h] : FLT_MAX) / 127.0f;
                             if (sc == 0.0f) sc = 1.0f;
-                            for (uint32_t e = 0; e < hd; ++e) {
-                                float qv = rintf(xr[e] / sc);
-                                xr[e] = qv < -127.0f ? -127.0f : (qv > 127.0f ? 127.0f : qv);
-                            }
+                            for (uint32_t e = 0; e < hd; ++e) xr[e] = (float)or_kv8_code(xr[e], sc);
                             (which ? VSl : KSl)[(size_t)pos * nkv + h] = sc;
                         }
                 }

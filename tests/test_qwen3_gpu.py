@@ -58,16 +58,28 @@ def engine_for(cfg, w, max_batch, max_seq, max_rows=None):
 
 
 def compare(cfg, w, prompts, steps, max_rows=None):
-    toks_o, logits_o = o.qwen3_generate(cfg, w, prompts, steps, int8=True)
+    compare_clip(cfg, w, prompts, steps, None, None, max_rows)
+
+
+def compare_clip(cfg, w, prompts, steps, kclip, vclip, max_rows=None):
+    """The engine against the oracle; kclip/vclip [n_layers, n_kv_heads] are
+    int8 KV clip tables given to both (None: no clipping)."""
+    toks_o, logits_o = o.qwen3_generate(cfg, w, prompts, steps, int8=True, kclip=kclip, vclip=vclip)
     _, logits_f = o.qwen3_generate(cfg, w, prompts, 0, int8=False)
     e = engine_for(cfg, w, prompts.shape[0], prompts.shape[1] + steps + 1, max_rows)
+    for l in range(cfg["n_layers"]):
+        if kclip is not None:
+            e.set_kv_clip(l, 0, kclip[l])
+        if vclip is not None:
+            e.set_kv_clip(l, 1, vclip[l])
     first = e.prefill(prompts)
     got_logits = [e.logits()]
     got_toks = [first]
     for _ in range(steps):
         got_toks.append(e.decode(1)[0])
         got_logits.append(e.logits())
-    assert rel_l2(got_logits[0], logits_f[0]) < 0.10
+    if kclip is None and vclip is None:  # the reference's int8-vs-fp32 bound holds without clipping
+        assert rel_l2(got_logits[0], logits_f[0]) < 0.10
     checked = 0
     for s in range(steps + 1):
         per_seq = [rel_l2(got_logits[s][b], logits_o[s][b]) for b in range(prompts.shape[0])]
