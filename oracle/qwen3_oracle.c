@@ -91,6 +91,9 @@ static void lin_apply(const lin_t *l, const float *x, float *out) {
         or_max_abs_row(x, 1, k, &sx);
         or_quant_pack(x, &sx, 1, k, xq);
         const int8_t *a = (const int8_t *)xq;
+        /* Output rows are independent and each keeps its own order: threads
+         * only change the speed. */
+#pragma omp parallel for schedule(static)
         for (uint32_t j = 0; j < n; ++j) {
             const int8_t *b = (const int8_t *)(l->packed + (size_t)j * (k / 4));
             int64_t acc = 0;
@@ -100,6 +103,7 @@ static void lin_apply(const lin_t *l, const float *x, float *out) {
         }
         free(xq);
     } else {
+#pragma omp parallel for schedule(static)
         for (uint32_t j = 0; j < n; ++j) {
             const float *w = l->w + (size_t)j * k;
             double acc = 0.0;
@@ -179,6 +183,7 @@ int or_qwen3_generate_clip(const or_qwen3_config *c, const float *params, int in
     const float *head_w = c->tie_embeddings ? tok : p;
 
     lin_t *lq = (lin_t *)calloc(L * 7, sizeof(lin_t));
+#pragma omp parallel for schedule(dynamic)
     for (uint32_t l = 0; l < L; ++l) {
         lin_init(&lq[7 * l + 0], ly[l].wq, hq, d, int8);
         lin_init(&lq[7 * l + 1], ly[l].wk, hkv, d, int8);
