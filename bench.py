@@ -12,7 +12,10 @@ from HBM, not the Infinity Cache.
   roofline = the GEMV kernel alone: its algorithmic bytes (N*K + 4N + M*K + 2*M*N)
              / its average launch duration, timed with HIP events on the stream
              it runs on, vs 8 TB/s
-Also reported: the prefill GEMM sweep (configs[2], each shape timed as one HIP
+Also reported: each configs[1] shape alone, cold (a graph cycling over
+weight copies that exceed the Infinity Cache); configs[0] (one linear,
+M=16 K=1024 N=3072, f32 out) on the GPU beside the restated backend-cpu path
+on this host; the prefill GEMM sweep (configs[2], each shape timed as one HIP
 graph of back-to-back launches) in TOPS vs the 5.0 POPS int8
 dense MFMA peak, an MFMA roof probe, and the CPU baselines timed on this host
 on bounded samples: the restated backend-cpu decode path (OpenMP) for the
@@ -45,8 +48,8 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on CPU-baseline work")
-    ap.add_argument("--only", default="", help="profiling aid: 'decode', 'gemv', 'prefill', 'quant', 'qwen3', 'dit', "
-                    "'w4a8' or 'copy' only")
+    ap.add_argument("--only", default="", help="profiling aid: 'decode', 'gemv', 'shapes', 'config0', 'prefill', "
+                    "'quant', 'qwen3', 'dit', 'w4a8' or 'copy' only")
     ap.add_argument("--no-quant", action="store_true")
     ap.add_argument("--no-qwen3", action="store_true")
     ap.add_argument("--no-dit", action="store_true")
@@ -170,9 +173,8 @@ def gemv_measure(torch, sets, gemv, steps, step_ms, wall):
     # GEMV kernel duration: the step's 16 GEMV launches alone (activations
     # already quantized) captured as a second graph and replayed; events on the
     # replay stream bracket the replays, so the per-launch average counts the
-    # kernel plus the dispatch gap to the next node (a slight overestimate of
-    # the kernel-only time rocprofv3 reports). Per-shape times come from a
-    # graph of 8 launches of one shape each.
+    # kernel plus the dispatch gap to the next node. Every weight is re-read
+    # only after the other 15 (656 MB in total), so every launch is cold.
     ggraph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(ggraph):
         for s in sets:
@@ -188,28 +190,116 @@ def gemv_measure(torch, sets, gemv, steps, step_ms, wall):
     b.record(stream)
     torch.cuda.synchronize()
     mean_us = a.elapsed_time(b) * 1e3 / (reps * len(sets))
-    shapes = []
-    for s in sets:
-        g1 = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g1):
-            for _ in range(8):
-                gemv(s)
-        g1.replay()
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(3):
-            g1.replay()
-        b.record(stream)
-        torch.cuda.synchronize()
-        us = a.elapsed_time(b) * 1e3 / 24
-        shapes.append(dict(m=s["m"], k=s["k"], n=s["n"], gemv_us=round(us, 2),
-                           gemv_gbs=round(gemv_bytes(s["m"], s["k"], s["n"]) / us / 1e3, 1)))
-        del g1
     mean_bytes = sum(gemv_bytes(s["m"], s["k"], s["n"]) for s in sets) / len(sets)
     step_bytes = sum(linear_bytes(s["m"], s["k"], s["n"]) for s in sets)
     return dict(step_ms=step_ms, wall=wall, step_bytes=step_bytes, gemv_mean_us=mean_us,
-                gemv_mean_bytes=mean_bytes, shapes=shapes)
+                gemv_mean_bytes=mean_bytes)
+
+
+def graph_per_launch_us(torch, fns, reps=3):
+    """One HIP graph of one launch per callable (each on its own weight
+    copy), replayed `reps` times; microseconds per launch from HIP events on
+    the replay stream."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for fn in fns:
+            fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for fn in fns:
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    cur = torch.cuda.current_stream()
+    a.record(cur)
+    for _ in range(reps):
+        g.replay()
+    b.record(cur)
+    torch.cuda.synchronize()
+    del g
+    return a.elapsed_time(b) * 1e3 / (reps * len(fns))
+
+
+def cold_copies(torch, dev, gen, m, k, n, pool_bytes=512 << 20, max_copies=128):
+    """Enough weight copies of one shape that a graph cycling through them
+    reads every launch's weights from HBM (together above the 256 MB
+    Infinity Cache)."""
+    c = max(2, min(max_copies, -(-pool_bytes // (n * k))))
+    ws = [torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev, generator=gen).view(torch.int32)
+          for _ in range(c)]
+    sw = torch.empty(n, device=dev).uniform_(0.002, 0.02, generator=gen)
+    return ws, sw
+
+
+def bench_decode_shapes(torch, lib, dev, gen):
+    """Each configs[1] shape alone, cold: a graph of launches cycling over
+    weight copies that together exceed the Infinity Cache (the GEMV alone on
+    a pre-quantized activation, bf16 out)."""
+    from brain_amd._lib import BH_OUT_BF16, check
+    rows = []
+    for m in DECODE_M:
+        for k, n in DECODE_KN:
+            ws, sw = cold_copies(torch, dev, gen, m, k, n)
+            xq = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=dev, generator=gen).view(torch.int32)
+            sx = torch.empty(m, device=dev).uniform_(0.001, 0.05, generator=gen)
+            out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+
+            def fn(w):
+                return lambda: check(lib.bh_matmul_i8_gemv(torch.cuda.current_stream().cuda_stream, xq.data_ptr(),
+                                                           w.data_ptr(), sx.data_ptr(), sw.data_ptr(), None,
+                                                           out.data_ptr(), BH_OUT_BF16, m, k // 4, n))
+            us = graph_per_launch_us(torch, [fn(w) for w in ws])
+            gb = gemv_bytes(m, k, n)
+            rows.append(dict(m=m, k=k, n=n, copies=len(ws), gemv_us=round(us, 2), gemv_gbs=round(gb / us / 1e3, 1),
+                             frac=round(gb / us / 1e3 / HBM_PEAK_GBS, 3)))
+            del ws
+    return rows
+
+
+def bench_config0(torch, lib, dev, gen, cpu=True, budget_s=5.0):
+    """one int8 linear, M=16, K=1024, N=3072, f32 out (per-token
+    quantization inside the call: bh_linear_i8), cold weights on the GPU;
+    beside it the restated backend-cpu path (max_abs_row -> quant_pack ->
+    matmul_i8_gemv, OpenMP over output columns) on this host, same shape."""
+    from brain_amd._lib import BH_OUT_F32, check
+    m, k, n = 16, 1024, 3072
+    ws, sw = cold_copies(torch, dev, gen, m, k, n)
+    x = torch.randn(m, k, device=dev, generator=gen)
+    sx = torch.empty(m, device=dev)
+    xq = torch.empty(m, k // 4, dtype=torch.int32, device=dev)
+    out = torch.empty(m, n, device=dev)
+
+    def fn(w):
+        return lambda: check(lib.bh_linear_i8(torch.cuda.current_stream().cuda_stream, x.data_ptr(), w.data_ptr(),
+                                              sw.data_ptr(), None, sx.data_ptr(), xq.data_ptr(), out.data_ptr(),
+                                              BH_OUT_F32, m, k, n))
+    us = graph_per_launch_us(torch, [fn(w) for w in ws])
+    byts = linear_bytes(m, k, n) + 2 * m * n  # f32 out: 4 bytes per output
+    res = {"workload": "configs[0]: int8 linear M=16 K=1024 N=3072, per-token quant + GEMV, f32 out",
+           "gpu_us": round(us, 2), "gpu_gbs": round(byts / us / 1e3, 1), "copies": len(ws)}
+    if cpu:
+        import numpy as np
+        from oracle import oracle as o
+        threads = min(len(os.sched_getaffinity(0)), 16)
+        wq, swh = o.synth_weights(n, k, 3)
+        xh = o.synth_acts(m, k, 4)
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 200):
+            t0 = time.perf_counter()
+            o.cpu_linear_gemv(xh, wq, swh, threads)
+            times.append(time.perf_counter() - t0)
+        t = sorted(times)[len(times) // 2] * 1e6
+        res.update({"cpu_us": round(t, 1), "cpu_gbs": round(byts / t / 1e3, 2), "cpu_cores": threads,
+                    "cpu_kind": "port", "cpu_sample": f"the same linear, {len(times)} runs, median",
+                    "gpu_vs_cpu": round(t / us, 1)})
+        del np
+    del ws
+    return res
 
 
 def bench_prefill(torch, lib, dev, gen, reps):
@@ -616,6 +706,10 @@ def main():
         sets = make_decode_set(torch, dev, gen)
         res["decode"] = bench_decode(torch, lib, sets, args.steps, args.warmup, gemv_only=args.only == "gemv")
         del sets
+    if args.only in ("", "shapes"):
+        res["shapes"] = bench_decode_shapes(torch, lib, dev, gen)
+    if args.only in ("", "config0"):
+        res["config0"] = bench_config0(torch, lib, dev, gen, cpu=not args.no_cpu)
     if args.only in ("", "prefill") and not args.no_prefill:
         res["prefill"] = bench_prefill(torch, lib, dev, gen, args.prefill_reps)
     if args.only in ("", "quant") and not args.no_quant:
@@ -667,7 +761,8 @@ def main():
                      "kernel": "gemv_i8_kernel", "avg_launch_us": round(d["gemv_mean_us"], 2),
                      "avg_algorithmic_bytes": round(d["gemv_mean_bytes"])},
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
-        "decode_shapes_warm": d["shapes"],
+        "decode_shapes_cold": res["shapes"],
+        "config0_linear": res["config0"],
         "mfma_roof_probe_tops": roof,
     }
     if "prefill" in res:

@@ -493,6 +493,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
 // item is loaded ahead of its weights, so no wait in the loop drains the
 // memory pipe. Work items are (column group, batch of U = 16 64-byte K
 // chunks); K (= KB bytes) is a compile-time multiple of 1024.
+// Measured on MI355X (LM head, cold): two waves per SIMD (256 VGPRs, fewer
+// parked results) and non-temporal weight loads were both slower than this
+// form (one wave per SIMD, 288 VGPRs with the accumulation registers).
 template <int OUT, bool HAS_BIAS, int KB>
 __global__ __launch_bounds__(256) void gemv_i8_stream_kernel(GemvArgs a, int groups_per_wave) {
     constexpr int U = 16, kbytes = KB, nbatch = KB / 1024;
