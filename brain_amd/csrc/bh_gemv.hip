@@ -77,7 +77,11 @@ struct GemvArgs {
 // LDS first, 2 = quantized from f32 into LDS by the workgroup itself (each
 // wave quantizes whole rows: exact row max, sx = max(max,1e-8)/127, codes
 // clamp(rne(x * (1/sx))) -- bit-identical to bh_quantize_rows).
-template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int KSPLIT, int XMODE, int U, int CG, int NW = GV_WAVES>
+// PRE (XMODE 3 / 4 with several rows): 8 * R + G fixes the prologue's rows
+// per thread and float4 groups per row at compile time; 0 picks them at run
+// time.
+template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int KSPLIT, int XMODE, int U, int CG, int NW = GV_WAVES,
+          int PRE = 0>
 __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
     constexpr bool XLDS = XMODE != 0;
     constexpr int SLOTS = NW / KSPLIT;  // wave slots per workgroup, each CG column groups
@@ -175,97 +179,177 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
         if (threadIdx.x == 0) sxs[0] = sxv;
         __syncthreads();
       } else {
-        // Rows in groups of 256 threads (NW/4 rows per round). The sum of
-        // squares uses exactly the reduction of the decoder's separate
-        // norm_quant kernel -- thread t accumulates float4 groups t, t+256, ...
-        // in order, a wave xor-tree, then the 4 wave sums in order -- so the
-        // quantized rows are bit-identical to that kernel's.
+        // Rows in groups of 256 threads, NW/4 groups; each thread holds R
+        // rows (group grp takes rows grp, grp + NG, ...), so up to NG * R
+        // rows share one burst of loads and two barriers. The loads
+        // are unconditional (rows past m and float4 groups past K read
+        // clamped addresses and are zeroed afterwards): a load under a branch
+        // gets its own wait, one memory round trip per row. The sum of
+        // squares of a row uses exactly the reduction of the decoder's
+        // separate norm_quant kernel -- thread t accumulates float4 groups t,
+        // t+256, ... in order, a wave xor-tree, then the 4 wave sums in
+        // order -- so the quantized rows are bit-identical to that kernel's.
+        //   R (1, 2 or 4) and G are picked at run time, each case its own
+        // unrolled code: the kernel runs once per decoder linear, so its
+        // executed code is fetched cold every launch and must stay short.
         static_assert(NW % 4 == 0, "row groups of 4 waves");
-        constexpr int NG = NW / 4, GMAX = 4;  // rows per round, float4 per thread (K <= 4096)
-        __shared__ float gred[NW];
+        constexpr int NG = NW / 4;  // row groups
+        __shared__ float gred[4][NW];
+        __shared__ float gmx[4][NW];
         const int grp = wave >> 2, gt = threadIdx.x & 255;
         const int d = kbytes, d4 = d >> 2;
         const bool first = blockIdx.x == 0;
-        // The norm weights (the same for every row) go out with the first
-        // loads, not behind the reduction and the residual stores.
-        float4 wv[GMAX];
+        // G: float4 groups per thread and row (K <= 1024 G); K <= 4096.
+        auto rows = [&](auto gtag, auto rtag) {
+            constexpr int G = decltype(gtag)::value;
+            constexpr int RMAX = decltype(rtag)::value;
+            // The norm weights (the same for every row) go out with the
+            // first loads, not behind the reduction and the residual stores.
+            float4 wv[G];
 #pragma unroll
-        for (int g = 0; g < GMAX; ++g) {
-            const int i = gt + 256 * g;
-            wv[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if constexpr (XMODE == 3)
-                if (i < d4) wv[g] = reinterpret_cast<const float4*>(a.pre_w)[i];
-        }
-        for (int r0 = 0; r0 < m; r0 += NG) {
-            const int r = r0 + grp;
-            const bool live = r < m;
-            float4 v[GMAX];
-            float ss = 0.0f;
+            for (int g = 0; g < G; ++g) {
+                wv[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if constexpr (XMODE == 3) wv[g] = reinterpret_cast<const float4*>(a.pre_w)[min(gt + 256 * g, d4 - 1)];
+            }
+            for (int r0 = 0; r0 < m; r0 += NG * RMAX) {
+                float4 v[RMAX][G];
+                int rc[RMAX];
 #pragma unroll
-            for (int g = 0; g < GMAX; ++g) {
-                const int i = gt + 256 * g;
-                v[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (!live || i >= d4) continue;
+                for (int j = 0; j < RMAX; ++j) rc[j] = min(r0 + grp + NG * j, m - 1);
                 if constexpr (XMODE == 3) {
-                    const float4* src = a.pre_tok ? reinterpret_cast<const float4*>(a.pre_emb + (size_t)a.pre_tok[r] * d)
-                                                  : reinterpret_cast<const float4*>(a.pre_a + (size_t)r * d);
-                    float4 x = src[i];
-                    if (a.pre_b) {
-                        const float4 b = reinterpret_cast<const float4*>(a.pre_b + (size_t)r * d)[i];
-                        x = make_float4(x.x + b.x, x.y + b.y, x.z + b.z, x.w + b.w);
+                    if (a.pre_tok) {
+                        int tk[RMAX];
+#pragma unroll
+                        for (int j = 0; j < RMAX; ++j) tk[j] = (int)a.pre_tok[rc[j]];
+#pragma unroll
+                        for (int j = 0; j < RMAX; ++j)
+#pragma unroll
+                            for (int g = 0; g < G; ++g)
+                                v[j][g] = reinterpret_cast<const float4*>(a.pre_emb + (size_t)tk[j] * d)[min(gt + 256 * g, d4 - 1)];
+                    } else if (a.pre_b) {
+                        float4 bv[RMAX][G];
+#pragma unroll
+                        for (int j = 0; j < RMAX; ++j)
+#pragma unroll
+                            for (int g = 0; g < G; ++g) {
+                                const int ic = min(gt + 256 * g, d4 - 1);
+                                v[j][g] = reinterpret_cast<const float4*>(a.pre_a + (size_t)rc[j] * d)[ic];
+                                bv[j][g] = reinterpret_cast<const float4*>(a.pre_b + (size_t)rc[j] * d)[ic];
+                            }
+#pragma unroll
+                        for (int j = 0; j < RMAX; ++j)
+#pragma unroll
+                            for (int g = 0; g < G; ++g)
+                                v[j][g] = make_float4(v[j][g].x + bv[j][g].x, v[j][g].y + bv[j][g].y,
+                                                      v[j][g].z + bv[j][g].z, v[j][g].w + bv[j][g].w);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < RMAX; ++j)
+#pragma unroll
+                            for (int g = 0; g < G; ++g)
+                                v[j][g] = reinterpret_cast<const float4*>(a.pre_a + (size_t)rc[j] * d)[min(gt + 256 * g, d4 - 1)];
                     }
-                    v[g] = x;
-                    ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
-                    if (first) reinterpret_cast<float4*>(a.res_out + (size_t)r * d)[i] = x;
                 } else {
-                    const float4 gv = reinterpret_cast<const float4*>(a.pre_a + (size_t)r * 2 * d)[i];
-                    const float4 uv = reinterpret_cast<const float4*>(a.pre_a + (size_t)r * 2 * d + d)[i];
-                    v[g] = make_float4(gv.x / (1.0f + expf(-gv.x)) * uv.x, gv.y / (1.0f + expf(-gv.y)) * uv.y,
-                                       gv.z / (1.0f + expf(-gv.z)) * uv.z, gv.w / (1.0f + expf(-gv.w)) * uv.w);
-                }
-            }
-            if constexpr (XMODE == 3) {
+                    float4 uv[RMAX][G];
 #pragma unroll
-                for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
-                if (lane == 0) gred[wave] = ss;
+                    for (int j = 0; j < RMAX; ++j)
+#pragma unroll
+                        for (int g = 0; g < G; ++g) {
+                            const int ic = min(gt + 256 * g, d4 - 1);
+                            v[j][g] = reinterpret_cast<const float4*>(a.pre_a + (size_t)rc[j] * 2 * d)[ic];
+                            uv[j][g] = reinterpret_cast<const float4*>(a.pre_a + (size_t)rc[j] * 2 * d + d)[ic];
+                        }
+#pragma unroll
+                    for (int j = 0; j < RMAX; ++j)
+#pragma unroll
+                        for (int g = 0; g < G; ++g) {
+                            const float4 gv = v[j][g], u = uv[j][g];
+                            v[j][g] = make_float4(gv.x / (1.0f + expf(-gv.x)) * u.x, gv.y / (1.0f + expf(-gv.y)) * u.y,
+                                                  gv.z / (1.0f + expf(-gv.z)) * u.z, gv.w / (1.0f + expf(-gv.w)) * u.w);
+                        }
+                }
+                // Rows past m and groups past K hold clamped copies: zero them.
+#pragma unroll
+                for (int j = 0; j < RMAX; ++j)
+#pragma unroll
+                    for (int g = 0; g < G; ++g)
+                        if (r0 + grp + NG * j >= m || gt + 256 * g >= d4) v[j][g] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if constexpr (XMODE == 3) {
+#pragma unroll
+                    for (int j = 0; j < RMAX; ++j) {
+                        const int r = r0 + grp + NG * j;
+                        float ss = 0.0f;
+#pragma unroll
+                        for (int g = 0; g < G; ++g) {
+                            const float4 x = v[j][g];
+                            ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+                            if (first && r < m && gt + 256 * g < d4)
+                                reinterpret_cast<float4*>(a.res_out + (size_t)r * d)[gt + 256 * g] = x;
+                        }
+#pragma unroll
+                        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+                        if (lane == 0) gred[j][wave] = ss;
+                    }
+                    __syncthreads();
+#pragma unroll
+                    for (int j = 0; j < RMAX; ++j) {
+                        float tot = gred[j][grp * 4];
+#pragma unroll
+                        for (int w = 1; w < 4; ++w) tot += gred[j][grp * 4 + w];
+                        const float inv = 1.0f / sqrtf(tot / (float)d + a.eps);
+                        const bool live = r0 + grp + NG * j < m;
+#pragma unroll
+                        for (int g = 0; g < G; ++g)
+                            if (live && gt + 256 * g < d4)
+                                v[j][g] = make_float4(v[j][g].x * inv * wv[g].x, v[j][g].y * inv * wv[g].y,
+                                                      v[j][g].z * inv * wv[g].z, v[j][g].w * inv * wv[g].w);
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < RMAX; ++j) {
+                    float am = 0.0f;
+#pragma unroll
+                    for (int g = 0; g < G; ++g)
+                        am = fmaxf(am, fmaxf(fmaxf(fabsf(v[j][g].x), fabsf(v[j][g].y)),
+                                             fmaxf(fabsf(v[j][g].z), fabsf(v[j][g].w))));
+#pragma unroll
+                    for (int off = 32; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+                    if (lane == 0) gmx[j][wave] = am;
+                }
                 __syncthreads();
-                float tot = gred[grp * 4];
 #pragma unroll
-                for (int w = 1; w < 4; ++w) tot += gred[grp * 4 + w];
-                const float inv = 1.0f / sqrtf(tot / (float)d + a.eps);
+                for (int j = 0; j < RMAX; ++j) {
+                    const int r = r0 + grp + NG * j;
+                    if (r >= m) continue;
+                    float rm = gmx[j][grp * 4];
 #pragma unroll
-                for (int g = 0; g < GMAX; ++g) {
-                    const int i = gt + 256 * g;
-                    if (!live || i >= d4) continue;
-                    v[g] = make_float4(v[g].x * inv * wv[g].x, v[g].y * inv * wv[g].y, v[g].z * inv * wv[g].z,
-                                       v[g].w * inv * wv[g].w);
+                    for (int w = 1; w < 4; ++w) rm = fmaxf(rm, gmx[j][grp * 4 + w]);
+                    const float sxv = fmaxf(rm, 1e-8f) / 127.0f;
+                    const float invq = 1.0f / sxv;
+                    uint8_t* xr8 = xs + r * xstride;
+#pragma unroll
+                    for (int g = 0; g < G; ++g) {
+                        const int i = gt + 256 * g;
+                        if (i < d4) *reinterpret_cast<uint32_t*>(xr8 + 4 * i) = quant_word(v[j][g], invq);
+                    }
+                    if (gt < 4) *reinterpret_cast<uint32_t*>(xr8 + d + 4 * gt) = 0u;  // pad past K
+                    if (gt == 0) sxs[r] = sxv;
                 }
-                __syncthreads();  // gred is reused for the max
+                __syncthreads();  // the rows are in LDS for every wave; gred / gmx are reused by the next round
             }
-            float am = 0.0f;
-#pragma unroll
-            for (int g = 0; g < GMAX; ++g)
-                am = fmaxf(am, fmaxf(fmaxf(fabsf(v[g].x), fabsf(v[g].y)), fmaxf(fabsf(v[g].z), fabsf(v[g].w))));
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
-            if (lane == 0) gred[wave] = am;
-            __syncthreads();
-            if (live) {
-                float rm = gred[grp * 4];
-#pragma unroll
-                for (int w = 1; w < 4; ++w) rm = fmaxf(rm, gred[grp * 4 + w]);
-                const float sxv = fmaxf(rm, 1e-8f) / 127.0f;
-                const float invq = 1.0f / sxv;
-                uint8_t* xr8 = xs + r * xstride;
-#pragma unroll
-                for (int g = 0; g < GMAX; ++g) {
-                    const int i = gt + 256 * g;
-                    if (i < d4) *reinterpret_cast<uint32_t*>(xr8 + 4 * i) = quant_word(v[g], invq);
-                }
-                if (gt < 4) *reinterpret_cast<uint32_t*>(xr8 + d + 4 * gt) = 0u;  // pad past K
-                if (gt == 0) sxs[r] = sxv;
-            }
-            __syncthreads();  // gred is reused by the next round
+        };
+        auto by_k = [&](auto rtag) {
+            if (d4 <= 256) rows(std::integral_constant<int, 1>{}, rtag);
+            else if (d4 <= 512) rows(std::integral_constant<int, 2>{}, rtag);
+            else if (d4 <= 768) rows(std::integral_constant<int, 3>{}, rtag);
+            else rows(std::integral_constant<int, 4>{}, rtag);
+        };
+        if constexpr (PRE != 0) {
+            rows(std::integral_constant<int, PRE % 8>{}, std::integral_constant<int, PRE / 8>{});
+        } else {
+            if (m <= NG) by_k(std::integral_constant<int, 1>{});
+            else if (m <= 2 * NG) by_k(std::integral_constant<int, 2>{});
+            else by_k(std::integral_constant<int, 4>{});
         }
       }
     } else if constexpr (XMODE == 2) {
@@ -653,14 +737,14 @@ static int gv_cfg() {
     return v;
 }
 
-template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int U, int CG, int KSPLIT = 4, int XMODE = 0>
+template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int U, int CG, int KSPLIT = 4, int XMODE = 0, int PRE = 0>
 static hipError_t gv_go(hipStream_t s, const GemvArgs& a) {
     constexpr int NW = KSPLIT > GV_WAVES ? KSPLIT : GV_WAVES;  // waves per workgroup
     constexpr int per_wg = (NW / KSPLIT) * CG;
     const int ngroups = (a.n + 15) / 16;
     const int grid = (ngroups + per_wg - 1) / per_wg;
     const size_t lds = XMODE ? (size_t)MT * 16 * (a.kg * 4 + 16) + MT * 16 * 4 : 0;
-    gemv_i8_kernel<MT, OUT, HAS_BIAS, ALIGNED, KSPLIT, XMODE, U, CG, NW><<<grid, NW * 64, lds, s>>>(a);
+    gemv_i8_kernel<MT, OUT, HAS_BIAS, ALIGNED, KSPLIT, XMODE, U, CG, NW, PRE><<<grid, NW * 64, lds, s>>>(a);
     return hipGetLastError();
 }
 
@@ -817,6 +901,20 @@ hipError_t launch_gemv_i8_pre(hipStream_t s, int mode, const uint32_t* pre_tok, 
     GemvArgs a{nullptr, wq, nullptr, sw, nullptr, out, m, kg, n, nullptr, 0, 0, nullptr, nullptr, nullptr,
                pre_tok, pre_emb, pre_a, pre_b, pre_w, res_out, eps};
     const int nchunks = (kbytes + 63) / 64;
+    // The decoder's own shapes (norm over K = 1024 on 8 waves, SwiGLU over
+    // K = 3072 on 16) get prologues fixed at compile time.
+    const int ng = nchunks >= 32 ? 4 : 2;  // row groups of the launch below
+    const int rpt = m <= ng ? 1 : m <= 2 * ng ? 2 : 4;
+    if (mode == 3 && kbytes == 1024) {
+        if (rpt == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 8 + 1>(s, a);
+        if (rpt == 2) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 16 + 1>(s, a);
+        return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 32 + 1>(s, a);
+    }
+    if (mode == 4 && kbytes == 3072) {
+        if (rpt == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 16, 4, 8 + 3>(s, a);
+        if (rpt == 2) return gv_go<1, OUT_F32, false, true, 4, 1, 16, 4, 16 + 3>(s, a);
+        return gv_go<1, OUT_F32, false, true, 4, 1, 16, 4, 32 + 3>(s, a);
+    }
     if (mode == 3) {
         if (nchunks >= 32) return gv_go<1, OUT_F32, false, true, 4, 1, 16, 3>(s, a);
         return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3>(s, a);

@@ -1104,13 +1104,20 @@ int launch_combine_quant(bh_qwen3* e, int rows, int splits) {
     return BH_OK;
 }
 
-// The fused producer + GEMV path: at most 4 rows (every workgroup redoes the
-// producer for all rows; at batch 8 that measured 19% slower than the
-// separate kernels, at batch 1 10% faster), K a multiple of 16 up to 4096,
-// and no measured preference for the MFMA tile at this shape.
+// The fused producer + GEMV path: at most 4 rows (BH_QWEN3_FUSE_ROWS
+// overrides it for measurements). Every workgroup redoes the producer for
+// all rows, re-reading their inputs from L2 (at 8 rows 64 KB per workgroup
+// for the norm, 196 KB for the SwiGLU): at batch 8 that measured 15% slower
+// than the separate kernels even with all rows in one burst of loads, at
+// batch 1 10% faster. K a multiple of 16 up to 4096, and no measured
+// preference for the MFMA tile at this shape.
 bool fused_ok(bh_qwen3* e, int rows, int k, int n) {
     (void)e;
-    if (rows < 1 || rows > 4 || k % 16 != 0 || k > 4096) return false;
+    static const int max_rows = [] {
+        const char* v = getenv("BH_QWEN3_FUSE_ROWS");
+        return v ? atoi(v) : 4;
+    }();
+    if (rows < 1 || rows > max_rows || k % 16 != 0 || k > 4096) return false;
     return tuned_variant((uint32_t)rows, (uint32_t)n, (uint32_t)k) != BH_VARIANT_PACKED_INT8;
 }
 
