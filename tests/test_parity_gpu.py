@@ -275,7 +275,8 @@ def test_linear_config0(gpu):
 
 
 @pytest.mark.parametrize("m", [1, 4, 8, 16])
-@pytest.mark.parametrize("k,n", [(1024, 3072), (3072, 1024), (1024, 2048), (1024, 151936), (32, 7), (2032, 40)])
+@pytest.mark.parametrize("k,n", [(1024, 3072), (3072, 1024), (1024, 2048), (1024, 151936), (1024, 40001), (32, 7),
+                                 (2032, 40)])
 def test_linear_fused_quant(gpu, m, k, n):
     """bh_linear_i8 on the decode path quantizes inside the GEMV: outputs (f32
     and bf16 with bias) and the sx / xq scratch it leaves must be exactly the
