@@ -183,10 +183,19 @@ def test_gemm_split_k(gpu, m, k, n):
     run_and_check(gpu, m, k, n, "dyn", seed=m + 5 * k + n, bias=True)
 
 
-def test_gemm_split_k_big_tiles(gpu):
-    # The DiT down projection: 150 tiles of 256x128 over 160 K stages, taken
-    # as 256x256 tiles split 3 ways over K.
-    run_and_check(gpu, 1152, 10240, 3840, "dyn", seed=77, bias=True, sample=300)
+@pytest.mark.parametrize("m,k,n", [(1152, 10240, 3840), (2048, 16384, 3072)])
+def test_gemm_split_k_big_tiles(gpu, m, k, n):
+    # 256x256 tiles split over K: the DiT down projection (150 tiles of
+    # 256x128 over 160 K stages, split 3 ways) and 192 tiles of 256x128 over
+    # 256 K stages (split 2 ways).
+    run_and_check(gpu, m, k, n, "dyn", seed=77 + m, bias=True, sample=300)
+
+
+@pytest.mark.parametrize("k,n", [(3840, 3840), (3840, 10240), (3840, 11520)])
+def test_gemm_dit_shapes(gpu, k, n):
+    # Config 4's other linears at M = 1152 (4.5 rows of 256-row tiles): the
+    # out projection on 256x128 tiles, FFN up and QKV on 256x256.
+    run_and_check(gpu, 1152, k, n, "dyn", seed=k + n, bias=True, sample=300)
 
 
 def test_static_scale_matmul_split_k(gpu):
