@@ -637,7 +637,22 @@ def cpu_baseline(budget_s):
     byts = sum(linear_bytes(m, k, n) for m in DECODE_M for k, n in DECODE_KN)
     return dict(value=round(byts / t / 1e9, 2), unit="GB/s", cores=threads, kind="port",
                 sample=f"full 16-linear decode sweep, {len(times)} runs, median {t * 1e3:.1f} ms per sweep",
-                step_ms=round(t * 1e3, 2))
+                step_ms=round(t * 1e3, 2), host=host_cpu())
+
+
+def host_cpu():
+    """The host the CPU baselines ran on: CPU model, logical CPUs, and the
+    CPUs this process may use."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
 
 
 def prefill_cpu_baseline(budget_s):
@@ -760,7 +775,7 @@ def main():
                      "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "gemv_i8_kernel", "avg_launch_us": round(d["gemv_mean_us"], 2),
                      "avg_algorithmic_bytes": round(d["gemv_mean_bytes"])},
-        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample", "host")},
         "decode_shapes_cold": res["shapes"],
         "config0_linear": res["config0"],
         "mfma_roof_probe_tops": roof,

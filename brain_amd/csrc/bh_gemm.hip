@@ -857,7 +857,9 @@ enum TileCfg {
     TILE_64x128 = 2,  // 64x128, 4 waves of 32x64, 4 stages
     TILE_64 = 3,      // 64x64, 4 waves of 32x32, 4 stages
     TILE_64_DEEP = 4,  // 64x64 with 8 stages in flight (long K on a few tiles)
-    TILE_256x128 = 5   // 256x128, 8 waves of 64x64, 4 stages
+    TILE_256x128 = 5,  // 256x128, 8 waves of 64x64, 4 stages
+    TILE_64_K128 = 6,     // 64x64, 8 stages of 128 K-bytes (what TILE_64_DEEP runs)
+    TILE_64x128_K128 = 7  // 64x128, 4 stages of 128 K-bytes (what TILE_64x128 runs)
 };
 
 struct TileChoice {
@@ -1007,13 +1009,30 @@ static int big_cfg() {
 }
 
 // The DMA kernel for every tile but 256x256.
+// The two small tiles that run long K chains on few CUs take 128-byte K
+// stages: half the barriers and waits per K byte, which is what a lone small
+// tile's stage time is made of (measured: 512x3072x1024 12.3 -> 10.7 us,
+// 2048x3072x1024 15.0 -> 14.1 us, Qwen3 prefill 1-3% faster; more stages of
+// 64 bytes instead, 16 in flight, measured slower). BH_GEMM_DK128=0 keeps
+// 64-byte stages, for measurements.
+static int dk128_env() {
+    static int v = env_int("BH_GEMM_DK128", 1);
+    return v;
+}
+
 template <int OUT, bool HAS_BIAS, bool STATIC, bool SPLITK>
 static hipError_t go_small(hipStream_t s, int cfg, const GemmArgs& a) {
+    if (dk128_env()) {
+        if (cfg == TILE_64_DEEP) cfg = TILE_64_K128;
+        if (cfg == TILE_64x128) cfg = TILE_64x128_K128;
+    }
     switch (cfg) {
         case TILE_64x128: return go_dma<64, 128, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
         case TILE_64: return go_dma<64, 64, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
         case TILE_64_DEEP: return go_dma<64, 64, 2, 2, 8, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
         case TILE_256x128: return go_dma<256, 128, 4, 2, 4, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
+        case TILE_64_K128: return go_dma<64, 64, 2, 2, 8, 128, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
+        case TILE_64x128_K128: return go_dma<64, 128, 2, 2, 4, 128, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
         default: return go_dma<128, 128, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
     }
 }
