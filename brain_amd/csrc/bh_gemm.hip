@@ -859,7 +859,8 @@ enum TileCfg {
     TILE_64_DEEP = 4,  // 64x64 with 8 stages in flight (long K on a few tiles)
     TILE_256x128 = 5,  // 256x128, 8 waves of 64x64, 4 stages
     TILE_64_K128 = 6,     // 64x64, 8 stages of 128 K-bytes (what TILE_64_DEEP runs)
-    TILE_64x128_K128 = 7  // 64x128, 4 stages of 128 K-bytes (what TILE_64x128 runs)
+    TILE_64x128_K128 = 7,  // 64x128, 4 stages of 128 K-bytes (what TILE_64x128 runs)
+    TILE_256x128_K128 = 8  // 256x128, 3 stages of 128 K-bytes (what TILE_256x128 runs)
 };
 
 struct TileChoice {
@@ -1009,12 +1010,14 @@ static int big_cfg() {
 }
 
 // The DMA kernel for every tile but 256x256.
-// The two small tiles that run long K chains on few CUs take 128-byte K
-// stages: half the barriers and waits per K byte, which is what a lone small
-// tile's stage time is made of (measured: 512x3072x1024 12.3 -> 10.7 us,
-// 2048x3072x1024 15.0 -> 14.1 us, Qwen3 prefill 1-3% faster; more stages of
-// 64 bytes instead, 16 in flight, measured slower). BH_GEMM_DK128=0 keeps
-// 64-byte stages, for measurements.
+// The small tiles that run long K chains on few CUs, and the 8-wave 256x128
+// tile, take 128-byte K stages: half the barriers and waits per K byte, which
+// is what a lone small tile's stage time is made of (measured: 512x3072x1024
+// 12.3 -> 10.7 us, 2048x3072x1024 15.0 -> 14.1 us, Qwen3 prefill 1-3%
+// faster; more stages of 64 bytes instead, 16 in flight, measured slower;
+// 256x128 in 3 stages of 128 bytes: 2048x4096x11008 118.8 -> 111.6 us,
+// 8192x3072x1024 35.0 -> 31.0 us; 128x128 mixed, so it keeps 64-byte
+// stages). BH_GEMM_DK128=0 keeps 64-byte stages, for measurements.
 static int dk128_env() {
     static int v = env_int("BH_GEMM_DK128", 1);
     return v;
@@ -1025,6 +1028,7 @@ static hipError_t go_small(hipStream_t s, int cfg, const GemmArgs& a) {
     if (dk128_env()) {
         if (cfg == TILE_64_DEEP) cfg = TILE_64_K128;
         if (cfg == TILE_64x128) cfg = TILE_64x128_K128;
+        if (cfg == TILE_256x128) cfg = TILE_256x128_K128;
     }
     switch (cfg) {
         case TILE_64x128: return go_dma<64, 128, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
@@ -1033,6 +1037,7 @@ static hipError_t go_small(hipStream_t s, int cfg, const GemmArgs& a) {
         case TILE_256x128: return go_dma<256, 128, 4, 2, 4, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
         case TILE_64_K128: return go_dma<64, 64, 2, 2, 8, 128, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
         case TILE_64x128_K128: return go_dma<64, 128, 2, 2, 4, 128, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
+        case TILE_256x128_K128: return go_dma<256, 128, 4, 2, 3, 128, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
         default: return go_dma<128, 128, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
     }
 }
