@@ -800,33 +800,63 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
 // ---------------------------------------------------------------- split-K reduction
 // out[r, c] = epilogue(sum_s ws[s][r][c]). VEC: four consecutive columns per
 // thread (n % 4 == 0 and the output aligned for a 4-element store).
-template <int OUT, bool HAS_BIAS, bool STATIC, bool VEC>
+// SN > 0: the split count at compile time, so every slab load (and the
+// row's scale, the columns' scales and bias) of a 4-column group issues before
+// the first add; SN = 0 reads S from the arguments.
+template <int OUT, bool HAS_BIAS, bool STATIC, bool VEC, int SN = 0>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a) {
-    const int n = a.n, S = a.splits;
+    const int n = a.n, S = SN > 0 ? SN : a.splits;
     const int64_t mn = (int64_t)a.m * n;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     if constexpr (VEC) {
         const v4i* ws = reinterpret_cast<const v4i*>(a.ws);
         const int64_t q4 = mn >> 2;
         for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < q4; q += stride) {
-            v4i acc = ws[q];
-            for (int sp = 1; sp < S; ++sp) {
-                const v4i v = ws[(int64_t)sp * q4 + q];
-                acc[0] += v[0]; acc[1] += v[1]; acc[2] += v[2]; acc[3] += v[3];
-            }
             const int64_t idx = q << 2;
             const int row = (int)(idx / n), col = (int)(idx - (int64_t)row * n);
+            v4i acc;
+            float sxm = 0.0f;
+            float4 swv = make_float4(0.f, 0.f, 0.f, 0.f), bv = make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (SN > 0) {
+                v4i v[SN];
+#pragma unroll
+                for (int sp = 0; sp < SN; ++sp) v[sp] = ws[(int64_t)sp * q4 + q];
+                if constexpr (OUT != OUT_I32 && !STATIC) {
+                    sxm = a.sx[row];
+                    swv = make_float4(a.sw[col], a.sw[col + 1], a.sw[col + 2], a.sw[col + 3]);
+                }
+                if constexpr (OUT != OUT_I32 && HAS_BIAS)
+                    bv = make_float4(a.bias[col], a.bias[col + 1], a.bias[col + 2], a.bias[col + 3]);
+                acc = v[0];
+#pragma unroll
+                for (int sp = 1; sp < SN; ++sp) {
+                    acc[0] += v[sp][0]; acc[1] += v[sp][1]; acc[2] += v[sp][2]; acc[3] += v[sp][3];
+                }
+            } else {
+                acc = ws[q];
+                for (int sp = 1; sp < S; ++sp) {
+                    const v4i v = ws[(int64_t)sp * q4 + q];
+                    acc[0] += v[0]; acc[1] += v[1]; acc[2] += v[2]; acc[3] += v[3];
+                }
+                if constexpr (OUT != OUT_I32 && !STATIC) {
+                    sxm = a.sx[row];
+                    swv = make_float4(a.sw[col], a.sw[col + 1], a.sw[col + 2], a.sw[col + 3]);
+                }
+                if constexpr (OUT != OUT_I32 && HAS_BIAS)
+                    bv = make_float4(a.bias[col], a.bias[col + 1], a.bias[col + 2], a.bias[col + 3]);
+            }
             if constexpr (OUT == OUT_I32) {
                 reinterpret_cast<v4i*>(a.out)[q] = acc;
             } else {
                 float f[4];
-                const float sxm = STATIC ? 0.0f : a.sx[row];
                 const bool off = gated_off(a, row);
+                const float sv[4] = {swv.x, swv.y, swv.z, swv.w};
+                const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     if constexpr (STATIC) f[e] = (float)acc[e] * (a.ssx * a.ssw);
-                    else f[e] = dequant(acc[e], sxm, a.sw[col + e]);
-                    if constexpr (HAS_BIAS) f[e] = f[e] + a.bias[col + e];
+                    else f[e] = dequant(acc[e], sxm, sv[e]);
+                    if constexpr (HAS_BIAS) f[e] = f[e] + bb[e];
                     if (off) f[e] = 0.0f;
                 }
                 if constexpr (OUT == OUT_F32)
@@ -1109,8 +1139,16 @@ static hipError_t run_gemm(hipStream_t s, bool al, bool dma, const TileChoice& t
     const bool vec = (a.n % 4) == 0 && (reinterpret_cast<uintptr_t>(a.out) & need) == 0;
     const int64_t work = vec ? mn / 4 : mn;
     const unsigned grid = (unsigned)std::min<int64_t>((work + 255) / 256, 256 * 16);
-    if (vec) splitk_reduce_kernel<OUT, HAS_BIAS, STATIC, true><<<grid, 256, 0, s>>>(a);
-    else splitk_reduce_kernel<OUT, HAS_BIAS, STATIC, false><<<grid, 256, 0, s>>>(a);
+    if (vec) {
+        switch (a.splits) {
+            case 2: splitk_reduce_kernel<OUT, HAS_BIAS, STATIC, true, 2><<<grid, 256, 0, s>>>(a); break;
+            case 3: splitk_reduce_kernel<OUT, HAS_BIAS, STATIC, true, 3><<<grid, 256, 0, s>>>(a); break;
+            case 4: splitk_reduce_kernel<OUT, HAS_BIAS, STATIC, true, 4><<<grid, 256, 0, s>>>(a); break;
+            default: splitk_reduce_kernel<OUT, HAS_BIAS, STATIC, true><<<grid, 256, 0, s>>>(a); break;
+        }
+    } else {
+        splitk_reduce_kernel<OUT, HAS_BIAS, STATIC, false><<<grid, 256, 0, s>>>(a);
+    }
     return hipGetLastError();
 }
 
