@@ -1104,21 +1104,29 @@ int launch_combine_quant(bh_qwen3* e, int rows, int splits) {
     return BH_OK;
 }
 
-// The fused producer + GEMV path: at most 4 rows (BH_QWEN3_FUSE_ROWS
-// overrides it for measurements). Every workgroup redoes the producer for
-// all rows, re-reading their inputs from L2 (at 8 rows 64 KB per workgroup
-// for the norm, 196 KB for the SwiGLU): at batch 8 that measured 15% slower
-// than the separate kernels even with all rows in one burst of loads, at
-// batch 1 10% faster. K a multiple of 16 up to 4096, and no measured
-// preference for the MFMA tile at this shape.
-bool fused_ok(bh_qwen3* e, int rows, int k, int n) {
-    (void)e;
-    static const int max_rows = [] {
-        const char* v = getenv("BH_QWEN3_FUSE_ROWS");
-        return v ? atoi(v) : 4;
-    }();
+// The fused producer + GEMV paths, up to 4 rows each. Every workgroup redoes
+// the producer for all rows, re-reading their inputs from L2 (for the RMSNorm
+// 2 x 4 KB per row, for the SwiGLU 24 KB per row). Measured at batch 8
+// (step time, HIP graph): the norm fused at 8 rows 1.317 ms per step against
+// 1.221 with the separate norm kernel, so both stay at 4 rows; at batch 1
+// fusing is 10% faster. BH_QWEN3_FUSE_ROWS / BH_QWEN3_FUSE_SWIGLU_ROWS
+// override the two limits for measurements. K a multiple of 16 up to 4096,
+// and no measured preference for the MFMA tile at this shape.
+static int env_rows(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v ? atoi(v) : dflt;
+}
+bool fused_ok(int rows, int k, int n, int max_rows) {
     if (rows < 1 || rows > max_rows || k % 16 != 0 || k > 4096) return false;
     return tuned_variant((uint32_t)rows, (uint32_t)n, (uint32_t)k) != BH_VARIANT_PACKED_INT8;
+}
+int fuse_norm_rows() {
+    static const int v = env_rows("BH_QWEN3_FUSE_ROWS", 4);
+    return v;
+}
+int fuse_swiglu_rows() {
+    static const int v = env_rows("BH_QWEN3_FUSE_SWIGLU_ROWS", 4);
+    return v;
 }
 
 // `splits`: key chunks of KCH covering the longest row of this launch (the
@@ -1150,8 +1158,9 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
         // Residual stream ping-pongs between res and res2 (two swaps per
         // layer): a fused producer's workgroup 0 writes the new residual while
         // other workgroups still read the old one.
-        const bool fuse = !e->nofuse && fused_ok(e, rows, d, (int)e->W) && fused_ok(e, rows, d, 2 * ff) &&
-                          fused_ok(e, rows, ff, d);
+        const bool fuse = !e->nofuse && fused_ok(rows, d, (int)e->W, fuse_norm_rows()) &&
+                          fused_ok(rows, d, 2 * ff, fuse_norm_rows());
+        const bool fuse_sw = !e->nofuse && fused_ok(rows, ff, d, fuse_swiglu_rows());
         if (fuse) {
             BH_HIP(launch_gemv_i8_pre(e->stream, 3, l == 0 ? tok : nullptr, e->emb, l == 0 ? nullptr : cur,
                                       l == 0 ? nullptr : e->proj, Ly.ln1, nxt, c.rms_eps, Ly.wqkv, Ly.sqkv, e->qkv,
@@ -1218,7 +1227,7 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
         // thread with the loads issued before the position read, which costs
         // less than a launch. With more rows each workgroup merges them one
         // after another (measured slower from 2 rows: batch 4 1.19 -> 1.43 ms).
-        if (fuse && rows == 1 && fused_ok(e, rows, (int)e->hq, d) && e->hq <= 2048) {
+        if (fuse && rows == 1 && fused_ok(rows, (int)e->hq, d, 1) && e->hq <= 2048) {
             // The merge of the chunks inside the output projection's prologue.
             BH_HIP(launch_gemv_i8_merge(e->stream, e->part_o, e->part_ml, e->cur_pos, nh, hd, splits, Ly.wo, Ly.so,
                                         e->proj, rows, (int)e->hq / 4, d),
@@ -1232,9 +1241,6 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
                                       Ly.sgu, e->gu, rows, d / 4, 2 * ff),
                    "fused norm + gate/up launch");
             std::swap(cur, nxt);
-            BH_HIP(launch_gemv_i8_pre(e->stream, 4, nullptr, nullptr, e->gu, nullptr, nullptr, nullptr, 0.0f, Ly.wdown,
-                                      Ly.sdown, e->proj, rows, ff / 4, d),
-                   "fused swiglu + down launch");
         } else {
             NormQuantArgs nb{};
             nb.a = cur;
@@ -1249,6 +1255,12 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
             BH_TRY(launch_norm_quant(e, nb, rows));
             std::swap(cur, nxt);
             BH_TRY(launch_linear(e, Ly.wgu, Ly.sgu, e->gu, rows, d, 2 * ff));
+        }
+        if (fuse_sw) {
+            BH_HIP(launch_gemv_i8_pre(e->stream, 4, nullptr, nullptr, e->gu, nullptr, nullptr, nullptr, 0.0f, Ly.wdown,
+                                      Ly.sdown, e->proj, rows, ff / 4, d),
+                   "fused swiglu + down launch");
+        } else {
             BH_TRY(launch_swiglu_quant(e, rows));
             BH_TRY(launch_linear(e, Ly.wdown, Ly.sdown, e->proj, rows, ff, d));
         }
