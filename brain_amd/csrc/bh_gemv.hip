@@ -127,13 +127,49 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
     }
     const int my_chunks = g0 < ngroups ? (nchunks - ks + KSPLIT - 1) / KSPLIT : 0;  // chunks ks + KSPLIT*j
 
-    // The first batch of weight loads goes out before the activation staging.
+    // The first batch of weight loads. Most launches issue it here, ahead of
+    // the activation or the prologue's inputs. The SwiGLU prologue (XMODE 4)
+    // issues it right after its own input loads and before their first use,
+    // so its long chain (its inputs come from L2, the weights from HBM) runs
+    // while the weights are in flight: vmcnt completes in order, so waiting
+    // for inputs issued after the weights waits for the weights too.
+    // Measured per launch: SwiGLU + down 8.56 -> 7.39 us at 4 rows, 5.44 ->
+    // 5.32 at 1 row; the same order made the norm (5.45 -> 5.64 us) and the
+    // merge (7.46 -> 8.15 us) slower, their chains being shorter than the
+    // head start the weights lose behind the inputs' load instructions.
     v4i wf[U][CG];
+    auto issue_w = [&]() {
+        if constexpr (XMODE != 4) {
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-        if (u < my_chunks)
+            for (int u = 0; u < U; ++u)
+                if (u < my_chunks)
 #pragma unroll
-            for (int c = 0; c < CG; ++c) wf[u][c] = load_k16<ALIGNED>(wp[c], (ks + KSPLIT * u) * 64 + ksub, kbytes);
+                    for (int c = 0; c < CG; ++c)
+                        wf[u][c] = load_k16<ALIGNED>(wp[c], (ks + KSPLIT * u) * 64 + ksub, kbytes);
+        } else {
+            // Unconditional, and with no masking (this mode needs K % 64 ==
+            // 0): slots past this wave's chunks reload its last one (never
+            // consumed). A load under a branch, or a select on its value,
+            // would leave the compiler unable to count it, and it would wait
+            // for all of them before the prologue's first use of its inputs.
+            // The scheduling barriers keep them after the prologue's loads
+            // and ahead of its arithmetic (the scheduler would otherwise
+            // interleave the independent loads).
+            // A wave that owns no chunk (ks >= nchunks when K has fewer
+            // chunks than the waves splitting it) reloads the row's last
+            // chunk, so no load leaves the row.
+            const int last = my_chunks > 0 ? my_chunks - 1 : 0;
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int c = 0; c < CG; ++c)
+                    wf[u][c] = *reinterpret_cast<const v4i*>(
+                        wp[c] + min(ks + KSPLIT * min(u, last), nchunks - 1) * 64 + ksub);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    if constexpr (XMODE != 4) issue_w();
 
     float* sxs = reinterpret_cast<float*>(xs + MT * 16 * xstride);  // XMODE 2-4: row scales
     if constexpr (XMODE == 3 || XMODE == 4) {
@@ -148,16 +184,25 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
         const int d = kbytes, d4 = d >> 2;
         const float4* g4 = reinterpret_cast<const float4*>(a.pre_a);
         const float4* u4 = g4 + d4;
-        float4 h[GX];
+        float4 h[GX], gv[GX], uv[GX];
         float am = 0.0f;
+        // Unconditional loads (groups past K read a clamped copy), then the
+        // weights, then the arithmetic.
+#pragma unroll
+        for (int gi = 0; gi < GX; ++gi) {
+            const int i = min((int)threadIdx.x + NTH * gi, d4 - 1);
+            gv[gi] = g4[i];
+            uv[gi] = u4[i];
+        }
+        issue_w();
 #pragma unroll
         for (int gi = 0; gi < GX; ++gi) {
             const int i = threadIdx.x + NTH * gi;
             h[gi] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (i < d4) {
-                const float4 gv = g4[i], uv = u4[i];
-                h[gi] = make_float4(gv.x / (1.0f + expf(-gv.x)) * uv.x, gv.y / (1.0f + expf(-gv.y)) * uv.y,
-                                    gv.z / (1.0f + expf(-gv.z)) * uv.z, gv.w / (1.0f + expf(-gv.w)) * uv.w);
+                const float4 g = gv[gi], u = uv[gi];
+                h[gi] = make_float4(g.x / (1.0f + expf(-g.x)) * u.x, g.y / (1.0f + expf(-g.y)) * u.y,
+                                    g.z / (1.0f + expf(-g.z)) * u.z, g.w / (1.0f + expf(-g.w)) * u.w);
                 am = fmaxf(am, fmaxf(fmaxf(fabsf(h[gi].x), fabsf(h[gi].y)), fmaxf(fabsf(h[gi].z), fabsf(h[gi].w))));
             }
         }
@@ -259,6 +304,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
                             v[j][g] = reinterpret_cast<const float4*>(a.pre_a + (size_t)rc[j] * 2 * d)[ic];
                             uv[j][g] = reinterpret_cast<const float4*>(a.pre_a + (size_t)rc[j] * 2 * d + d)[ic];
                         }
+                    if (r0 == 0) issue_w();
 #pragma unroll
                     for (int j = 0; j < RMAX; ++j)
 #pragma unroll
@@ -890,13 +936,14 @@ hipError_t launch_linear_i8_fused(hipStream_t s, const float* x, const uint32_t*
 
 // The decoder's fused producer + linear for m <= 16 rows, f32 out:
 // mode 3 = [residual add |] RMSNorm + quantize + GEMV, mode 4 = SwiGLU +
-// quantize + GEMV (K = the SwiGLU width, pre_a = [m, 2K]). K % 16 == 0,
-// K <= 4096. Returns hipErrorNotSupported outside those limits.
+// quantize + GEMV (K = the SwiGLU width, pre_a = [m, 2K]). K % 16 == 0 (64
+// for mode 4), K <= 4096. Returns hipErrorNotSupported outside those limits.
 hipError_t launch_gemv_i8_pre(hipStream_t s, int mode, const uint32_t* pre_tok, const float* pre_emb,
                               const float* pre_a, const float* pre_b, const float* pre_w, float* res_out, float eps,
                               const uint32_t* wq, const float* sw, float* out, int m, int kg, int n) {
     const int kbytes = kg * 4;
-    if (m < 1 || m > 16 || kbytes % 16 != 0 || kbytes > 4096 || (reinterpret_cast<uintptr_t>(wq) & 15u) != 0)
+    if (m < 1 || m > 16 || kbytes % 16 != 0 || kbytes < 16 || kbytes > 4096 || (mode == 4 && kbytes % 64 != 0) ||
+        (reinterpret_cast<uintptr_t>(wq) & 15u) != 0)
         return hipErrorNotSupported;
     GemvArgs a{nullptr, wq, nullptr, sw, nullptr, out, m, kg, n, nullptr, 0, 0, nullptr, nullptr, nullptr,
                pre_tok, pre_emb, pre_a, pre_b, pre_w, res_out, eps};
@@ -911,9 +958,10 @@ hipError_t launch_gemv_i8_pre(hipStream_t s, int mode, const uint32_t* pre_tok, 
         return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 32 + 1>(s, a);
     }
     if (mode == 4 && kbytes == 3072) {
-        if (rpt == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 16, 4, 8 + 3>(s, a);
-        if (rpt == 2) return gv_go<1, OUT_F32, false, true, 4, 1, 16, 4, 16 + 3>(s, a);
-        return gv_go<1, OUT_F32, false, true, 4, 1, 16, 4, 32 + 3>(s, a);
+        // 48 K-chunks over 16 waves: each wave's 3 chunks in one batch.
+        if (rpt == 1) return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 8 + 3>(s, a);
+        if (rpt == 2) return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 16 + 3>(s, a);
+        return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 32 + 3>(s, a);
     }
     if (mode == 3) {
         if (nchunks >= 32) return gv_go<1, OUT_F32, false, true, 4, 1, 16, 3>(s, a);

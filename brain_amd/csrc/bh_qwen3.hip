@@ -1110,8 +1110,9 @@ int launch_combine_quant(bh_qwen3* e, int rows, int splits) {
 // (step time, HIP graph): the norm fused at 8 rows 1.317 ms per step against
 // 1.221 with the separate norm kernel, so both stay at 4 rows; at batch 1
 // fusing is 10% faster. BH_QWEN3_FUSE_ROWS / BH_QWEN3_FUSE_SWIGLU_ROWS
-// override the two limits for measurements. K a multiple of 16 up to 4096,
-// and no measured preference for the MFMA tile at this shape.
+// override the two limits for measurements. K a multiple of 16 up to 4096
+// (64 for the SwiGLU), and no measured preference for the MFMA tile at this
+// shape.
 static int env_rows(const char* name, int dflt) {
     const char* v = getenv(name);
     return v ? atoi(v) : dflt;
@@ -1160,7 +1161,7 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
         // other workgroups still read the old one.
         const bool fuse = !e->nofuse && fused_ok(rows, d, (int)e->W, fuse_norm_rows()) &&
                           fused_ok(rows, d, 2 * ff, fuse_norm_rows());
-        const bool fuse_sw = !e->nofuse && fused_ok(rows, ff, d, fuse_swiglu_rows());
+        const bool fuse_sw = !e->nofuse && ff % 64 == 0 && fused_ok(rows, ff, d, fuse_swiglu_rows());
         if (fuse) {
             BH_HIP(launch_gemv_i8_pre(e->stream, 3, l == 0 ? tok : nullptr, e->emb, l == 0 ? nullptr : cur,
                                       l == 0 ? nullptr : e->proj, Ly.ln1, nxt, c.rms_eps, Ly.wqkv, Ly.sqkv, e->qkv,
