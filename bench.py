@@ -376,10 +376,12 @@ def mfma_roof(torch, lib, dev):
 
 
 def bench_w4a8(reps=20):
-    """W4A8 (matmul_q4_gemv / matmul_q4_dyn): the configs[1] decode shapes and
-    two prefill shapes with int4 weights, one HIP graph of `reps` launches
-    per shape (weights re-read from the Infinity Cache, so these are warm
-    numbers). Decode: GB/s over N*K/2 + 4N + M*K + 2*M*N; prefill: TOPS."""
+    """W4A8 (matmul_q4_gemv / matmul_q4_dyn): the configs[1] decode shapes at
+    M = 1 and 16 and two prefill shapes with int4 weights. Decode is measured
+    cold, like the int8 per-shape table: one graph of launches cycling over
+    weight copies that together exceed the Infinity Cache; GB/s over
+    N*K/2 + 4N + M*K + 2*M*N. Prefill: one HIP graph of `reps` launches on one
+    weight (as the int8 prefill sweep), TOPS."""
     import torch
     from brain_amd import ops
     dev = torch.device("cuda:0")
@@ -404,19 +406,31 @@ def bench_w4a8(reps=20):
         torch.cuda.synchronize()
         return (time.perf_counter() - t0) / reps
 
-    for m, (k, n) in [(m, kn) for kn in DECODE_KN for m in (1, 16)] + [(512, (4096, 11008)), (2048, (4096, 4096))]:
+    for m, (k, n) in [(m, kn) for kn in DECODE_KN for m in (1, 16)]:
+        xq = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=dev, generator=g).view(torch.int32)
+        copies = max(2, min(128, -(-(512 << 20) // (n * k // 2))))
+        ws = [torch.randint(-2**31, 2**31 - 1, (n, k // 8), dtype=torch.int32, device=dev, generator=g)
+              for _ in range(copies)]
+        sx = torch.rand(m, device=dev, generator=g)
+        sw = torch.rand(n, device=dev, generator=g) * 0.01
+        o = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+
+        def fn(w4):
+            return lambda: ops.matmul_q4(xq, w4, sx, sw, None, torch.bfloat16, "auto", out=o)
+        us = graph_per_launch_us(torch, [fn(w) for w in ws])
+        b = n * k // 2 + 4 * n + m * k + 2 * m * n
+        out["decode"].append({"m": m, "k": k, "n": n, "copies": copies, "us": round(us, 2),
+                              "gbs": round(b / us / 1e3, 1)})
+        del ws
+    for m, (k, n) in [(512, (4096, 11008)), (2048, (4096, 4096))]:
         xq = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=dev, generator=g).view(torch.int32)
         w4 = torch.randint(-2**31, 2**31 - 1, (n, k // 8), dtype=torch.int32, device=dev, generator=g)
         sx = torch.rand(m, device=dev, generator=g)
         sw = torch.rand(n, device=dev, generator=g) * 0.01
         o = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
         dt = timed(lambda: ops.matmul_q4(xq, w4, sx, sw, None, torch.bfloat16, "auto", out=o))
-        if m <= 32:
-            b = n * k // 2 + 4 * n + m * k + 2 * m * n
-            out["decode"].append({"m": m, "k": k, "n": n, "us": round(dt * 1e6, 2), "gbs": round(b / dt / 1e9, 1)})
-        else:
-            out["prefill"].append({"m": m, "k": k, "n": n, "us": round(dt * 1e6, 2),
-                                   "tops": round(2 * m * n * k / dt / 1e12, 1)})
+        out["prefill"].append({"m": m, "k": k, "n": n, "us": round(dt * 1e6, 2),
+                               "tops": round(2 * m * n * k / dt / 1e12, 1)})
     return out
 
 

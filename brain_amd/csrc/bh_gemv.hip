@@ -626,9 +626,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
 // Measured on MI355X (LM head, cold): two waves per SIMD (256 VGPRs, fewer
 // parked results) and non-temporal weight loads were both slower than this
 // form (one wave per SIMD, 288 VGPRs with the accumulation registers).
-template <int OUT, bool HAS_BIAS, int KB>
+// Q4: W4A8 weights (matmul_q4_gemv, crates/kernels/wgsl/matmul_q4_gemv.wgsl):
+// rows of KB/2 bytes, 8 int4 per u32 word; per 128-K chunk each lane loads 16
+// bytes of int4 (K 32q..32q+31 of its column, q = lane/16), unpacks them to
+// two int8 fragments and feeds two MFMAs against the activation bytes of the
+// same K (a permutation of K inside the chunk shared by both operands, so the
+// sum is exact; the same pairing as gemv_q4_kernel).
+template <int OUT, bool HAS_BIAS, int KB, bool Q4 = false>
 __global__ __launch_bounds__(256) void gemv_i8_stream_kernel(GemvArgs a, int groups_per_wave) {
-    constexpr int U = 16, kbytes = KB, nbatch = KB / 1024;
+    constexpr int U = Q4 ? 8 : 16, kbytes = KB, nbatch = KB / 1024;
+    constexpr int wbytes = Q4 ? KB / 2 : KB;  // weight bytes per row
     __shared__ __attribute__((aligned(16))) uint8_t xs[16 * (KB + 16)];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -656,7 +663,7 @@ __global__ __launch_bounds__(256) void gemv_i8_stream_kernel(GemvArgs a, int gro
             it.sw = OUT != OUT_I32 ? a.sw[r] : 0.0f;
             it.bias = HAS_BIAS ? a.bias[r] : 0.0f;
         }
-        const uint8_t* rp = reinterpret_cast<const uint8_t*>(a.wq) + (int64_t)r * kbytes + b * U * 64 + ksub;
+        const uint8_t* rp = reinterpret_cast<const uint8_t*>(a.wq) + (int64_t)r * wbytes + b * U * 64 + ksub;
 #pragma unroll
         for (int u = 0; u < U; ++u) it.w[u] = *reinterpret_cast<const v4i*>(rp + u * 64);
     };
@@ -694,7 +701,7 @@ __global__ __launch_bounds__(256) void gemv_i8_stream_kernel(GemvArgs a, int gro
     __syncthreads();
     if (items == 0) return;
 
-    const uint8_t* xrow = xs + (lane & 15) * xstride + ksub;
+    const uint8_t* xrow = xs + (lane & 15) * xstride + (Q4 ? 2 * ksub : ksub);
     v4i acc = {0, 0, 0, 0};
     // Results of the last npend groups (slot k = group i_last - k), not yet stored.
     constexpr int NPEND = 8;
@@ -727,11 +734,24 @@ __global__ __launch_bounds__(256) void gemv_i8_stream_kernel(GemvArgs a, int gro
     };
     auto consume = [&](const Item& it, int j) {
         const int i = j / nbatch, b = j - i * nbatch;
-        const uint8_t* xp = xrow + b * U * 64;
+        if constexpr (Q4) {
+            const uint8_t* xp = xrow + b * U * 128;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const v4i xf = *reinterpret_cast<const v4i*>(xp + u * 64);
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(xf, it.w[u], acc, 0, 0, 0);
+            for (int u = 0; u < U; ++u) {
+                v4i b0, b1;
+                unpack_q4x4(it.w[u], b0, b1);
+                const v4i x0 = *reinterpret_cast<const v4i*>(xp + u * 128);
+                const v4i x1 = *reinterpret_cast<const v4i*>(xp + u * 128 + 16);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, b0, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, b1, acc, 0, 0, 0);
+            }
+        } else {
+            const uint8_t* xp = xrow + b * U * 64;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const v4i xf = *reinterpret_cast<const v4i*>(xp + u * 64);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(xf, it.w[u], acc, 0, 0, 0);
+            }
         }
         if (b != nbatch - 1) return;
         // Park the group's results; the stores go out in bursts of NPEND
@@ -796,7 +816,7 @@ static hipError_t gv_go(hipStream_t s, const GemvArgs& a) {
 
 // The streaming wide-N kernel: as many waves as can be resident (so the
 // whole grid is one round), each owning an equal share of the column groups.
-template <int OUT, bool HAS_BIAS, int KB>
+template <int OUT, bool HAS_BIAS, int KB, bool Q4 = false>
 static hipError_t gv_stream_kb(hipStream_t s, const GemvArgs& a) {
     // Resident waves (the whole grid is one round).
     static const int slots = [] {
@@ -804,7 +824,8 @@ static hipError_t gv_stream_kb(hipStream_t s, const GemvArgs& a) {
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
             cus = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_i8_stream_kernel<OUT, HAS_BIAS, KB>, 256, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_i8_stream_kernel<OUT, HAS_BIAS, KB, Q4>, 256,
+                                                         0) !=
                 hipSuccess || per_cu < 1)
             per_cu = 1;
         return cus * per_cu * 4;
@@ -812,7 +833,7 @@ static hipError_t gv_stream_kb(hipStream_t s, const GemvArgs& a) {
     const int ngroups = (a.n + 15) / 16;
     const int gpw = (ngroups + slots - 1) / slots;  // groups per wave
     const int waves = (ngroups + gpw - 1) / gpw;    // balanced: every wave gpw or gpw-1 groups
-    gemv_i8_stream_kernel<OUT, HAS_BIAS, KB><<<(waves + 3) / 4, 256, 0, s>>>(a, gpw);
+    gemv_i8_stream_kernel<OUT, HAS_BIAS, KB, Q4><<<(waves + 3) / 4, 256, 0, s>>>(a, gpw);
     return hipGetLastError();
 }
 
@@ -886,6 +907,22 @@ static hipError_t gv_out(hipStream_t s, bool aligned, int out_dtype, const GemvA
     }
     if (a.bias) return gv_align<MT, OUT_BF16, true>(s, aligned, a);
     return gv_align<MT, OUT_BF16, false>(s, aligned, a);
+}
+
+// The W4A8 LM head on the streaming kernel: K = 1024, m <= 16, wide N (at
+// least 1024 column groups), 16-byte aligned operands; hipErrorNotSupported
+// otherwise (the caller keeps its own GEMV).
+hipError_t launch_gemv_q4_stream(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
+                                 const float* sw, const float* bias, void* out, int out_dtype, int m, int k, int n) {
+    const uintptr_t al = reinterpret_cast<uintptr_t>(xq) | reinterpret_cast<uintptr_t>(wq);
+    if (k != 1024 || m < 1 || m > 16 || (n + 15) / 16 < 1024 || (al & 15u) != 0 || gv_cfg() == 9)
+        return hipErrorNotSupported;
+    GemvArgs a{xq, wq, sx, sw, bias, out, m, k / 4, n, nullptr, 0, 0, nullptr, nullptr, nullptr,
+               nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0.0f};
+    if (out_dtype == OUT_I32) return gv_stream_kb<OUT_I32, false, 1024, true>(s, a);
+    if (out_dtype == OUT_F32)
+        return bias ? gv_stream_kb<OUT_F32, true, 1024, true>(s, a) : gv_stream_kb<OUT_F32, false, 1024, true>(s, a);
+    return bias ? gv_stream_kb<OUT_BF16, true, 1024, true>(s, a) : gv_stream_kb<OUT_BF16, false, 1024, true>(s, a);
 }
 
 // Preconditions are checked by the C-ABI layer: 1 <= m <= 32, kg >= 0, n >= 1.

@@ -18,6 +18,9 @@
 
 namespace bh {
 
+hipError_t launch_gemv_q4_stream(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
+                                 const float* sw, const float* bias, void* out, int out_dtype, int m, int k, int n);
+
 struct GemvQ4Args {
     const uint32_t* xq;
     const uint32_t* wq;
@@ -162,6 +165,13 @@ static hipError_t q4_out(hipStream_t s, bool aligned, int out_dtype, const GemvQ
 
 hipError_t launch_gemv_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
                           const float* bias, void* out, int out_dtype, int m, int k, int n) {
+    // Wide N at K = 1024 (the LM head): the streaming kernel (activation
+    // staged once per workgroup in LDS, each wave streaming many column
+    // groups), as for int8.
+    if (m <= 16 && (n + 15) / 16 >= 1024 && k == 1024) {
+        const hipError_t e = launch_gemv_q4_stream(s, xq, wq, sx, sw, bias, out, out_dtype, m, k, n);
+        if (e != hipErrorNotSupported) return e;
+    }
     GemvQ4Args a{xq, wq, sx, sw, bias, out, m, k, n};
     // Aligned loads need whole 16-byte pieces in every row of both operands.
     const bool aligned = (k % 32) == 0 && ((reinterpret_cast<uintptr_t>(xq) | reinterpret_cast<uintptr_t>(wq)) & 15u) == 0;

@@ -61,6 +61,14 @@ def test_q4_gemv_decode_shapes(gpu, m, k, n):
     check(gpu, m, k, n, "gemv", seed=m * 7 + k + n, sample=400 if n > 20000 else None)
 
 
+@pytest.mark.parametrize("m,n", [(1, 16384), (5, 16390), (16, 40001), (3, 151936)])
+def test_q4_gemv_wide_n_streaming(gpu, m, n):
+    # Wide N at K = 1024 takes the streaming kernel (the activation staged
+    # once per workgroup, each wave streaming many column groups): ragged N,
+    # row counts that leave the 16-row tile partly empty.
+    check(gpu, m, 1024, n, "gemv", seed=m + n, sample=300 if n > 20000 else None)
+
+
 @pytest.mark.parametrize("m,k,n", [(1, 8, 1), (3, 24, 17), (5, 136, 33), (2, 1000, 40), (32, 4104, 64)])
 def test_q4_gemv_edges(gpu, m, k, n):
     check(gpu, m, k, n, "gemv", seed=m + k + n)
