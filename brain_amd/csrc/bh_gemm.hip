@@ -83,7 +83,13 @@ struct GemmArgs {
     // is +0 when gate[r * gate_stride + gate_col] <= 0.
     const float* gate;
     int gate_stride, gate_col;
+    // Output row stride in elements (0: n). A launch over a column range of
+    // a wider output (the column split of launch_gemm_i8) writes row r at
+    // out + r * ldo; the split-K slabs stay compact ([S][m][n]).
+    int ldo = 0;
 };
+
+__host__ __device__ __forceinline__ int64_t out_ld(const GemmArgs& a) { return a.ldo ? a.ldo : a.n; }
 
 __device__ __forceinline__ bool gated_off(const GemmArgs& a, int row) {
     return a.gate && a.gate[(int64_t)row * a.gate_stride + a.gate_col] <= 0.0f;
@@ -113,7 +119,7 @@ __device__ __forceinline__ bool gated_tile_skipped(const GemmArgs& a, int row0, 
 // One output element through the epilogue.
 template <int OUT, bool HAS_BIAS, bool STATIC>
 __device__ __forceinline__ void emit(const GemmArgs& a, int row, int col, int acc, float sxm, float swn, float bn) {
-    const int64_t idx = (int64_t)row * a.n + col;
+    const int64_t idx = (int64_t)row * out_ld(a) + col;
     if constexpr (OUT == OUT_I32) {
         reinterpret_cast<int*>(a.out)[idx] = acc;
     } else {
@@ -261,7 +267,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_kernel(GemmArgs a) {
     // Split-K: this workgroup's partial sums go raw to its own slab of the
     // workspace (the kernel is instantiated with OUT_I32 for it).
     if constexpr (SPLITK)
-        if (S > 1) a.out = a.ws + (int64_t)split * m * n;
+        if (S > 1) {
+            a.out = a.ws + (int64_t)split * m * n;
+            a.ldo = 0;
+        }
 
     float swv[C::FN], bv[C::FN];
 #pragma unroll
@@ -637,7 +646,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
     const int cbase = col0 + wn * C::WTN + 4 * (lane >> 5);
 
     if constexpr (SPLITK)
-        if (S > 1) a.out = a.ws + (int64_t)split * m * n;  // raw partials to this split's slab
+        if (S > 1) {
+            a.out = a.ws + (int64_t)split * m * n;  // raw partials to this split's (compact) slab
+            a.ldo = 0;
+        }
 
     if constexpr (EP_COLS) {
         if (t < BN) {
@@ -669,7 +681,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
         constexpr int EP_CPR = C::WTN * ESZ / 16;  // 16-byte chunks per tile row
         static_assert(WM * WN * EP_REGION <= STAGES * C::STAGE, "epilogue staging fits in the stage buffers");
         static_assert((32 * EP_CPR) % 64 == 0, "whole copy-out passes");
-        const bool staged = (n % 8) == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15u) == 0;
+        const bool staged = (n % 8) == 0 && (out_ld(a) % 8) == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15u) == 0;
         if (staged) {
             uint8_t* reg = lds + wave * EP_REGION;
             const int lrow = lane & 31;
@@ -728,7 +740,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
                     const v4i v = *reinterpret_cast<const v4i*>(reg + r * EP_PITCH + c * 16);
                     const int grow = wrow0 + i * 32 + r, gcol = wcol0 + c * (16 / ESZ);
                     if (grow < m && gcol < n)
-                        *reinterpret_cast<v4i*>(reinterpret_cast<uint8_t*>(a.out) + ((int64_t)grow * n + gcol) * ESZ) = v;
+                        *reinterpret_cast<v4i*>(reinterpret_cast<uint8_t*>(a.out) + ((int64_t)grow * out_ld(a) + gcol) * ESZ) = v;
                 }
                 __builtin_amdgcn_s_waitcnt(0xC07F);
                 __builtin_amdgcn_wave_barrier();
@@ -740,7 +752,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
     // Direct epilogue: four consecutive columns per (fragment, e/4) group,
     // stored as one vector when n % 4 == 0 and the output is aligned for it
     // (a step_sliced word offset may break that), else element by element.
-    const bool vec_ok = (n % 4) == 0 && (reinterpret_cast<uintptr_t>(a.out) & (OUT == OUT_BF16 ? 7u : 15u)) == 0;
+    const bool vec_ok = (n % 4) == 0 && (out_ld(a) % 4) == 0 &&
+                        (reinterpret_cast<uintptr_t>(a.out) & (OUT == OUT_BF16 ? 7u : 15u)) == 0;
 #pragma unroll
     for (int j = 0; j < C::FN; ++j)
 #pragma unroll
@@ -775,7 +788,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
                         if (off) f[q] = 0.0f;
                     }
                 }
-                const int64_t idx = (int64_t)row * n + col;
+                const int64_t idx = (int64_t)row * out_ld(a) + col;
                 if (vec_ok && col + 3 < n) {
                     if constexpr (OUT == OUT_I32)
                         *reinterpret_cast<v4i*>(reinterpret_cast<int*>(a.out) + idx) = v4i{v[0], v[1], v[2], v[3]};
@@ -845,8 +858,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a) {
                 if constexpr (OUT != OUT_I32 && HAS_BIAS)
                     bv = make_float4(a.bias[col], a.bias[col + 1], a.bias[col + 2], a.bias[col + 3]);
             }
+            const int64_t o4 = ((int64_t)row * out_ld(a) + col) >> 2;  // output index / 4 (ldo % 4 == 0)
             if constexpr (OUT == OUT_I32) {
-                reinterpret_cast<v4i*>(a.out)[q] = acc;
+                reinterpret_cast<v4i*>(a.out)[o4] = acc;
             } else {
                 float f[4];
                 const bool off = gated_off(a, row);
@@ -860,9 +874,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a) {
                     if (off) f[e] = 0.0f;
                 }
                 if constexpr (OUT == OUT_F32)
-                    reinterpret_cast<float4*>(a.out)[q] = make_float4(f[0], f[1], f[2], f[3]);
+                    reinterpret_cast<float4*>(a.out)[o4] = make_float4(f[0], f[1], f[2], f[3]);
                 else
-                    reinterpret_cast<uint2*>(a.out)[q] = make_uint2(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]));
+                    reinterpret_cast<uint2*>(a.out)[o4] = make_uint2(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]));
             }
         }
     } else {
@@ -1103,8 +1117,14 @@ static inline bool gemm_aligned(const void* xq, const void* wq, int kg) {
 int* splitk_workspace(hipStream_t s, size_t ints, hipError_t* err, int slot = 0);
 
 // Workspace elements the GEMM needs for this shape (0 = no split-K).
+static int column_split(int m, int kg, int n, const TileChoice& tc, bool dma);
+
 size_t gemm_workspace_ints(int m, int kg, int n) {
     const TileChoice tc = choose_tiles(m, kg, n);
+    if (const int n_main = column_split(m, kg, n, tc, (kg * 4) % 128 == 0)) {
+        const TileChoice tt = choose_tiles(m, kg, n - n_main);  // the column-split tail's own GEMM
+        return tt.splits > 1 ? (size_t)tt.splits * m * (n - n_main) : 0;
+    }
     return tc.splits > 1 ? (size_t)tc.splits * m * n : 0;
 }
 
@@ -1136,7 +1156,7 @@ static hipError_t run_gemm(hipStream_t s, bool al, bool dma, const TileChoice& t
     if (err != hipSuccess) return err;
     const int64_t mn = (int64_t)a.m * a.n;
     const uintptr_t need = OUT == OUT_BF16 ? 7u : 15u;
-    const bool vec = (a.n % 4) == 0 && (reinterpret_cast<uintptr_t>(a.out) & need) == 0;
+    const bool vec = (a.n % 4) == 0 && (out_ld(a) % 4) == 0 && (reinterpret_cast<uintptr_t>(a.out) & need) == 0;
     const int64_t work = vec ? mn / 4 : mn;
     const unsigned grid = (unsigned)std::min<int64_t>((work + 255) / 256, 256 * 16);
     if (vec) {
@@ -1152,12 +1172,67 @@ static hipError_t run_gemm(hipStream_t s, bool al, bool dma, const TileChoice& t
     return hipGetLastError();
 }
 
+// Column split of a 256x256 grid whose last round would run mostly empty
+// (e.g. 8192x4096x11008: 1376 tiles, 5.4 rounds of 256 CUs): the first
+// n_main columns as whole rounds of 256x256 tiles, the rest as its own GEMM
+// with its own tile choice (there 768 columns, one round of 192 256x128
+// tiles at about half a 256x256 round's cost), when the per-round cost model
+// of choose_tiles says the pair finishes first. Returns n_main, or 0.
+static int column_split(int m, int kg, int n, const TileChoice& tc, bool dma) {
+    if (!dma || tc.cfg != TILE_256 || tc.splits != 1 || tile_env() >= 0 || splitk_env() > 0 || big_cfg() != 0)
+        return 0;
+    constexpr long CUS = 256;
+    const long tm = (m + 255) / 256, tn = (n + 255) / 256;
+    const long rounds = (tm * tn + CUS - 1) / CUS;
+    if (rounds < 2 || (tm * tn) % CUS == 0) return 0;
+    long g = CUS, t = tm;  // gcd(tm, CUS): tile columns per whole number of rounds = CUS / gcd
+    while (t) {
+        const long r = g % t;
+        g = t;
+        t = r;
+    }
+    const long step = CUS / g;
+    const long c_main = (tn - 1) / step * step;  // whole rounds, at least one column left over
+    if (c_main <= 0) return 0;
+    const int n_main = (int)(c_main * 256), n_tail = n - n_main;
+    const long t2x1 = tm * ((n_tail + 127) / 128), t128 = ((m + 127) / 128) * ((n_tail + 127) / 128);
+    const double tail = std::min({4.0 * (double)((tm * ((n_tail + 255) / 256) + CUS - 1) / CUS),
+                                  2.2 * (double)((t2x1 + CUS - 1) / CUS), 1.4 * (double)((t128 + CUS - 1) / CUS)});
+    const double cost = 4.0 * (double)(tm * c_main / CUS) + tail + 0.25;  // 0.25: the second launch
+    return cost < 4.0 * (double)rounds ? n_main : 0;
+}
+
 hipError_t launch_gemm_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n) {
     GemmArgs a{xq, wq, sx, sw, bias, out, m, kg, n, 0.f, 0.f, 1, nullptr};
     const bool al = gemm_aligned(xq, wq, kg);
     const bool dma = al && ((kg * 4) % 128 == 0);
     const TileChoice tc = choose_tiles(m, kg, n);
+    if (const int n_main = column_split(m, kg, n, tc, dma)) {
+        const size_t esz = out_dtype == OUT_BF16 ? 2 : 4;
+        GemmArgs t = a;
+        t.n = n - n_main;
+        t.ldo = n;
+        t.wq = wq + (size_t)n_main * kg;
+        t.sw = sw + n_main;
+        t.bias = bias ? bias + n_main : nullptr;
+        t.out = static_cast<uint8_t*>(out) + (size_t)n_main * esz;
+        const TileChoice tt = choose_tiles(m, kg, t.n);
+        a.n = n_main;
+        a.ldo = n;
+        hipError_t e;
+        if (out_dtype == OUT_I32) e = run_gemm<OUT_I32, false, false>(s, al, dma, tc, a);
+        else if (out_dtype == OUT_F32) e = bias ? run_gemm<OUT_F32, true, false>(s, al, dma, tc, a)
+                                                : run_gemm<OUT_F32, false, false>(s, al, dma, tc, a);
+        else e = bias ? run_gemm<OUT_BF16, true, false>(s, al, dma, tc, a) : run_gemm<OUT_BF16, false, false>(s, al, dma, tc, a);
+        if (e != hipSuccess) return e;
+        const bool tal = gemm_aligned(xq, t.wq, kg);
+        const bool tdma = tal && ((kg * 4) % 128 == 0);
+        if (out_dtype == OUT_I32) return run_gemm<OUT_I32, false, false>(s, tal, tdma, tt, t);
+        if (out_dtype == OUT_F32) return bias ? run_gemm<OUT_F32, true, false>(s, tal, tdma, tt, t)
+                                              : run_gemm<OUT_F32, false, false>(s, tal, tdma, tt, t);
+        return bias ? run_gemm<OUT_BF16, true, false>(s, tal, tdma, tt, t) : run_gemm<OUT_BF16, false, false>(s, tal, tdma, tt, t);
+    }
     if (out_dtype == OUT_I32) return run_gemm<OUT_I32, false, false>(s, al, dma, tc, a);
     if (out_dtype == OUT_F32) {
         if (bias) return run_gemm<OUT_F32, true, false>(s, al, dma, tc, a);

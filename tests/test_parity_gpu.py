@@ -191,6 +191,15 @@ def test_gemm_split_k_big_tiles(gpu, m, k, n):
     run_and_check(gpu, m, k, n, "dyn", seed=77 + m, bias=True, sample=300)
 
 
+@pytest.mark.parametrize("n", [11008, 10995])
+def test_gemm_column_split(gpu, n):
+    # 32 x 43 tiles of 256x256 would be 5.4 rounds of 256 CUs: the first
+    # 10240 columns run as 5 whole rounds, the rest as a second GEMM writing
+    # into the same rows (output row stride n, its own tile choice). An odd
+    # width takes the per-element stores.
+    run_and_check(gpu, 8192, 1024, n, "dyn", seed=n, bias=True, sample=300)
+
+
 @pytest.mark.parametrize("k,n", [(3840, 3840), (3840, 10240), (3840, 11520)])
 def test_gemm_dit_shapes(gpu, k, n):
     # Config 4's other linears at M = 1152 (4.5 rows of 256-row tiles): the
