@@ -1275,8 +1275,9 @@ static int* scratch_ptr(hipError_t* err) {
 
 size_t noalloc_scratch_bytes() { return NOALLOC_SCRATCH_BYTES; }
 
-// bh_matmul_i8_dyn without allocation: the same kernels and launch choice;
-// the split-K slabs go to the fixed scratch. *need_bytes reports the slab
+// bh_matmul_i8_dyn without allocation: the same kernels and tile choice
+// (one launch over all columns, without launch_gemm_i8's column split; the
+// results are the same bits); the split-K slabs go to the fixed scratch. *need_bytes reports the slab
 // bytes the shape needs (0 when it does not split K); hipErrorInvalidValue
 // when that exceeds the scratch.
 hipError_t launch_gemm_i8_noalloc(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
