@@ -27,6 +27,7 @@ import json
 import os
 import sys
 import time
+import traceback
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
@@ -735,26 +736,37 @@ def main():
         sets = make_decode_set(torch, dev, gen)
         res["decode"] = bench_decode(torch, lib, sets, args.steps, args.warmup, gemv_only=args.only == "gemv")
         del sets
+    def leg(key, fn):
+        # A secondary leg that raises is recorded as such, so the line (and
+        # the decode measurement it carries) still prints.
+        try:
+            res[key] = fn()
+        except Exception as e:  # noqa: BLE001 - reported in the line and on stderr
+            traceback.print_exc()
+            res[key] = {"error": f"{type(e).__name__}: {e}"}
+
     if args.only in ("", "shapes"):
-        res["shapes"] = bench_decode_shapes(torch, lib, dev, gen)
+        leg("shapes", lambda: bench_decode_shapes(torch, lib, dev, gen))
     if args.only in ("", "config0"):
-        res["config0"] = bench_config0(torch, lib, dev, gen, cpu=not args.no_cpu)
+        leg("config0", lambda: bench_config0(torch, lib, dev, gen, cpu=not args.no_cpu))
     if args.only in ("", "prefill") and not args.no_prefill:
-        res["prefill"] = bench_prefill(torch, lib, dev, gen, args.prefill_reps)
+        leg("prefill", lambda: bench_prefill(torch, lib, dev, gen, args.prefill_reps))
     if args.only in ("", "quant") and not args.no_quant:
-        res["quant"] = bench_quant()
+        leg("quant", bench_quant)
     if args.only in ("", "qwen3") and not args.no_qwen3:
-        res["qwen3"] = bench_qwen3(cpu=not args.no_cpu)
+        leg("qwen3", lambda: bench_qwen3(cpu=not args.no_cpu))
     if args.only in ("", "dit") and not args.no_dit:
-        res["dit"] = bench_dit()
+        leg("dit", bench_dit)
     if args.only in ("", "w4a8") and not args.no_w4a8:
-        res["w4a8"] = bench_w4a8()
+        leg("w4a8", bench_w4a8)
     if args.only:
         print(json.dumps(res))
         return
     roof = mfma_roof(torch, lib, dev)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
-    pcpu = None if args.no_cpu or "prefill" not in res else prefill_cpu_baseline(min(args.cpu_seconds, 10.0))
+    pcpu = None
+    if not args.no_cpu and "prefill" in res and "error" not in res["prefill"]:
+        pcpu = prefill_cpu_baseline(min(args.cpu_seconds, 10.0))
 
     d = res["decode"]
     value = d["step_bytes"] / (d["step_ms"] * 1e-3) / 1e9
@@ -796,7 +808,7 @@ def main():
     }
     if "prefill" in res:
         line["prefill"] = res["prefill"]
-        if pcpu is not None:
+        if pcpu is not None:  # (the prefill leg succeeded)
             line["prefill_cpu_baseline"] = pcpu
             g = [r for r in res["prefill"]["shapes"] if (r["m"], r["k"], r["n"]) == (512, 1024, 3072)]
             if g:
