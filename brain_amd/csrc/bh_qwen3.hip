@@ -294,6 +294,72 @@ __device__ __forceinline__ void rope_head(const RopeArgs& p, const float* src, c
     }
 }
 
+// rope_head split in two for the decode attention launch: the loads (every
+// one unconditional: lanes past half the head repeat its last element and
+// are zeroed by rope_apply; a missing norm table reads the row instead, and
+// the value head reads the first (cos, sin) row) so they can go out ahead of
+// the cache reads, then the same arithmetic in the same order.
+struct RopeIn {
+    float y0[2], y1[2], w0[2], w1[2];
+    float2 cs[2];
+};
+__device__ __forceinline__ void rope_load(const RopeArgs& p, const float* src, const float* nw, bool rot, uint32_t pos,
+                                          int lane, RopeIn& in) {
+    const int half = p.hd >> 1;
+    const float* w = (rot && p.qk_norm) ? nw : src;
+    const size_t cs_row = rot ? (size_t)pos * half : 0;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int m = min(lane + 64 * u, half - 1);
+        in.y0[u] = src[m];
+        in.y1[u] = src[m + half];
+        in.w0[u] = w[m];
+        in.w1[u] = w[m + half];
+        in.cs[u] = p.cs[cs_row + m];
+    }
+}
+__device__ __forceinline__ void rope_apply(const RopeArgs& p, bool rot, int lane, const RopeIn& in, float (&y0)[2],
+                                           float (&y1)[2]) {
+    const int half = p.hd >> 1;
+    const bool norm = rot && p.qk_norm;
+    float ss = 0.0f, w0[2] = {0.0f, 0.0f}, w1[2] = {0.0f, 0.0f};
+    float2 cs[2] = {make_float2(1.0f, 0.0f), make_float2(1.0f, 0.0f)};
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int m = lane + 64 * u;
+        y0[u] = y1[u] = 0.0f;
+        if (m < half) {
+            y0[u] = in.y0[u];
+            y1[u] = in.y1[u];
+            if (norm) {
+                w0[u] = in.w0[u];
+                w1[u] = in.w1[u];
+            }
+            if (rot) cs[u] = in.cs[u];
+            ss += y0[u] * y0[u] + y1[u] * y1[u];
+        }
+    }
+    if (!rot) return;
+    float inv = 1.0f;
+    if (p.qk_norm) {
+        ss = wave_sum(ss);
+        inv = 1.0f / sqrtf(ss / (float)p.hd + p.eps);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int m = lane + 64 * u;
+        if (m >= half) continue;
+        float a = y0[u], b = y1[u];
+        if (p.qk_norm) {
+            a = a * inv * w0[u];
+            b = b * inv * w1[u];
+        }
+        const float c = cs[u].x, s = cs[u].y;
+        y0[u] = a * c - b * s;
+        y1[u] = b * c + a * s;
+    }
+}
+
 // Appends one key or value head at cache slot `tok`: f32 as is, or (KV8)
 // int8 codes with one scale per (token, kv head), min(max|x|, clip) / 127
 // (1 when that is 0), as paged_kv_append_i8_clipped_batched.wgsl. With KV8
@@ -496,13 +562,35 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     // Decode (ROPE): the chunk's addresses do not depend on the row's
     // position, so its reads go out before the position arrives, over every
     // key slot of the chunk inside the cache.
+    // One rotated head per wave (the group's query heads, the new key and
+    // value: G + 2 <= 4): its loads go out first, ahead of the cache reads,
+    // so the rotation runs while those are in flight (vmcnt completes in
+    // order: a rotation waiting on loads issued after the cache reads would
+    // wait for the cache reads too).
+    // The row's position is read once, here, ahead of the cache reads (a
+    // scalar load; read again after the DMA's memory clobber it would be a
+    // vector load, and waiting for it would wait for every cache read).
+    const bool one_head = ROPE && G + 2 <= RT / 64;
+    RopeIn rin;
+    uint32_t pos_r = 0;
     if constexpr (ROPE) {
+        pos_r = p.pos[r];
+        if (one_head) {
+            const int wave = tid >> 6, lane = tid & 63;
+            const RopeArgs& ro = p.ro;
+            const uint32_t pos = pos_r;
+            const float* row = ro.qkv + (size_t)r * (ro.hq + 2 * ro.hkv);
+            const int h = min(wave, G + 1);
+            const float* src = h < G ? row + (size_t)(kh * G + h) * p.hd
+                                     : row + ro.hq + (h == G ? 0 : ro.hkv) + kh * p.hd;
+            rope_load(ro, src, h < G ? ro.qn : ro.kn, h <= G, pos, lane, rin);
+        }
         load_chunk(min(KCH, p.max_seq - j0));
         // Keeps the loads above the early exit below (the compiler would
         // otherwise sink them past it, behind the position's load).
         asm volatile("" ::: "memory");
     }
-    const int t = (int)p.pos[r] + 1;
+    const int t = (int)(ROPE ? pos_r : p.pos[r]) + 1;
     if (j0 >= t) {
         // A chunk past the row: nothing to do, but its V staging loads still
         // write this workgroup's LDS, so they land before the workgroup ends
@@ -514,28 +602,23 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     const bool last = ROPE && j0 + n == t;  // this chunk ends at the new key
     const int nc = last ? n - 1 : n;        // keys read from the cache
     if constexpr (!ROPE) load_chunk(nc);
-    // Keys past the cached ones contribute zeros.
-#pragma unroll
-    for (int u = 0; u < KP; ++u) {
-        const int c = l8 * 4 + 32 * u;
-        if constexpr (KV8) kv[u] = i8x4(k8[u]);
-        if (kk >= nc || c >= p.hd) kv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
     if constexpr (ROPE) {
         const int wave = tid >> 6, lane = tid & 63, half = p.hd >> 1;
         const RopeArgs& ro = p.ro;
-        const uint32_t pos = p.pos[r];
+        const uint32_t pos = pos_r;
         const float* row = ro.qkv + (size_t)r * (ro.hq + 2 * ro.hkv);
         for (int h = wave; h < G + 2; h += RT / 64) {
             if (h >= G && !last) continue;
             float y0[2], y1[2];
             float* dst;
             if (h < G) {
-                rope_head(ro, row + (size_t)(kh * G + h) * p.hd, ro.qn, true, pos, lane, y0, y1);
+                if (one_head) rope_apply(ro, true, lane, rin, y0, y1);
+                else rope_head(ro, row + (size_t)(kh * G + h) * p.hd, ro.qn, true, pos, lane, y0, y1);
                 dst = qs + h * p.hd;
             } else {
                 const bool is_k = h == G;
-                rope_head(ro, row + ro.hq + (is_k ? 0 : ro.hkv) + kh * p.hd, ro.kn, is_k, pos, lane, y0, y1);
+                if (one_head) rope_apply(ro, is_k, lane, rin, y0, y1);
+                else rope_head(ro, row + ro.hq + (is_k ? 0 : ro.hkv) + kh * p.hd, ro.kn, is_k, pos, lane, y0, y1);
                 const float sc = kv_append<KV8>(ro, is_k, kh, sq * p.max_seq + pos, lane, y0, y1);
                 dst = is_k ? nk : nv;
                 if (lane == 0) newsc[is_k ? 0 : 1] = sc;
@@ -557,6 +640,14 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     if constexpr (KV8) {
         if (tid < KCH) ksc[tid] = tid < n ? (tid < nc ? scl : newsc[0]) : 0.0f;
         else if (tid < 2 * KCH) vsc[tid - KCH] = tid - KCH < n ? (tid - KCH < nc ? scl : newsc[1]) : 0.0f;
+    }
+    // Keys past the cached ones contribute zeros (done after the rotation,
+    // which would otherwise wait for these registers' loads first).
+#pragma unroll
+    for (int u = 0; u < KP; ++u) {
+        const int c = l8 * 4 + 32 * u;
+        if constexpr (KV8) kv[u] = i8x4(k8[u]);
+        if (kk >= nc || c >= p.hd) kv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     if (last && kk == n - 1) {
 #pragma unroll
