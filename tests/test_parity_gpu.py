@@ -191,6 +191,15 @@ def test_gemm_split_k_big_tiles(gpu, m, k, n):
     run_and_check(gpu, m, k, n, "dyn", seed=77 + m, bias=True, sample=300)
 
 
+@pytest.mark.parametrize("m,k,n", [(2048, 1024, 2048), (2048, 9216, 2048), (1024, 8192, 2048), (1280, 2048, 1536)])
+def test_gemm_mid_tiles(gpu, m, k, n):
+    # Tile configurations the other shapes do not reach: exactly 256 tiles of
+    # 128x128 (the 128x128 DMA tile), the same split 2 ways over a long K,
+    # 128 tiles of 128x128 as 64x128 tiles split 2 ways, and 480 tiles of
+    # 64x64 (the 4-stage 64-byte form).
+    run_and_check(gpu, m, k, n, "dyn", seed=m + 3 * k + n, bias=True, sample=300)
+
+
 @pytest.mark.parametrize("n", [11008, 10995])
 def test_gemm_column_split(gpu, n):
     # 32 x 43 tiles of 256x256 would be 5.4 rounds of 256 CUs: the first
@@ -270,14 +279,19 @@ def test_gemv_rejects_more_than_32_rows(gpu):
         ops.matmul_i8(xq, xq[:5], torch.ones(33, device=gpu), torch.ones(5, device=gpu), variant="gemv")
 
 
-def test_static_scale_matmul(gpu):
-    m, k, n = 70, 264, 150
+@pytest.mark.parametrize("m,k,n", [(70, 264, 150), (512, 1024, 3072), (2048, 1024, 4096), (4096, 1024, 8192)])
+def test_static_scale_matmul(gpu, m, k, n):
+    # The register-staged kernel (K % 128 != 0), then the LDS-DMA kernel on
+    # 64x64, 256x128 and 256x256 tiles.
     xq = o.quant_pack(o.synth_acts(m, k, 1), np.full(m, 0.02, np.float32))
     wq, _ = o.synth_weights(n, k, 2)
     sx, sw = np.float32(0.0123), np.float32(0.0071)
     got = ops.matmul_i8_static(dev_u32(xq, gpu), dev_u32(wq, gpu), sx, sw).cpu().numpy()
-    want = o.epilogue_static(o.acc_exact(xq, wq), sx, sw)
-    assert (got.view(np.uint32) == want.view(np.uint32)).all()
+    rng = np.random.default_rng(m + n)
+    rows = np.unique(np.concatenate([[0, m - 1], rng.integers(0, m, 200)])) if m > 512 else np.arange(m)
+    cols = np.unique(np.concatenate([[0, n - 1], rng.integers(0, n, 200)])) if m > 512 else np.arange(n)
+    want = o.epilogue_static(o.acc_exact(xq, wq, rows, cols), sx, sw)
+    assert (got[np.ix_(rows, cols)].view(np.uint32) == want.view(np.uint32)).all()
 
 
 def test_linear_config0(gpu):
