@@ -111,7 +111,7 @@ __device__ __forceinline__ bool gated_tile_skipped(const GemmArgs& a, int row0, 
     const int rows = min(BM, a.m - row0), cols = min(BN, a.n - col0);
     for (int i = t; i < rows * cols; i += NT) {
         const int r = i / cols, c = i - r * cols;
-        out[(int64_t)(row0 + r) * a.n + col0 + c] = 0.0f;
+        out[(int64_t)(row0 + r) * out_ld(a) + col0 + c] = 0.0f;
     }
     return true;
 }
