@@ -27,9 +27,23 @@ FLAGS = [
 ]
 
 
-def _compile(src):
+# Sources whose code decides the GEMV/tile crossover: the tune store keys its
+# tables by a fingerprint of these and of FLAGS (bh_tune_save / bh_tune_load).
+FP_SOURCES = ["bh_gemv.hip", "bh_gemm.hip", "bh_common.h"]
+
+
+def kernel_fingerprint():
+    """FNV-1a 64 over the tuned kernels' sources and the compile flags."""
+    h = 0xcbf29ce484222325
+    data = b"".join(open(os.path.join(CSRC, f), "rb").read() for f in FP_SOURCES) + " ".join(FLAGS).encode()
+    for byte in data:
+        h = ((h ^ byte) * 0x100000001b3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def _compile(src, fp):
     obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, f"-DBH_KERNEL_FP=0x{fp:016x}ULL", "-c", os.path.join(CSRC, src), "-o", obj]
     p = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the packed-fp32 feature; that warning is noise.
     err = "\n".join(l for l in p.stderr.splitlines() if "packed-fp32-ops" not in l)
@@ -43,7 +57,8 @@ def _compile(src):
 def build(verbose=False):
     os.makedirs(OBJ, exist_ok=True)
     with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        fp = kernel_fingerprint()
+        objs = list(ex.map(lambda src: _compile(src, fp), SOURCES))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     p = subprocess.run(cmd, capture_output=True, text=True)

@@ -610,16 +610,46 @@ void bh_tune_clear(void) {
 
 int bh_tune_get(uint32_t m, uint32_t n, uint32_t k) { return tuned_variant(m, n, k); }
 
-// Text store (gpu_core::tune::FileTuneStore's role): a header naming the
-// format, the ABI version and the gfx target, then "m n k variant" lines.
-static const char* TUNE_HEADER = "brain-hip-tune 1 gfx950";
+// Text store (gpu_core::tune::FileTuneStore's role,
+// crates/qwen3/src/serve.rs:1118-1121): the header names the format, the ABI
+// version, the device the table was measured on and a fingerprint of the
+// GEMV/GEMM kernel sources and flags this library was built from (BH_KERNEL_FP,
+// set by the build), then "m n k variant" lines. A table measured on another
+// device or another kernel build is refused: its crossovers do not carry over.
+#ifndef BH_KERNEL_FP
+#error "BH_KERNEL_FP (the kernel-source fingerprint) must be defined by the build"
+#endif
+static const char* TUNE_HEADER = "brain-hip-tune 2";
+
+// The current device as one token: "<gcnArchName>|<marketing name>" with
+// blanks replaced, or "nodevice" when no GPU is visible.
+static std::string tune_device_tag() {
+    int dev = 0;
+    hipDeviceProp_t prop{};
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return "nodevice";
+    }
+    std::string tag = std::string(prop.gcnArchName) + "|" + prop.name;
+    for (char& ch : tag)
+        if (ch == ' ' || ch == '\t' || ch == '\n') ch = '_';
+    return tag;
+}
+
+static std::string tune_header_line() {
+    char buf[512];
+    snprintf(buf, sizeof buf, "%s abi %d device %s kernels %016llx", TUNE_HEADER, BH_ABI_VERSION,
+             tune_device_tag().c_str(), (unsigned long long)BH_KERNEL_FP);
+    return buf;
+}
 
 int bh_tune_save(const char* path) {
     if (!path) return fail(BH_ERR_INVALID, "bh_tune_save: null path");
+    const std::string hdr = tune_header_line();
     FILE* f = fopen(path, "w");
     if (!f) return fail(BH_ERR_INVALID, "bh_tune_save: cannot write %s", path);
     std::lock_guard<std::mutex> g(g_tune_mu);
-    fprintf(f, "%s abi %d\n", TUNE_HEADER, BH_ABI_VERSION);
+    fprintf(f, "%s\n", hdr.c_str());
     for (const auto& kv : g_tune)
         fprintf(f, "%u %u %u %d\n", std::get<0>(kv.first), std::get<1>(kv.first), std::get<2>(kv.first), kv.second);
     fclose(f);
@@ -630,12 +660,18 @@ int bh_tune_load(const char* path) {
     if (!path) return fail(BH_ERR_INVALID, "bh_tune_load: null path");
     FILE* f = fopen(path, "r");
     if (!f) return fail(BH_ERR_INVALID, "bh_tune_load: cannot read %s", path);
-    char line[256];
-    char want[128];
-    snprintf(want, sizeof want, "%s abi %d", TUNE_HEADER, BH_ABI_VERSION);
-    if (!fgets(line, sizeof line, f) || strncmp(line, want, strlen(want)) != 0) {
+    char line[512];
+    const std::string want = tune_header_line();
+    if (!fgets(line, sizeof line, f)) {
         fclose(f);
-        return fail(BH_ERR_INVALID, "bh_tune_load: %s was not written by this library build", path);
+        return fail(BH_ERR_INVALID, "bh_tune_load: %s is empty", path);
+    }
+    std::string got(line);
+    while (!got.empty() && (got.back() == '\n' || got.back() == '\r')) got.pop_back();
+    if (got != want) {
+        fclose(f);
+        return fail(BH_ERR_INVALID, "bh_tune_load: %s was measured on another device or kernel build (\"%s\", this "
+                    "process: \"%s\")", path, got.c_str(), want.c_str());
     }
     std::map<std::tuple<uint32_t, uint32_t, uint32_t>, int> t;
     unsigned m, n, k;

@@ -365,7 +365,9 @@ const char* bh_variant_kernel(int variant);
  * row bucket and returns it (ms[0] GEMV, ms[1] tile, mean per dispatch).
  * bh_matmul_i8 and the Qwen3 engine consult the recorded choices; without
  * one the static selector applies. The store is a text file: a header naming
- * this library build, then "m n k variant" lines. */
+ * the ABI version, the device and a fingerprint of the GEMV/GEMM kernel
+ * sources and flags, then "m n k variant" lines; bh_tune_load refuses a file
+ * whose header differs (a table from another device or kernel build). */
 int bh_tune_i8(void* stream, uint32_t m, uint32_t k, uint32_t n, uint32_t reps, int* variant, float ms[2]);
 int bh_tune_set(uint32_t m, uint32_t n, uint32_t k, int variant); /* variant 0 removes the entry */
 int bh_tune_get(uint32_t m, uint32_t n, uint32_t k);               /* 0: none recorded */
