@@ -487,7 +487,7 @@ static int paged_read(void* stream, bool apply, const char* who, const float* in
                     group, kv_stride / hd);
     if (batch == 0 || n_heads == 0 || (!apply && cap == 0)) return BH_OK;
     if (!in || !pool || !bt || !seq_lens || !scales || !out) return fail(BH_ERR_INVALID, "%s: null buffer", who);
-    if ((uint64_t)batch * n_heads * ((apply ? hd : cap) + 63) / 64 > I32MAX)
+    if ((uint64_t)batch * n_heads * (((apply ? hd : cap) + 63) / 64) > I32MAX)
         return fail(BH_ERR_INVALID, "%s: grid too large", who);
     PagedReadArgs a{in, pool, pool_words, bt, seq_lens, scales, n_scales, out, n_heads, group, hd, bs, kv_stride,
                     cap, max_bt, scale};

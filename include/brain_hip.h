@@ -105,7 +105,8 @@ int bh_matmul_i8_dyn(void* stream, const uint32_t* xq, const uint32_t* wq, const
 /* bh_matmul_i8_dyn that allocates nothing. No counterpart in the reference:
  * it is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). Same
- * kernels, launch choice and results as bh_matmul_i8_dyn; when the shape
+ * kernels and results as bh_matmul_i8_dyn, in one launch without the column
+ * split that bh_matmul_i8_dyn takes for some wide shapes; when the shape
  * splits K, the i32 partial slabs go to a fixed 32 MiB device array that the
  * library holds on each GPU until the process ends (instead of the per-stream
  * workspace bh_matmul_i8_dyn grows). A shape whose slabs exceed 32 MiB
@@ -195,8 +196,9 @@ int bh_paged_decode_scores_i8(void* stream, const float* q, const uint32_t* pool
                               uint32_t head_dim, uint32_t block_size, uint32_t kv_stride, uint32_t cap,
                               uint32_t max_bt, float scale);
 /* paged_decode_apply_i8_batched (crates/kernels/wgsl/paged_decode_apply_i8_batched.wgsl:28-53):
- * ctx[b][h*head_dim + d] = sum over j < seq_lens[b] (in order) of (probs[b][h][j] * code)
- * * vscale. Step bindings [probs, pool, block_tables, seq_lens, scales, ctx], params
+ * ctx[b][h*head_dim + d] = sum over j < min(seq_lens[b], cap) (in order) of
+ * (probs[b][h][j] * code) * vscale. The reference loops to seq_lens[b]; past cap it would
+ * read the next row's probabilities, so the sum stops at the row's end here. Step bindings [probs, pool, block_tables, seq_lens, scales, ctx], params
  * [batch, n_heads, group, head_dim, block_size, kv_stride, cap, max_bt]. */
 int bh_paged_decode_apply_i8(void* stream, const float* probs, const uint32_t* pool, uint64_t pool_words,
                              const uint32_t* block_tables, const uint32_t* seq_lens, const float* scales,

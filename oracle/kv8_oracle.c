@@ -74,7 +74,12 @@ void or_paged_decode_scores_i8(const float *q, const uint32_t *pool, const uint3
     }
 }
 
-/* paged_decode_apply_i8_batched.wgsl:28-53 */
+/* paged_decode_apply_i8_batched.wgsl:28-53. The sum runs over
+ * j < min(seq_lens[b], cap): the WGSL loops to seq_lens[b], and past cap it
+ * would read the next row's probabilities (or, at the buffer end, whatever
+ * robust access returns), which no caller relies on since probs rows are cap
+ * wide. The HIP kernel clamps the same way; both are pinned by a test with
+ * seq_lens > cap. */
 void or_paged_decode_apply_i8(const float *probs, const uint32_t *pool, const uint32_t *block_tables,
                               const uint32_t *seq_lens, const float *scales, float *ctx, uint32_t batch,
                               uint32_t n_heads, uint32_t group, uint32_t head_dim, uint32_t block_size,
@@ -83,7 +88,7 @@ void or_paged_decode_apply_i8(const float *probs, const uint32_t *pool, const ui
     for (uint32_t idx = 0; idx < batch * n_heads * hd; ++idx) {
         const uint32_t b = idx / (n_heads * hd), rem = idx % (n_heads * hd);
         const uint32_t h = rem / hd, d = rem % hd;
-        const uint32_t t = seq_lens[b], kvh = h / group, pbase = (b * n_heads + h) * cap;
+        const uint32_t t = seq_lens[b] < cap ? seq_lens[b] : cap, kvh = h / group, pbase = (b * n_heads + h) * cap;
         float acc = 0.0f;
         for (uint32_t j = 0; j < t; ++j) {
             const uint32_t physical = block_tables[b * max_bt + j / block_size];

@@ -176,3 +176,37 @@ def test_engine_clip_matches_oracle(gpu):
     vclip = np.where(rng.random(shape) < 0.5, FMAX, rng.uniform(0.02, 0.2, shape)).astype(np.float32)
     prompts = rng.integers(0, cfg["vocab"], size=(2, 9))
     compare_clip(cfg, w, prompts, 6, kclip, vclip)
+
+
+def test_append_non_finite_matches_oracle(be):
+    """NaN / Inf heads: the kernel's policy (NaN dropped from max|x| and coded
+    0; Inf bounded by the clip and saturated to +-127) equals the oracle's."""
+    hd, bs = 8, 1
+    cache = Cache(be, 3, bs, 2, hd)
+    src = np.array([[np.nan, 2.0, -1.0, 0.5, 0.0, 1.0, -2.0, 0.25, np.inf, 2.0, -1e37, 0.5, -np.inf, 1.0, -2.0, 0.25],
+                    [np.inf, 2.0, -1e37, 0.5, -np.inf, 1.0, -2.0, 0.25, np.nan, np.nan, 3.0, 0, 0, 0, 0, 0]],
+                   np.float32)
+    cache.append(src, np.array([0, 2], np.uint32), np.array([0, 0], np.uint32), np.array([FMAX, 12.7], np.float32))
+    cache.check()
+
+
+def test_apply_stops_at_cap(be):
+    """seq_lens > cap: the context sums the row's cap probabilities only."""
+    rng = np.random.default_rng(11)
+    n_kv, hd, bs, group, max_bt = 2, 64, 4, 2, 3
+    nh, cap, batch = n_kv * group, 8, 2
+    cache = Cache(be, batch * max_bt, bs, n_kv, hd)
+    bt = np.arange(batch * max_bt, dtype=np.uint32).reshape(batch, max_bt)
+    for j in range(max_bt * bs):
+        src = rng.standard_normal((batch, n_kv * hd)).astype(np.float32)
+        cache.append(src, bt[:, j // bs].copy(), np.full(batch, j % bs, np.uint32), np.full(n_kv, FMAX, np.float32))
+    lens = np.array([12, 9], np.uint32)
+    probs = rng.random((batch, nh, cap)).astype(np.float32)
+    ctx = be.storage(batch * nh * hd)
+    bufs = [be.storage_init("probs", probs), cache.pool, be.storage_init("bt", u32_as_f32(bt)),
+            be.storage_init("len", u32_as_f32(lens)), cache.sc, ctx]
+    be.submit([], [be.step(be.kernel_index(NAMES[2]), bufs, [batch, nh, group, hd, bs, n_kv * hd, cap, max_bt],
+                           batch * nh * hd)])
+    got = be.read(ctx, batch * nh * hd, np.uint32)
+    want = o.paged_decode_apply_i8(probs, cache.pool_h, bt, [cap, cap], cache.sc_h, nh, group, hd, bs, n_kv * hd, cap)
+    same(got, f32bits(want), "context")

@@ -149,3 +149,35 @@ def test_scores_and_apply_against_float64():
             np.testing.assert_allclose(got[b, h, :lens[b]], want, rtol=2e-5, atol=2e-5 * np.abs(want).max())
             wc = probs[b, h, :lens[b]].astype(np.float64) @ k
             np.testing.assert_allclose(ctx[b, h * hd:(h + 1) * hd], wc, rtol=2e-5, atol=2e-5 * np.abs(wc).max())
+
+
+def test_apply_stops_at_cap_when_seq_len_exceeds_it():
+    """seq_lens[b] > cap: the sum ends at the row's cap probabilities (the WGSL
+    loop would read the next row's); equal to seq_lens[b] == cap."""
+    rng = np.random.default_rng(3)
+    batch, nh, n_kv, hd, bs, cap, max_bt = 2, 4, 2, 16, 4, 8, 3
+    pool, scales, bt = build_cache(rng, batch, n_kv, hd, bs, [12, 12], batch * max_bt, max_bt)
+    probs = rng.random((batch, nh, cap)).astype(np.float32)
+    over = o.paged_decode_apply_i8(probs, pool, bt, [12, 9], scales, nh, nh // n_kv, hd, bs, n_kv * hd, cap)
+    at = o.paged_decode_apply_i8(probs, pool, bt, [cap, cap], scales, nh, nh // n_kv, hd, bs, n_kv * hd, cap)
+    assert np.array_equal(over.view(np.uint32), at.view(np.uint32))
+
+
+def test_append_non_finite_policy():
+    """NaN and Inf in a head (the WGSL leaves max() with NaN implementation
+    defined; this build fixes it): max|x| drops NaN (fmaxf), so the scale comes
+    from the other elements and the NaN's code is 0 (i32(NaN) = 0); an Inf
+    makes max|x| Inf, the clip (FLT_MAX when unclipped) bounds the scale, and
+    Inf / scale saturates to +-127 while every finite element codes to 0."""
+    hd = 8
+    x = np.array([[np.nan, 2.0, -1.0, 0.5, 0.0, 1.0, -2.0, 0.25]], np.float32)
+    pool, scales = append(x, [0], [0], [FMAX], 1, 1, hd)
+    assert scales[0] == np.float32(2.0) / np.float32(127.0)
+    assert list(unpack_codes(pool)) == [0, 127, -64, 32, 0, 64, -127, 16]
+    y = np.array([[np.inf, 2.0, -1e37, 0.5, -np.inf, 1.0, -2.0, 0.25]], np.float32)
+    pool, scales = append(y, [0], [0], [FMAX], 1, 1, hd)
+    assert scales[0] == np.float32(FMAX) / np.float32(127.0)
+    assert list(unpack_codes(pool)) == [127, 0, -4, 0, -127, 0, 0, 0]
+    pool, scales = append(y, [0], [0], [12.7], 1, 1, hd)          # clipped: scale 0.1
+    assert scales[0] == np.float32(12.7) / np.float32(127.0)
+    assert list(unpack_codes(pool)) == [127, 20, -127, 5, -127, 10, -20, 2]

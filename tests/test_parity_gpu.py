@@ -106,7 +106,7 @@ def test_quant_unaligned_rows_and_odd_k_scale(gpu):
 
 
 # ---------------------------------------------------------------- matmul helpers
-def run_and_check(gpu, m, k, n, variant, seed, bias=False, sample=None):
+def run_and_check(gpu, m, k, n, variant, seed, bias=False, sample=None, must_rows=(), must_cols=()):
     x = special_acts(m, k, seed)
     sx = o.max_abs_row(x)
     xq = o.quant_pack(x, sx)
@@ -121,8 +121,8 @@ def run_and_check(gpu, m, k, n, variant, seed, bias=False, sample=None):
         rows, cols = np.arange(m), np.arange(n)
     else:
         rng = np.random.default_rng(seed)
-        rows = np.unique(np.concatenate([[0, m - 1], rng.integers(0, m, sample)]))
-        cols = np.unique(np.concatenate([[0, n - 1], rng.integers(0, n, sample)]))
+        rows = np.unique(np.concatenate([[0, m - 1], list(must_rows), rng.integers(0, m, sample)])).astype(np.int64)
+        cols = np.unique(np.concatenate([[0, n - 1], list(must_cols), rng.integers(0, n, sample)])).astype(np.int64)
     acc = o.acc_exact(xq, wq, rows, cols)
     bsub = None if b is None else b[cols]
     assert (acc_d[np.ix_(rows, cols)] == acc).all(), "i32 accumulators differ"
@@ -205,8 +205,12 @@ def test_gemm_column_split(gpu, n):
     # 32 x 43 tiles of 256x256 would be 5.4 rounds of 256 CUs: the first
     # 10240 columns run as 5 whole rounds, the rest as a second GEMM writing
     # into the same rows (output row stride n, its own tile choice). An odd
-    # width takes the per-element stores.
-    run_and_check(gpu, 8192, 1024, n, "dyn", seed=n, bias=True, sample=300)
+    # width takes the per-element stores. The seam between the two GEMMs
+    # (columns 10240 +- 64, each side's last and first tile columns), the
+    # last column and the tile-row boundaries are always in the sample.
+    seam = list(range(10240 - 64, 10240 + 64)) + [n - 2, n - 1]
+    run_and_check(gpu, 8192, 1024, n, "dyn", seed=n, bias=True, sample=300, must_cols=seam,
+                  must_rows=[1, 255, 256, 257, 4095, 4096, 8190])
 
 
 @pytest.mark.parametrize("k,n", [(3840, 3840), (3840, 10240), (3840, 11520)])
