@@ -86,6 +86,7 @@ static void lin_free(lin_t *l) {
 static void lin_apply(const lin_t *l, const float *x, float *out) {
     const uint32_t n = l->n, k = l->k;
     if (l->packed) {
+        if (k >= 133143u) abort();
         float sx;
         uint32_t *xq = (uint32_t *)malloc((size_t)k);
         or_max_abs_row(x, 1, k, &sx);
@@ -96,7 +97,10 @@ static void lin_apply(const lin_t *l, const float *x, float *out) {
 #pragma omp parallel for schedule(static)
         for (uint32_t j = 0; j < n; ++j) {
             const int8_t *b = (const int8_t *)(l->packed + (size_t)j * (k / 4));
-            int64_t acc = 0;
+            /* |acc| <= 127 * 127 * k: exact in i32 for k < 133143 (checked
+             * below), so the (vectorised) sum equals the int64 one. */
+            int32_t acc = 0;
+#pragma omp simd reduction(+ : acc)
             for (uint32_t c = 0; c < k; ++c) acc += (int32_t)a[c] * (int32_t)b[c];
             const float v = (float)(int32_t)acc * sx;
             out[j] = v * l->scale[j];
