@@ -1102,6 +1102,7 @@ struct bh_qwen3 {
     bool nofuse = false;        // BH_QWEN3_UNFUSED for the current decode call
     bool graph_nofuse = false;  // the mode the captured step was recorded in
     std::vector<void*> allocs;
+    std::vector<size_t> alloc_bytes;  // parallel to allocs
 
     ~bh_qwen3() {
         (void)hipSetDevice(device);
@@ -1120,9 +1121,27 @@ int dalloc(bh_qwen3* e, T** p, size_t count) {
     const size_t bytes = std::max<size_t>(count * sizeof(T), 256);
     if (hipMalloc(&v, bytes) != hipSuccess) return fail(BH_ERR_NOMEM, "bh_qwen3: hipMalloc of %zu bytes failed", bytes);
     e->allocs.push_back(v);
+    e->alloc_bytes.push_back(bytes);
     if (hipMemset(v, 0, bytes) != hipSuccess) return fail(BH_ERR_HIP, "bh_qwen3: hipMemset failed");
     *p = static_cast<T*>(v);
     return BH_OK;
+}
+
+// Host-side guard for every copy between the engine's device buffers and the
+// caller: [p, p + bytes) must lie inside one engine allocation. The copies
+// below are sized from max_batch / max_seq / the live batch; a slip there
+// would read or write past an allocation, so it is refused instead.
+int check_span(const bh_qwen3* e, const void* p, size_t bytes, const char* what) {
+    const uintptr_t a = (uintptr_t)p;
+    for (size_t i = 0; i < e->allocs.size(); ++i) {
+        const uintptr_t b = (uintptr_t)e->allocs[i];
+        if (a >= b && a < b + e->alloc_bytes[i])
+            return bytes <= b + e->alloc_bytes[i] - a
+                       ? BH_OK
+                       : fail(BH_ERR_INVALID, "bh_qwen3: %s: %zu bytes at offset %zu of a %zu-byte buffer", what,
+                              bytes, (size_t)(a - b), e->alloc_bytes[i]);
+    }
+    return fail(BH_ERR_INVALID, "bh_qwen3: %s: pointer outside the engine's buffers", what);
 }
 
 #define BH_TRY(x)                 \
@@ -1785,6 +1804,8 @@ int bh_qwen3_prefill(bh_qwen3* e, const uint32_t* tokens, uint32_t batch, uint32
             }
         const bool last = p0 + cc == len;
         for (uint32_t b = 0; b < batch; ++b) map[b] = (int)(b * cc + cc - 1);
+        BH_TRY(check_span(e, e->tok_rows, rows * 4, "prefill rows"));
+        if (last) BH_TRY(check_span(e, e->row_map, batch * 4, "prefill row map"));
         BH_HIP(hipMemcpyAsync(e->tok_rows, tok.data(), rows * 4, hipMemcpyHostToDevice, e->stream), "upload");
         BH_HIP(hipMemcpyAsync(e->pos_rows, pos.data(), rows * 4, hipMemcpyHostToDevice, e->stream), "upload");
         BH_HIP(hipMemcpyAsync(e->seq_rows, seq.data(), rows * 4, hipMemcpyHostToDevice, e->stream), "upload");
@@ -1795,6 +1816,8 @@ int bh_qwen3_prefill(bh_qwen3* e, const uint32_t* tokens, uint32_t batch, uint32
     }
     std::vector<uint32_t> pdec(batch, len);
     const uint32_t ctl[2] = {len, e->max_seq};
+    BH_TRY(check_span(e, e->pos_dec, batch * 4, "prefill positions"));
+    BH_TRY(check_span(e, e->tok_dec, batch * 4, "prefill tokens"));
     BH_HIP(hipMemcpyAsync(e->pos_dec, pdec.data(), batch * 4, hipMemcpyHostToDevice, e->stream), "upload");
     BH_HIP(hipMemcpyAsync(e->ctl, ctl, sizeof ctl, hipMemcpyHostToDevice, e->stream), "upload");
     BH_HIP(hipMemcpyAsync(next, e->tok_dec, batch * 4, hipMemcpyDeviceToHost, e->stream), "download");
@@ -1841,6 +1864,7 @@ int bh_qwen3_decode(bh_qwen3* e, uint32_t steps, uint32_t flags, uint32_t* out) 
         }
         for (uint32_t s = 0; s < steps; ++s) BH_HIP(hipGraphLaunch(e->graph, e->stream), "graph launch");
     }
+    BH_TRY(check_span(e, e->hist + (size_t)e->decoded * b, (size_t)steps * b * 4, "decoded tokens"));
     BH_HIP(hipMemcpyAsync(out, e->hist + (size_t)e->decoded * b, (size_t)steps * b * 4, hipMemcpyDeviceToHost, e->stream),
            "download");
     BH_TRY(sync(e));
@@ -1853,6 +1877,7 @@ int bh_qwen3_logits(bh_qwen3* e, float* out, uint64_t n) {
     const uint64_t want = (uint64_t)e->batch * e->c.vocab;
     if (!e->batch || n < want) return fail(BH_ERR_INVALID, "bh_qwen3_logits: need %llu floats", (unsigned long long)want);
     (void)hipSetDevice(e->device);
+    BH_TRY(check_span(e, e->logits, want * 4, "logits"));
     BH_HIP(hipMemcpyAsync(out, e->logits, want * 4, hipMemcpyDeviceToHost, e->stream), "download");
     return sync(e);
 }
@@ -1865,12 +1890,14 @@ int bh_qwen3_kv_read(bh_qwen3* e, uint32_t layer, uint32_t seq, uint32_t which, 
     (void)hipSetDevice(e->device);
     const size_t tok0 = (size_t)seq * e->max_seq + pos0;
     const uint8_t* cache = static_cast<const uint8_t*>(which ? e->vc : e->kc) + (size_t)layer * e->layer_kv * e->kv_elem;
+    BH_TRY(check_span(e, cache + tok0 * e->hkv * e->kv_elem, (size_t)npos * e->hkv * e->kv_elem, "kv read"));
     BH_HIP(hipMemcpyAsync(data, cache + tok0 * e->hkv * e->kv_elem, (size_t)npos * e->hkv * e->kv_elem,
                           hipMemcpyDeviceToHost, e->stream),
            "kv read");
     if (e->c.kv_int8 && scales) {
         const size_t nkv = e->c.n_kv_heads;
         const float* sc = (which ? e->vscale : e->kscale) + (size_t)layer * e->max_batch * e->max_seq * nkv;
+        BH_TRY(check_span(e, sc + tok0 * nkv, (size_t)npos * nkv * 4, "kv scale read"));
         BH_HIP(hipMemcpyAsync(scales, sc + tok0 * nkv, (size_t)npos * nkv * 4, hipMemcpyDeviceToHost, e->stream),
                "kv scale read");
     }
