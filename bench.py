@@ -376,6 +376,28 @@ def mfma_roof(torch, lib, dev):
     return round(ops / (a.elapsed_time(b) * 1e-3) / 1e12, 1)
 
 
+def hbm_read_probe(torch, lib, dev, seg_bytes=256 << 20, nseg=4):
+    """The plain streaming-read ceiling on this box (bh_roof_hbm_read: 16-byte
+    loads, as the GEMV's): one graph reading `nseg` distinct 256 MiB segments
+    in turn (1 GiB, so each read is cold), best over four grid sizes."""
+    from brain_amd._lib import check
+    buf = torch.empty(seg_bytes * nseg // 4, dtype=torch.int32, device=dev).random_(-2**31, 2**31 - 1)
+    best = None
+    for blocks in (2048, 4096, 8192, 16384):
+        out = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+        fns = [lambda i=i: check(lib.bh_roof_hbm_read(torch.cuda.current_stream().cuda_stream,
+                                                       buf.data_ptr() + i * seg_bytes, seg_bytes, blocks,
+                                                       out.data_ptr())) for i in range(nseg)]
+        us = graph_per_launch_us(torch, fns, reps=3)
+        gbs = seg_bytes / (us * 1e-6) / 1e9
+        if best is None or gbs > best["gbs"]:
+            best = {"gbs": round(gbs, 1), "blocks": blocks, "us_per_256mib": round(us, 1)}
+    del buf
+    torch.cuda.empty_cache()
+    best["frac_of_8tbs"] = round(best["gbs"] / HBM_PEAK_GBS, 4)
+    return best
+
+
 def bench_w4a8(reps=20):
     """W4A8 (matmul_q4_gemv / matmul_q4_dyn): the configs[1] decode shapes at
     M = 1 and 16 and two prefill shapes with int4 weights. Decode is measured
@@ -575,8 +597,18 @@ def bench_qwen3(prompt_len=128, gen=256, batches=(1, 4, 8), cpu=True):
     out = {"model": "Qwen3-0.6B architecture (28 layers, d 1024, 16q/8kv heads, hd 128, ff 3072, vocab 151936, tied)",
            "weights": "random init (device, seeded), int8 per-channel", "prompt_len": prompt_len, "decode_steps": gen,
            "int8_weight_mb_per_step": round(wbytes / 1e6, 1)}
-    for b, kv8 in [(b, 0) for b in batches] + [(max(batches), 1)]:
-        e = Qwen3Engine(dict(c, kv_int8=kv8), b, prompt_len + gen + 8, max_rows=b * prompt_len)
+    max_seq = prompt_len + gen + 8
+    for b, kv8, paged in [(b, 0, False) for b in batches] + [(max(batches), 1, False), (max(batches), 1, True)]:
+        cfg = dict(c, kv_int8=kv8)
+        if paged:
+            # The reference's paged pool: blocks of 32 positions in a pool with
+            # spare blocks, each sequence's blocks scattered over it.
+            max_bt = -(-max_seq // 32)
+            nblk = b * max_bt + 16
+            cfg.update(kv_block_size=32, kv_num_blocks=nblk)
+        e = Qwen3Engine(cfg, b, max_seq, max_rows=b * prompt_len)
+        if paged:
+            e.set_block_table(np.random.default_rng(9).permutation(nblk)[:b * max_bt].reshape(b, max_bt))
         e.init_random(7)
         prompts = np.random.default_rng(b).integers(0, c["vocab"], size=(b, prompt_len))
         e.prefill(prompts)
@@ -590,7 +622,7 @@ def bench_qwen3(prompt_len=128, gen=256, batches=(1, 4, 8), cpu=True):
         step_s = (t2 - t1) / gen
         avg_ctx = prompt_len + (gen + 1) / 2.0
         kv_bytes = 2 * c["n_layers"] * b * avg_ctx * c["n_kv_heads"] * c["head_dim"] * (1 if kv8 else 4)
-        out[f"batch{b}" + ("_kv_int8" if kv8 else "")] = {"decode_tok_s": round(b * gen / (t2 - t1), 1), "ms_per_step": round(step_s * 1e3, 4),
+        out[f"batch{b}" + ("_kv_int8" if kv8 else "") + ("_paged32" if paged else "")] = {"decode_tok_s": round(b * gen / (t2 - t1), 1), "ms_per_step": round(step_s * 1e3, 4),
                             "prefill_ms": round((t1 - t0) * 1e3, 2),
                             "prefill_tok_s": round(b * prompt_len / (t1 - t0), 1),
                             "step_hbm_gbs": round((wbytes + kv_bytes) / step_s / 1e9, 1)}
@@ -729,8 +761,15 @@ def main():
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
+        # ... and the dwordx4 read probe (the GEMV's load width) over the same
+        # 256 MiB, 3 times: a second calibration point for FETCH_SIZE.
+        from brain_amd._lib import check
+        sink = torch.empty(2048 * 256, dtype=torch.int32, device=dev)
+        for _ in range(3):
+            check(lib.bh_roof_hbm_read(torch.cuda.current_stream().cuda_stream, src.data_ptr(), src.numel() * 4,
+                                       2048, sink.data_ptr()))
         torch.cuda.synchronize()
-        print(json.dumps({"copy_bytes": src.numel() * 4}))
+        print(json.dumps({"copy_bytes": src.numel() * 4, "read_probe_bytes": src.numel() * 4}))
         return
     if args.only in ("", "decode", "gemv"):
         sets = make_decode_set(torch, dev, gen)
@@ -763,6 +802,7 @@ def main():
         print(json.dumps(res))
         return
     roof = mfma_roof(torch, lib, dev)
+    hbm_roof = hbm_read_probe(torch, lib, dev)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     pcpu = None
     if not args.no_cpu and "prefill" in res and "error" not in res["prefill"]:
@@ -772,14 +812,28 @@ def main():
     value = d["step_bytes"] / (d["step_ms"] * 1e-3) / 1e9
     # HBM bytes per GEMV launch from the committed rocprofv3 FETCH_SIZE /
     # WRITE_SIZE runs of this workload (counters cannot be read live here).
-    traffic = None
+    traffic, tsrc = None, {}
     tpath = os.path.join(ROOT, "profiles", "gemv_traffic.txt")
     if os.path.exists(tpath):
         with open(tpath) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    traffic = int(line.split(":")[1])
+                key, _, val = line.partition(":")
+                if key == "traffic_bytes_per_launch":
+                    traffic = int(val)
+                elif key in ("measured_at_commit", "fetch_factor", "fetch_factor_read_probe", "write_factor"):
+                    tsrc[key] = val.strip()
     gemv_gbs = d["gemv_mean_bytes"] / (d["gemv_mean_us"] * 1e-6) / 1e9
+    # The same roofline per kernel, from the cold per-shape table: the 12
+    # narrow shapes run gemv_i8_kernel, the 4 LM heads gemv_i8_stream_kernel.
+    by_kernel = []
+    if isinstance(res.get("shapes"), list):
+        for name, rows in (("gemv_i8_kernel", [r for r in res["shapes"] if r["n"] < 16384]),
+                           ("gemv_i8_stream_kernel", [r for r in res["shapes"] if r["n"] >= 16384])):
+            gb = sum(gemv_bytes(r["m"], r["k"], r["n"]) for r in rows) / len(rows)
+            us = sum(r["gemv_us"] for r in rows) / len(rows)
+            by_kernel.append({"kernel": name, "shapes": len(rows), "avg_algorithmic_bytes": round(gb),
+                              "avg_launch_us_cold": round(us, 2), "gbs": round(gb / us / 1e3, 1),
+                              "frac": round(gb / us / 1e3 / HBM_PEAK_GBS, 4)})
     line = {
         "metric": "int8 GEMM TOPS & %peak (prefill); GEMV GB/s & %HBM (decode); vs CPU",
         "value": round(value, 1),
@@ -799,8 +853,14 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "gemv_i8_kernel", "avg_launch_us": round(d["gemv_mean_us"], 2),
-                     "avg_algorithmic_bytes": round(d["gemv_mean_bytes"])},
+                     "kernel": "gemv_i8_kernel (12 narrow shapes) + gemv_i8_stream_kernel (4 LM heads)",
+                     "avg_launch_us": round(d["gemv_mean_us"], 2),
+                     "avg_algorithmic_bytes": round(d["gemv_mean_bytes"]),
+                     "by_kernel": by_kernel,
+                     "traffic_source": dict(tsrc, file="profiles/gemv_traffic.txt",
+                                            how="rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of bench.py --only gemv, "
+                                                "committed summary, not measured in this run"),
+                     "hbm_read_probe": hbm_roof},
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample", "host")},
         "decode_shapes_cold": res["shapes"],
         "config0_linear": res["config0"],

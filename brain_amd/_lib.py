@@ -47,7 +47,7 @@ class StatsT(C.Structure):
 class Qwen3ConfigT(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in ("vocab", "n_layers", "d_model", "n_heads", "n_kv_heads", "head_dim", "d_ff")] + \
                [("rope_theta", C.c_float), ("rms_eps", C.c_float), ("tie_embeddings", C.c_uint32), ("qk_norm", C.c_uint32),
-                ("kv_int8", C.c_uint32)]
+                ("kv_int8", C.c_uint32), ("kv_block_size", C.c_uint32), ("kv_num_blocks", C.c_uint32)]
 
 
 class CostT(C.Structure):
@@ -77,6 +77,7 @@ SIGNATURES = {
     "bh_quantize_weight_device": (i32, [vp, vp, u32, u32, vp, vp]),
     "bh_f32_to_bf16": (i32, [vp, vp, vp, C.c_uint64]),
     "bh_roof_mfma_i8": (i32, [vp, u32, u32, vp]),
+    "bh_roof_hbm_read": (i32, [vp, vp, u64, u32, vp]),
     "bh_qwen3_create": (i32, [vp, u32, u32, u32, i32, vp]),
     "bh_qwen3_destroy": (None, [vp]),
     "bh_qwen3_set_weight": (i32, [vp, C.c_char_p, vp, u64]),
@@ -90,6 +91,8 @@ SIGNATURES = {
     "bh_qwen3_stream": (vp, [vp]),
     "bh_qwen3_load": (i32, [vp, C.c_char_p]),
     "bh_qwen3_set_kv_clip": (i32, [vp, u32, u32, vp]),
+    "bh_qwen3_set_block_table": (i32, [vp, vp, u32, u32]),
+    "bh_qwen3_kv_pool": (i32, [vp, u32, u32, P(vp), P(u64), P(vp), P(u64)]),
     "bh_qwen3_autotune": (i32, [vp, u32]),
     "bh_tune_i8": (i32, [vp, u32, u32, u32, u32, vp, vp]),
     "bh_tune_set": (i32, [u32, u32, u32, i32]),

@@ -155,6 +155,32 @@ __global__ __launch_bounds__(256) void roof_mfma_i8_kernel(uint32_t iters, int32
     out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
+// Bandwidth roof (the read side of crates/gpu-core/src/roof.rs:458-490's axpy
+// probe): `words4` 16-byte words read with 16-byte vector loads, as the GEMV
+// loads its weights. Each workgroup reads contiguous runs of 256 x 8 words
+// (8 loads in flight per thread, 4 KB apart), the runs spread over the grid;
+// the words are XOR-folded so no load is dead, one word per thread written.
+__global__ __launch_bounds__(256) void roof_hbm_read_kernel(const uint4* __restrict__ src, uint64_t words4,
+                                                            uint32_t* out) {
+    constexpr int U = 8;
+    const uint64_t stride = (uint64_t)gridDim.x * 256 * U;
+    uint32_t acc = 0;
+    uint64_t i = (uint64_t)blockIdx.x * 256 * U + threadIdx.x;
+    for (; i + (U - 1) * 256 < words4; i += stride) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = src[i + u * 256];
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (int u = 0; u < U; ++u)
+        if (i + u * 256 < words4) {
+            const uint4 v = src[i + u * 256];
+            acc ^= v.x ^ v.y ^ v.z ^ v.w;
+        }
+    out[(uint64_t)blockIdx.x * blockDim.x + threadIdx.x] = acc;
+}
+
 // ---------------------------------------------------------------- errors
 static thread_local std::string g_err;
 
@@ -525,6 +551,14 @@ int bh_roof_mfma_i8(void* stream, uint32_t blocks, uint32_t iters, int32_t* out)
     if (blocks == 0 || blocks > I32MAX || !out) return fail(BH_ERR_INVALID, "bh_roof_mfma_i8: blocks=%u", blocks);
     roof_mfma_i8_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(iters, out);
     return hip_status(hipGetLastError(), "roof_mfma_i8 launch");
+}
+
+int bh_roof_hbm_read(void* stream, const void* src, uint64_t bytes, uint32_t blocks, uint32_t* out) {
+    if (blocks == 0 || blocks > 65536 || !out || (bytes && !src) || bytes % 16 || ((uintptr_t)src & 15))
+        return fail(BH_ERR_INVALID, "bh_roof_hbm_read: blocks=%u bytes=%llu (16-byte aligned multiple of 16)", blocks,
+                    (unsigned long long)bytes);
+    roof_hbm_read_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(static_cast<const uint4*>(src), bytes / 16, out);
+    return hip_status(hipGetLastError(), "roof_hbm_read launch");
 }
 
 // ---------------------------------------------------------------- autotune

@@ -212,12 +212,33 @@ __global__ __launch_bounds__(NT) void swiglu_quant_kernel(const float* gu, int f
     quant_row<G, NT>(h, d4, red, sx + r, xq + (size_t)r * xq_words);
 }
 
+// Where position `pos` of sequence `seq` lives in a layer's cache: the token
+// slot whose K (V) row is [slot][hkv] and whose KV8 scales are [slot][nkv].
+// Contiguous slabs (bs == 0): slot = seq * max_seq + pos. Paged pool
+// (crates/qwen3/src/serve.rs:349-356, the layout of
+// paged_kv_append_i8_clipped_batched.wgsl:46-77): slot = block * bs + pos % bs
+// with block = bt[seq * max_bt + pos / bs]; bs is a multiple of the attention
+// chunk, so a chunk of keys lies inside one block. A table entry outside the
+// pool (an unallocated block) maps to block 0: only chunks past a row's
+// position read it (their reads are issued before the position is known and
+// never used), and the host refuses to run a row whose used blocks are not
+// allocated.
+struct KvMap {
+    const uint32_t* bt;  // [max_batch][max_bt] physical blocks (paged)
+    int max_bt, bs, nblk, max_seq;
+    __device__ __forceinline__ size_t slot(size_t seq, int pos) const {
+        if (bs == 0) return seq * max_seq + pos;
+        const uint32_t blk = bt[seq * max_bt + pos / bs];
+        return (size_t)(blk < (uint32_t)nblk ? blk : 0u) * bs + pos % bs;
+    }
+};
+
 struct RopeArgs {
     const float* qkv;  // [rows, hq + 2 hkv]
     float* q;          // [rows, hq]
-    void* kc;          // this layer's K cache [max_batch, max_seq, hkv] (f32, or int8 with KV8)
+    void* kc;          // this layer's K cache [slots, hkv] (f32, or int8 with KV8)
     void* vc;
-    float* ks;         // KV8: per (token slot, kv head) scales [max_batch, max_seq, nkv]
+    float* ks;         // KV8: per (token slot, kv head) scales [slots, nkv]
     float* vs;
     const float* kclip;  // KV8: per kv head ceilings (FLT_MAX: no clipping)
     const float* vclip;
@@ -228,6 +249,7 @@ struct RopeArgs {
     int nh, nkv, hd, hq, hkv, max_seq, qk_norm;
     float eps, theta;
     const float2* cs;  // [max_seq][hd/2] (cos, sin) of the rotation angles, rope_table_kernel
+    KvMap map;         // (seq, pos) -> cache slot
 };
 
 // The rotation of pair m at position pos, angle pos * theta^(-2m/hd)
@@ -412,7 +434,7 @@ __global__ __launch_bounds__(64) void qk_rope_append_kernel(RopeArgs p) {
     const int r = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const int W = p.hq + 2 * p.hkv;
     const uint32_t pos = p.pos[r];
-    const size_t tok = (size_t)p.seq[r] * p.max_seq + pos;
+    const size_t tok = p.map.slot(p.seq[r], (int)pos);
     const bool is_q = h < p.nh, is_k = !is_q && h < p.nh + p.nkv;
     const int kh = is_q ? 0 : (is_k ? h - p.nh : h - p.nh - p.nkv);
     const float* src = p.qkv + (size_t)r * W +
@@ -494,8 +516,8 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     float* nk = qs + G * p.hd;
     float* nv = nk + p.hd;
     float* vls = nv + p.hd;
-    const size_t tok0 = sq * p.max_seq + j0;  // cache slot of this chunk's first key
-    const size_t base = sq * p.max_seq * p.hkv + (size_t)kh * p.hd;
+    const size_t tok0 = p.ro.map.slot(sq, j0);  // cache slot of this chunk's first key
+    const size_t cb = tok0 * p.hkv + (size_t)kh * p.hd;  // element of this chunk's first key, this head
 
     // Every cache read of the chunk is issued first, so its latency overlaps
     // the query rotation: this lane's K pieces (8 lanes per key, float4
@@ -515,7 +537,7 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     constexpr bool VST = ROPE;
     constexpr int VPT = VST ? KCH * 256 / 4 / RT : 0;
     const int hd4 = p.hd >> 2;
-    const size_t vbo = base + (size_t)j0 * p.hkv;
+    const size_t vbo = cb;
     const uint32_t vls_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)vls;
     float scl = 0.0f;  // KV8: ksc[tid] (tid < KCH) or vsc[tid - KCH]
     // The loads are unconditional, at indices clamped into the first `lim`
@@ -524,7 +546,7 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     // load goes out. Lanes past `lim` get a repeat of a valid key, masked
     // (K) or never used (V, scales).
     auto load_chunk = [&](int lim) {
-        const size_t kro = base + (size_t)(j0 + min(kk, lim - 1)) * p.hkv;
+        const size_t kro = cb + (size_t)min(kk, lim - 1) * p.hkv;
 #pragma unroll
         for (int u = 0; u < KP; ++u) {
             // Pieces past head_dim repeat its last piece (masked below).
@@ -619,7 +641,7 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
                 const bool is_k = h == G;
                 if (one_head) rope_apply(ro, is_k, lane, rin, y0, y1);
                 else rope_head(ro, row + ro.hq + (is_k ? 0 : ro.hkv) + kh * p.hd, ro.kn, is_k, pos, lane, y0, y1);
-                const float sc = kv_append<KV8>(ro, is_k, kh, sq * p.max_seq + pos, lane, y0, y1);
+                const float sc = kv_append<KV8>(ro, is_k, kh, ro.map.slot(sq, (int)pos), lane, y0, y1);
                 dst = is_k ? nk : nv;
                 if (lane == 0) newsc[is_k ? 0 : 1] = sc;
             }
@@ -765,7 +787,8 @@ __global__ __launch_bounds__(RT) void attn_prefill_kernel(AttnArgs p, int rows_p
     __shared__ int posq[PQ];
     __shared__ float ksc[KCH], vsc[KCH];
     const size_t seq = p.seq[r0];
-    const size_t base = seq * p.max_seq * p.hkv + (size_t)kh * hd;
+    const size_t tok0 = p.ro.map.slot(seq, j0);  // cache slot of this chunk's first key
+    const size_t base = tok0 * p.hkv + (size_t)kh * hd;
     // Every global read is issued before the first use.
     float4 qv[NP], kf[KV8 ? 1 : NP], vf[KV8 ? 1 : NP];
     uint32_t k8[KV8 ? NP : 1], v8[KV8 ? NP : 1];
@@ -776,7 +799,7 @@ __global__ __launch_bounds__(RT) void attn_prefill_kernel(AttnArgs p, int rows_p
                          : make_float4(0.f, 0.f, 0.f, 0.f);
         const int k = idx / hd4;  // the same piece index over the K / V chunk
         const bool live = k < nk;
-        const size_t o = base + (size_t)(j0 + k) * p.hkv + c;
+        const size_t o = base + (size_t)k * p.hkv + c;
         if constexpr (KV8) {
             k8[u] = live ? *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.kc) + o) : 0u;
             v8[u] = live ? *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.vc) + o) : 0u;
@@ -788,7 +811,7 @@ __global__ __launch_bounds__(RT) void attn_prefill_kernel(AttnArgs p, int rows_p
     float scl = 0.0f;
     if constexpr (KV8) {
         const int k = tid < KCH ? tid : tid - KCH;
-        if (tid < 2 * KCH && k < nk) scl = (tid < KCH ? p.ks : p.vs)[(seq * p.max_seq + j0 + k) * p.nkv + kh];
+        if (tid < 2 * KCH && k < nk) scl = (tid < KCH ? p.ks : p.vs)[(tok0 + k) * p.nkv + kh];
     }
     if (tid < PQ) {
         const int i = tid / G;
@@ -1079,7 +1102,15 @@ struct bh_qwen3 {
     uint32_t* head = nullptr;
     float* shead = nullptr;
     void *kc = nullptr, *vc = nullptr;  // f32 or int8 elements
-    float *kscale = nullptr, *vscale = nullptr;  // KV8: [L][max_batch][max_seq][nkv]
+    float *kscale = nullptr, *vscale = nullptr;  // KV8: [L][slots][nkv]
+    // Cache addressing: slabs (kv_bs 0, slots = max_batch * max_seq) or a
+    // paged pool of kv_nblk blocks of kv_bs positions (slots = kv_nblk *
+    // kv_bs) through the block table bt [max_batch][kv_max_bt] (host mirror
+    // bt_host; BH_QWEN3_NO_BLOCK marks an unallocated entry).
+    uint32_t kv_bs = 0, kv_nblk = 0, kv_max_bt = 0;
+    size_t slots = 0;
+    uint32_t* bt = nullptr;
+    std::vector<uint32_t> bt_host;
     float *kclip = nullptr, *vclip = nullptr;    // KV8: [L][nkv], FLT_MAX = no clipping
     float2* rope_cs = nullptr;                   // [max_seq][hd/2] rotation (cos, sin)
     size_t layer_kv = 0;  // elements per layer per cache
@@ -1263,7 +1294,7 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
         const bh_qwen3::Layer& Ly = e->L[l];
         void* kc = static_cast<uint8_t*>(e->kc) + l * e->layer_kv * e->kv_elem;
         void* vc = static_cast<uint8_t*>(e->vc) + l * e->layer_kv * e->kv_elem;
-        const size_t lsc = (size_t)l * e->max_batch * e->max_seq * nkv;
+        const size_t lsc = (size_t)l * e->slots * nkv;
         float* ksl = e->c.kv_int8 ? e->kscale + lsc : nullptr;
         float* vsl = e->c.kv_int8 ? e->vscale + lsc : nullptr;
         // Residual stream ping-pongs between res and res2 (two swaps per
@@ -1299,7 +1330,8 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
         std::swap(cur, nxt);
         RopeArgs ra{e->qkv, e->q, kc, vc, ksl, vsl, e->kclip + (size_t)l * nkv, e->vclip + (size_t)l * nkv, Ly.qn,
                     Ly.kn, pos, seq, nh, nkv, hd, (int)e->hq, (int)e->hkv, (int)e->max_seq, (int)c.qk_norm,
-                    c.rms_eps, c.rope_theta, e->rope_cs};
+                    c.rms_eps, c.rope_theta, e->rope_cs,
+                    KvMap{e->bt, (int)e->kv_max_bt, (int)e->kv_bs, (int)e->kv_nblk, (int)e->max_seq}};
         AttnArgs aa{e->q, kc, vc, ksl, vsl, pos, seq, e->part_o, e->part_ml, nh, nkv, hd, (int)e->hq,
                     (int)e->hkv, (int)e->max_seq, splits, scale, ra};
         const dim3 agrid(rows, nkv, splits);
@@ -1493,6 +1525,24 @@ uint64_t fnv1a(const std::string& s) {
     return h;
 }
 
+// Paged pool: every block the first `npos` positions of sequences 0..batch-1
+// use must be allocated (inside the pool) and owned by one sequence only.
+int check_blocks(const bh_qwen3* e, uint32_t batch, uint64_t npos, const char* who) {
+    if (!e->kv_bs) return BH_OK;
+    const uint64_t nb = (npos + e->kv_bs - 1) / e->kv_bs;
+    std::vector<uint8_t> seen(e->kv_nblk, 0);
+    for (uint32_t b = 0; b < batch; ++b)
+        for (uint64_t i = 0; i < nb; ++i) {
+            const uint32_t blk = e->bt_host[(size_t)b * e->kv_max_bt + i];
+            if (blk >= e->kv_nblk)
+                return fail(BH_ERR_INVALID, "%s: sequence %u position %llu has no block (table entry %u, pool of %u)",
+                            who, b, (unsigned long long)(i * e->kv_bs), blk, e->kv_nblk);
+            if (seen[blk]++)
+                return fail(BH_ERR_INVALID, "%s: block %u is used by two sequences (or twice by one)", who, blk);
+        }
+    return BH_OK;
+}
+
 int sync(bh_qwen3* e) {
     BH_HIP(hipStreamSynchronize(e->stream), "stream synchronize");
     return BH_OK;
@@ -1518,6 +1568,13 @@ int bh_qwen3_create(const bh_qwen3_config* cfg, uint32_t max_batch, uint32_t max
     if (!max_batch || !max_seq || max_rows < max_batch)
         return fail(BH_ERR_INVALID, "bh_qwen3_create: max_batch %u max_seq %u max_rows %u", max_batch, max_seq, max_rows);
     if (max_seq > 65536) return fail(BH_ERR_INVALID, "bh_qwen3_create: max_seq %u above 65536", max_seq);
+    if (c.kv_block_size % KCH || (!c.kv_block_size && c.kv_num_blocks))
+        return fail(BH_ERR_INVALID, "bh_qwen3_create: kv_block_size %u must be a multiple of %d (0: slabs, then "
+                    "kv_num_blocks 0)", c.kv_block_size, KCH);
+    if (c.kv_block_size && (uint64_t)(c.kv_num_blocks ? c.kv_num_blocks : max_batch * ((max_seq + c.kv_block_size - 1) /
+                                                                                      c.kv_block_size)) *
+                                   c.kv_block_size > (1ull << 31))
+        return fail(BH_ERR_INVALID, "bh_qwen3_create: paged pool above 2^31 slots");
     if (hipSetDevice(device) != hipSuccess) return fail(BH_ERR_HIP, "bh_qwen3_create: hipSetDevice(%d)", device);
     bh_qwen3* e = new bh_qwen3();
     e->c = c;
@@ -1547,7 +1604,15 @@ int bh_qwen3_create(const bh_qwen3_config* cfg, uint32_t max_batch, uint32_t max
             (rc = dalloc(e, &Ly.wdown, d * ff / 4)) || (rc = dalloc(e, &Ly.sdown, d)))
             return bail(rc);
     }
-    e->layer_kv = (size_t)max_batch * max_seq * e->hkv;
+    if (c.kv_block_size) {
+        e->kv_bs = c.kv_block_size;
+        e->kv_max_bt = (max_seq + e->kv_bs - 1) / e->kv_bs;
+        e->kv_nblk = c.kv_num_blocks ? c.kv_num_blocks : max_batch * e->kv_max_bt;
+        e->slots = (size_t)e->kv_nblk * e->kv_bs;
+    } else {
+        e->slots = (size_t)max_batch * max_seq;
+    }
+    e->layer_kv = e->slots * e->hkv;
     e->kv_elem = c.kv_int8 ? 1 : 4;
     e->tmpw_floats = std::max<uint64_t>(std::max<uint64_t>((uint64_t)e->W * d, 2 * ff * d), d * std::max<uint64_t>(hq, ff));
     if (!c.tie_embeddings) e->tmpw_floats = std::max<uint64_t>(e->tmpw_floats, (uint64_t)c.vocab * d);
@@ -1556,8 +1621,9 @@ int bh_qwen3_create(const bh_qwen3_config* cfg, uint32_t max_batch, uint32_t max
         (rc = dalloc(e, &e->head, (uint64_t)c.vocab * d / 4)) || (rc = dalloc(e, &e->shead, c.vocab)) ||
         (rc = dalloc(e, (uint8_t**)&e->kc, e->layer_kv * c.n_layers * e->kv_elem)) ||
         (rc = dalloc(e, (uint8_t**)&e->vc, e->layer_kv * c.n_layers * e->kv_elem)) ||
-        (rc = dalloc(e, &e->kscale, c.kv_int8 ? (uint64_t)c.n_layers * max_batch * max_seq * c.n_kv_heads : 1)) ||
-        (rc = dalloc(e, &e->vscale, c.kv_int8 ? (uint64_t)c.n_layers * max_batch * max_seq * c.n_kv_heads : 1)) ||
+        (rc = dalloc(e, &e->kscale, c.kv_int8 ? (uint64_t)c.n_layers * e->slots * c.n_kv_heads : 1)) ||
+        (rc = dalloc(e, &e->vscale, c.kv_int8 ? (uint64_t)c.n_layers * e->slots * c.n_kv_heads : 1)) ||
+        (rc = dalloc(e, &e->bt, (uint64_t)max_batch * std::max<uint32_t>(e->kv_max_bt, 1))) ||
         (rc = dalloc(e, &e->kclip, (uint64_t)c.n_layers * c.n_kv_heads)) ||
         (rc = dalloc(e, &e->vclip, (uint64_t)c.n_layers * c.n_kv_heads)) ||
         (rc = dalloc(e, &e->rope_cs, (uint64_t)max_seq * (c.head_dim / 2))) ||
@@ -1582,6 +1648,16 @@ int bh_qwen3_create(const bh_qwen3_config* cfg, uint32_t max_batch, uint32_t max
     if (hipMemcpy(e->kclip, clip.data(), clip.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(e->vclip, clip.data(), clip.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
         return bail(fail(BH_ERR_HIP, "bh_qwen3_create: upload"));
+    if (e->kv_bs) {
+        // Default table: sequence b owns blocks b * max_bt .. b * max_bt +
+        // max_bt - 1 when the pool holds them (the slab layout, paged), else
+        // nothing is allocated until bh_qwen3_set_block_table.
+        e->bt_host.assign((size_t)max_batch * e->kv_max_bt, BH_QWEN3_NO_BLOCK);
+        if ((uint64_t)e->kv_nblk >= (uint64_t)max_batch * e->kv_max_bt)
+            for (size_t i = 0; i < e->bt_host.size(); ++i) e->bt_host[i] = (uint32_t)i;
+        if (hipMemcpy(e->bt, e->bt_host.data(), e->bt_host.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+            return bail(fail(BH_ERR_HIP, "bh_qwen3_create: block table upload"));
+    }
     std::vector<uint32_t> seq(max_batch);
     for (uint32_t b = 0; b < max_batch; ++b) seq[b] = b;
     if (hipMemcpy(e->seq_dec, seq.data(), max_batch * 4, hipMemcpyHostToDevice) != hipSuccess)
@@ -1783,6 +1859,7 @@ int bh_qwen3_prefill(bh_qwen3* e, const uint32_t* tokens, uint32_t batch, uint32
         return fail(BH_ERR_INVALID, "bh_qwen3_prefill: batch %u (max %u), len %u (max %u)", batch, e->max_batch, len,
                     e->max_seq);
     e->nofuse = false;  // the decode flag does not carry over
+    BH_TRY(check_blocks(e, batch, len, "bh_qwen3_prefill"));
     for (uint64_t i = 0; i < (uint64_t)batch * len; ++i)
         if (tokens[i] >= e->c.vocab) return fail(BH_ERR_INVALID, "bh_qwen3_prefill: token %u outside the vocabulary (%u)", tokens[i], e->c.vocab);
     (void)hipSetDevice(e->device);
@@ -1834,6 +1911,7 @@ int bh_qwen3_decode(bh_qwen3* e, uint32_t steps, uint32_t flags, uint32_t* out) 
     if ((uint64_t)e->prompt_len + e->decoded + steps > e->max_seq)
         return fail(BH_ERR_INVALID, "bh_qwen3_decode: %u more steps exceed max_seq %u", steps, e->max_seq);
     if (!steps) return BH_OK;
+    BH_TRY(check_blocks(e, e->batch, (uint64_t)e->prompt_len + e->decoded + steps, "bh_qwen3_decode"));
     (void)hipSetDevice(e->device);
     const int b = (int)e->batch;
     e->nofuse = (flags & BH_QWEN3_UNFUSED) != 0;
@@ -1888,19 +1966,65 @@ int bh_qwen3_kv_read(bh_qwen3* e, uint32_t layer, uint32_t seq, uint32_t which, 
         (uint64_t)pos0 + npos > e->max_seq)
         return fail(BH_ERR_INVALID, "bh_qwen3_kv_read: bad argument");
     (void)hipSetDevice(e->device);
-    const size_t tok0 = (size_t)seq * e->max_seq + pos0;
+    const size_t nkv = e->c.n_kv_heads, row = (size_t)e->hkv * e->kv_elem;
     const uint8_t* cache = static_cast<const uint8_t*>(which ? e->vc : e->kc) + (size_t)layer * e->layer_kv * e->kv_elem;
-    BH_TRY(check_span(e, cache + tok0 * e->hkv * e->kv_elem, (size_t)npos * e->hkv * e->kv_elem, "kv read"));
-    BH_HIP(hipMemcpyAsync(data, cache + tok0 * e->hkv * e->kv_elem, (size_t)npos * e->hkv * e->kv_elem,
-                          hipMemcpyDeviceToHost, e->stream),
-           "kv read");
-    if (e->c.kv_int8 && scales) {
-        const size_t nkv = e->c.n_kv_heads;
-        const float* sc = (which ? e->vscale : e->kscale) + (size_t)layer * e->max_batch * e->max_seq * nkv;
-        BH_TRY(check_span(e, sc + tok0 * nkv, (size_t)npos * nkv * 4, "kv scale read"));
-        BH_HIP(hipMemcpyAsync(scales, sc + tok0 * nkv, (size_t)npos * nkv * 4, hipMemcpyDeviceToHost, e->stream),
-               "kv scale read");
+    const float* sc = (which ? e->vscale : e->kscale) + (size_t)layer * e->slots * nkv;
+    // Runs of positions that are contiguous in the cache: the whole range
+    // with slabs, one block at a time in a paged pool.
+    for (uint32_t p = pos0; p < pos0 + npos;) {
+        size_t tok;
+        uint32_t run;
+        if (e->kv_bs) {
+            const uint32_t blk = e->bt_host[(size_t)seq * e->kv_max_bt + p / e->kv_bs];
+            if (blk >= e->kv_nblk)
+                return fail(BH_ERR_INVALID, "bh_qwen3_kv_read: position %u of sequence %u has no block", p, seq);
+            tok = (size_t)blk * e->kv_bs + p % e->kv_bs;
+            run = std::min(pos0 + npos - p, e->kv_bs - p % e->kv_bs);
+        } else {
+            tok = (size_t)seq * e->max_seq + p;
+            run = pos0 + npos - p;
+        }
+        uint8_t* dst = static_cast<uint8_t*>(data) + (size_t)(p - pos0) * row;
+        BH_TRY(check_span(e, cache + tok * row, (size_t)run * row, "kv read"));
+        BH_HIP(hipMemcpyAsync(dst, cache + tok * row, (size_t)run * row, hipMemcpyDeviceToHost, e->stream), "kv read");
+        if (e->c.kv_int8 && scales) {
+            BH_TRY(check_span(e, sc + tok * nkv, (size_t)run * nkv * 4, "kv scale read"));
+            BH_HIP(hipMemcpyAsync(scales + (size_t)(p - pos0) * nkv, sc + tok * nkv, (size_t)run * nkv * 4,
+                                  hipMemcpyDeviceToHost, e->stream),
+                   "kv scale read");
+        }
+        p += run;
     }
+    return sync(e);
+}
+
+int bh_qwen3_kv_pool(bh_qwen3* e, uint32_t layer, uint32_t which, void** pool, uint64_t* pool_words, float** scales,
+                     uint64_t* n_scales) {
+    if (!e || !pool || !pool_words || !scales || !n_scales || which > 1 || layer >= e->c.n_layers)
+        return fail(BH_ERR_INVALID, "bh_qwen3_kv_pool: bad argument");
+    *pool = static_cast<uint8_t*>(which ? e->vc : e->kc) + (size_t)layer * e->layer_kv * e->kv_elem;
+    *pool_words = e->layer_kv * e->kv_elem / 4;
+    *scales = e->c.kv_int8 ? (which ? e->vscale : e->kscale) + (size_t)layer * e->slots * e->c.n_kv_heads : nullptr;
+    *n_scales = e->c.kv_int8 ? e->slots * e->c.n_kv_heads : 0;
+    return BH_OK;
+}
+
+int bh_qwen3_set_block_table(bh_qwen3* e, const uint32_t* table, uint32_t rows, uint32_t max_blocks_per_seq) {
+    if (!e || !table) return fail(BH_ERR_INVALID, "bh_qwen3_set_block_table: null argument");
+    if (!e->kv_bs) return fail(BH_ERR_INVALID, "bh_qwen3_set_block_table: the engine keeps slabs (kv_block_size 0)");
+    if (rows > e->max_batch || max_blocks_per_seq != e->kv_max_bt)
+        return fail(BH_ERR_INVALID, "bh_qwen3_set_block_table: %u rows of %u blocks (engine: up to %u rows of %u)",
+                    rows, max_blocks_per_seq, e->max_batch, e->kv_max_bt);
+    for (uint64_t i = 0; i < (uint64_t)rows * max_blocks_per_seq; ++i)
+        if (table[i] >= e->kv_nblk && table[i] != BH_QWEN3_NO_BLOCK)
+            return fail(BH_ERR_INVALID, "bh_qwen3_set_block_table: entry %u outside the pool of %u blocks", table[i],
+                        e->kv_nblk);
+    (void)hipSetDevice(e->device);
+    std::copy(table, table + (size_t)rows * max_blocks_per_seq, e->bt_host.begin());
+    std::fill(e->bt_host.begin() + (size_t)rows * max_blocks_per_seq, e->bt_host.end(), BH_QWEN3_NO_BLOCK);
+    // Ordered on the engine's stream after any step still reading the table.
+    BH_HIP(hipMemcpyAsync(e->bt, e->bt_host.data(), e->bt_host.size() * 4, hipMemcpyHostToDevice, e->stream),
+           "block table upload");
     return sync(e);
 }
 

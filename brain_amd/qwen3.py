@@ -14,11 +14,13 @@ import numpy as np
 from ._lib import Qwen3ConfigT, check, load
 
 QWEN3_0_6B = dict(vocab=151936, n_layers=28, d_model=1024, n_heads=16, n_kv_heads=8, head_dim=128,
-                  d_ff=3072, rope_theta=1.0e6, rms_eps=1e-6, tie_embeddings=1, qk_norm=1, kv_int8=0)
+                  d_ff=3072, rope_theta=1.0e6, rms_eps=1e-6, tie_embeddings=1, qk_norm=1, kv_int8=0,
+                  kv_block_size=0, kv_num_blocks=0)
 """QwenConfig::qwen3_0_6b (crates/qwen3/src/config.rs:100-118)."""
 
 EAGER = 1
 UNFUSED = 2
+NO_BLOCK = 0xFFFFFFFF
 
 
 class Qwen3Engine:
@@ -26,7 +28,7 @@ class Qwen3Engine:
         self.cfg = dict(QWEN3_0_6B, **cfg) if cfg is not QWEN3_0_6B else dict(cfg)
         c = Qwen3ConfigT()
         for k in ("vocab", "n_layers", "d_model", "n_heads", "n_kv_heads", "head_dim", "d_ff", "tie_embeddings", "qk_norm",
-                  "kv_int8"):
+                  "kv_int8", "kv_block_size", "kv_num_blocks"):
             setattr(c, k, int(self.cfg[k]))
         c.rope_theta, c.rms_eps = float(self.cfg["rope_theta"]), float(self.cfg["rms_eps"])
         self._h = C.c_void_p()
@@ -72,6 +74,20 @@ class Qwen3Engine:
         """int8 KV ceilings per kv head for layer `layer`, K (which=0) or V (1)."""
         clip = np.ascontiguousarray(clip, dtype=np.float32)
         check(load().bh_qwen3_set_kv_clip(self._h, layer, which, clip.ctypes.data))
+
+    def set_block_table(self, table):
+        """Paged pool (kv_block_size > 0): table [rows, max_blocks_per_seq] of
+        physical blocks (NO_BLOCK = unallocated), as the reference's
+        BlockAllocator hands them out."""
+        t = np.ascontiguousarray(table, dtype=np.uint32)
+        check(load().bh_qwen3_set_block_table(self._h, t.ctypes.data, t.shape[0], t.shape[1]))
+
+    def kv_pool(self, layer, which):
+        """Device pointers of one layer's K/V pool: (pool, pool_words, scales, n_scales)."""
+        pool, words, sc, ns = C.c_void_p(), C.c_uint64(), C.c_void_p(), C.c_uint64()
+        check(load().bh_qwen3_kv_pool(self._h, layer, which, C.byref(pool), C.byref(words), C.byref(sc),
+                                      C.byref(ns)))
+        return pool.value, words.value, sc.value, ns.value
 
     def autotune(self, reps=8):
         """Measure GEMV vs tile for every linear shape at row buckets up to max_batch."""

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define BH_ABI_VERSION 1
+#define BH_ABI_VERSION 2
 
 enum {
     BH_OK = 0,
@@ -217,6 +217,12 @@ int bh_f32_to_bf16(void* stream, const float* x, uint16_t* out, uint64_t n);
  * blocks*4*iters*4*65536. The MI355X counterpart of the `roof_dp4a` probe
  * (crates/kernels/wgsl/roof_dp4a.wgsl:28-63, crates/gpu-core/src/roof.rs:99-130). */
 int bh_roof_mfma_i8(void* stream, uint32_t blocks, uint32_t iters, int32_t* out);
+/* HBM read roof probe (the bandwidth half of crates/gpu-core/src/roof.rs:458-490):
+ * `blocks` workgroups of 256 threads read `bytes` (a multiple of 16, 16-byte
+ * aligned) from `src` with 16-byte vector loads, 8 in flight per thread, and
+ * write one folded word per thread to `out` (blocks*256 words). Also the
+ * calibration kernel for the FETCH_SIZE counter (its loads are the GEMV's). */
+int bh_roof_hbm_read(void* stream, const void* src, uint64_t bytes, uint32_t blocks, uint32_t* out);
 
 /* ======================================================================
  * B. backend_api::Backend as a C ABI (crates/backend-api/src/lib.rs:696-908).
@@ -400,12 +406,18 @@ int bh_st_describe(const char* path, const char* name, int* dtype, uint64_t* sha
  *    SwiGLU -> int8 down -> residual; then RMSNorm, the int8 head and a
  *    greedy argmax on the device. Activations f32; every linear quantizes its
  *    input per token (max_abs_row + quant_pack semantics) and runs
- *    bh_matmul_i8 with f32 output. The KV cache is one contiguous
- *    [max_seq, kv_dim] slab per (layer, sequence) in one of two modes:
- *    f32 (kv_int8 = 0), or int8 codes (kv_int8 = 1) with one f32 scale per
- *    (token, kv head), min(max|x|, clip)/127 (1 when that is 0), where the
- *    clip ceilings are per (layer, kv head) and default to FLT_MAX (no
- *    clipping; see bh_qwen3_set_kv_clip).
+ *    bh_matmul_i8 with f32 output. The KV cache holds, per layer, K and V
+ *    rows [slot][kv_dim] in one of two modes: f32 (kv_int8 = 0), or int8
+ *    codes (kv_int8 = 1, 4 per u32 word) with one f32 scale per (slot, kv
+ *    head) [slot][n_kv_heads], min(max|x|, clip)/127 (1 when that is 0),
+ *    where the clip ceilings are per (layer, kv head) and default to FLT_MAX
+ *    (no clipping; see bh_qwen3_set_kv_clip). Slots are either one
+ *    contiguous slab of max_seq per sequence (kv_block_size = 0), or the
+ *    reference's paged pool (crates/qwen3/src/serve.rs:349-356,
+ *    paged_kv_append_i8_clipped_batched.wgsl:46-77): kv_num_blocks blocks of
+ *    kv_block_size slots, position p of sequence b at slot
+ *    table[b][p / kv_block_size] * kv_block_size + p % kv_block_size
+ *    (bh_qwen3_set_block_table).
  * ====================================================================== */
 typedef struct bh_qwen3 bh_qwen3;
 
@@ -418,6 +430,9 @@ typedef struct {
     uint32_t qk_norm;        /* 1: per-head RMSNorm of q and k before RoPE */
     uint32_t kv_int8;        /* engine option: 1 = int8 KV cache with per-(token, kv head) scales
                                 (paged_kv_append_i8_clipped_batched / paged_decode_{scores,apply}_i8_batched) */
+    uint32_t kv_block_size;  /* engine option: 0 = one slab per sequence; else a paged pool of blocks of
+                                this many positions (a multiple of 32) addressed through a block table */
+    uint32_t kv_num_blocks;  /* paged: blocks in the pool (0: max_batch * ceil(max_seq / kv_block_size)) */
 } bh_qwen3_config;
 
 /* Engine for up to max_batch sequences of max_seq positions each; prefill
@@ -469,6 +484,25 @@ int bh_qwen3_lengths(bh_qwen3* e, uint32_t* len, uint32_t batch);
  * A validation aid: the codes and scales are the engine's own. */
 int bh_qwen3_kv_read(bh_qwen3* e, uint32_t layer, uint32_t seq, uint32_t which, uint32_t pos0, uint32_t npos,
                      void* data, float* scales);
+/* Paged pool (kv_block_size > 0): the block table, table[rows][max_blocks_per_seq]
+ * (max_blocks_per_seq = ceil(max_seq / kv_block_size)), entry i of row b the
+ * physical block of positions [i * kv_block_size, (i + 1) * kv_block_size) of
+ * sequence b, or BH_QWEN3_NO_BLOCK; rows past `rows` become unallocated. The
+ * reference's BlockAllocator hands out such tables; bh_qwen3_prefill and
+ * bh_qwen3_decode refuse to run a sequence whose positions reach a block that
+ * is unallocated or also used by another sequence. Default when the pool
+ * holds max_batch * max_blocks_per_seq blocks: row b owns blocks
+ * b * max_blocks_per_seq + i; otherwise nothing is allocated. */
+#define BH_QWEN3_NO_BLOCK 0xFFFFFFFFu
+int bh_qwen3_set_block_table(bh_qwen3* e, const uint32_t* table, uint32_t rows, uint32_t max_blocks_per_seq);
+/* The device memory of one layer's K (which 0) or V (1) cache: `pool` (f32
+ * rows, or int8 codes 4 per u32 word, [slot][kv_dim], pool_words words) and,
+ * with kv_int8, `scales` [slot][n_kv_heads] (n_scales floats; else NULL, 0).
+ * With a paged pool these are the buffers the reference's paged kernels
+ * (bh_paged_decode_scores_i8 / _apply_i8) read with the same block table.
+ * Valid until bh_qwen3_destroy; writes race with the engine's own. */
+int bh_qwen3_kv_pool(bh_qwen3* e, uint32_t layer, uint32_t which, void** pool, uint64_t* pool_words, float** scales,
+                     uint64_t* n_scales);
 /* int8 KV: per-kv-head ceilings of layer `layer` for K (which 0) or V (1);
  * the scale is min(max|x|, clip)/127. Default FLT_MAX (no clipping), the
  * reference's uncalibrated sentinel. */

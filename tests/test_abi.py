@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(lib, n), n
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
-    assert lib.bh_abi_version() == 1
+    assert lib.bh_abi_version() == 2
 
 
 def test_cost_matches_reference_formula():
