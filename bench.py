@@ -55,6 +55,8 @@ def parse():
     ap.add_argument("--no-qwen3", action="store_true")
     ap.add_argument("--no-dit", action="store_true")
     ap.add_argument("--no-w4a8", action="store_true")
+    ap.add_argument("--qwen3-batch", type=int, default=0,
+                    help="profiling aid: the qwen3 leg at this one batch (f32 KV) only")
     return ap.parse_args()
 
 
@@ -586,7 +588,7 @@ def qwen3_cpu_baseline(budget_s=8.0, ctx=128):
             "sample": f"{steps} greedy int8 decode steps at batch 1 after {ctx} cached positions, random int8 weights"}
 
 
-def bench_qwen3(prompt_len=128, gen=256, batches=(1, 4, 8), cpu=True):
+def bench_qwen3(prompt_len=128, gen=256, batches=(1, 4, 8), cpu=True, kv8_legs=True):
     """Qwen3-0.6B-architecture int8 decoder, random init, greedy.
     Prefill of a random-id prompt, then `gen` decode steps (one HIP graph
     replay each); tok/s = batch * gen / decode wall time."""
@@ -598,7 +600,10 @@ def bench_qwen3(prompt_len=128, gen=256, batches=(1, 4, 8), cpu=True):
            "weights": "random init (device, seeded), int8 per-channel", "prompt_len": prompt_len, "decode_steps": gen,
            "int8_weight_mb_per_step": round(wbytes / 1e6, 1)}
     max_seq = prompt_len + gen + 8
-    for b, kv8, paged in [(b, 0, False) for b in batches] + [(max(batches), 1, False), (max(batches), 1, True)]:
+    legs = [(b, 0, False) for b in batches]
+    if kv8_legs:
+        legs += [(max(batches), 1, False), (max(batches), 1, True)]
+    for b, kv8, paged in legs:
         cfg = dict(c, kv_int8=kv8)
         if paged:
             # The reference's paged pool: blocks of 32 positions in a pool with
@@ -793,7 +798,10 @@ def main():
     if args.only in ("", "quant") and not args.no_quant:
         leg("quant", bench_quant)
     if args.only in ("", "qwen3") and not args.no_qwen3:
-        leg("qwen3", lambda: bench_qwen3(cpu=not args.no_cpu))
+        if args.qwen3_batch:
+            leg("qwen3", lambda: bench_qwen3(batches=(args.qwen3_batch,), cpu=False, kv8_legs=False))
+        else:
+            leg("qwen3", lambda: bench_qwen3(cpu=not args.no_cpu))
     if args.only in ("", "dit") and not args.no_dit:
         leg("dit", bench_dit)
     if args.only in ("", "w4a8") and not args.no_w4a8:
