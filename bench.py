@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on CPU-baseline work")
     ap.add_argument("--only", default="", help="profiling aid: 'decode', 'gemv', 'shapes', 'config0', 'prefill', "
-                    "'quant', 'qwen3', 'dit', 'w4a8' or 'copy' only")
+                    "'quant', 'qwen3', 'dit', 'w4a8', 'hbm' or 'copy' only")
     ap.add_argument("--no-quant", action="store_true")
     ap.add_argument("--no-qwen3", action="store_true")
     ap.add_argument("--no-dit", action="store_true")
@@ -775,6 +775,9 @@ def main():
                                        2048, sink.data_ptr()))
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes": src.numel() * 4, "read_probe_bytes": src.numel() * 4}))
+        return
+    if args.only == "hbm":
+        print(json.dumps({"hbm_read_probe": hbm_read_probe(torch, lib, dev)}))
         return
     if args.only in ("", "decode", "gemv"):
         sets = make_decode_set(torch, dev, gen)
