@@ -319,6 +319,10 @@ int bh_matmul_i8_dyn_noalloc(void* stream, const uint32_t* xq, const uint32_t* w
     size_t need = 0;
     hipError_t e = launch_gemm_i8_noalloc((hipStream_t)stream, xq, wq, sx, sw, bias, out, out_dtype, (int)m, (int)kg,
                                           (int)n, &need);
+    if (e == hipErrorNotReady)
+        return fail(BH_ERR_INVALID,
+                    "bh_matmul_i8_dyn_noalloc: a call on another stream of this GPU is still using the fixed "
+                    "split-K scratch; order the calls (same stream, or wait for the other stream) and retry");
     if (e == hipErrorInvalidValue && need > noalloc_scratch_bytes())
         return fail(BH_ERR_INVALID,
                     "bh_matmul_i8_dyn_noalloc: m=%u kg=%u n=%u needs %zu bytes of split-K scratch, more than the "

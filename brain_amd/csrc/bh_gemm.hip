@@ -1256,20 +1256,35 @@ constexpr int NOALLOC_MAX_DEVICES = 64;
 static std::mutex g_scratch_mu;
 static int* g_scratch_ptr[NOALLOC_MAX_DEVICES];
 
-// Device address of this device's `scratch` (current device), or null.
-static int* scratch_ptr(hipError_t* err) {
+// Overlap guard: the stream of the last call on each device that used the
+// scratch, and an event recorded after that call's kernels. A call from
+// another stream while that event is pending would race on the scratch, so
+// it is refused (hipErrorNotReady) instead. Calls under graph capture are
+// not tracked (their work runs when the graph is launched).
+struct ScratchUse {
+    hipEvent_t ev = nullptr;
+    hipStream_t last = nullptr;
+    bool used = false;
+};
+static ScratchUse g_scratch_use[NOALLOC_MAX_DEVICES];
+
+// Device address of this device's `scratch` (current device, *dev), or
+// null. Caller holds g_scratch_mu.
+static int* scratch_ptr(hipError_t* err, int* dev_out) {
     int dev = 0;
     if ((*err = hipGetDevice(&dev)) != hipSuccess) return nullptr;
     if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) {
         *err = hipErrorInvalidDevice;
         return nullptr;
     }
-    std::lock_guard<std::mutex> g(g_scratch_mu);
     if (!g_scratch_ptr[dev]) {
         void* p = nullptr;
         if ((*err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return nullptr;
+        if ((*err = hipEventCreateWithFlags(&g_scratch_use[dev].ev, hipEventDisableTiming)) != hipSuccess)
+            return nullptr;
         g_scratch_ptr[dev] = static_cast<int*>(p);
     }
+    *dev_out = dev;
     return g_scratch_ptr[dev];
 }
 
@@ -1290,15 +1305,29 @@ hipError_t launch_gemm_i8_noalloc(hipStream_t s, const uint32_t* xq, const uint3
     *need_bytes = tc.splits > 1 ? (size_t)tc.splits * m * n * 4 : 0;
     if (*need_bytes > NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;
     hipError_t err = hipSuccess;
-    int* ws = scratch_ptr(&err);  // the first call on a device looks the address up
+    std::lock_guard<std::mutex> g(g_scratch_mu);  // check, launch and record as one step per host thread
+    int dev = 0;
+    int* ws = scratch_ptr(&err, &dev);  // the first call on a device looks the address up
     if (!ws) return err;
-    if (out_dtype == OUT_I32) return run_gemm<OUT_I32, false, false>(s, al, dma, tc, a, ws);
-    if (out_dtype == OUT_F32) {
-        if (bias) return run_gemm<OUT_F32, true, false>(s, al, dma, tc, a, ws);
-        return run_gemm<OUT_F32, false, false>(s, al, dma, tc, a, ws);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if ((err = hipStreamIsCapturing(s, &cs)) != hipSuccess) return err;
+    ScratchUse& use = g_scratch_use[dev];
+    const bool tracked = tc.splits > 1 && cs == hipStreamCaptureStatusNone;
+    if (tracked && use.used && use.last != s) {
+        const hipError_t q = hipEventQuery(use.ev);
+        if (q == hipErrorNotReady) return hipErrorNotReady;
+        if (q != hipSuccess) return q;
     }
-    if (bias) return run_gemm<OUT_BF16, true, false>(s, al, dma, tc, a, ws);
-    return run_gemm<OUT_BF16, false, false>(s, al, dma, tc, a, ws);
+    if (out_dtype == OUT_I32) err = run_gemm<OUT_I32, false, false>(s, al, dma, tc, a, ws);
+    else if (out_dtype == OUT_F32) err = bias ? run_gemm<OUT_F32, true, false>(s, al, dma, tc, a, ws)
+                                              : run_gemm<OUT_F32, false, false>(s, al, dma, tc, a, ws);
+    else err = bias ? run_gemm<OUT_BF16, true, false>(s, al, dma, tc, a, ws)
+                    : run_gemm<OUT_BF16, false, false>(s, al, dma, tc, a, ws);
+    if (err != hipSuccess || !tracked) return err;
+    if ((err = hipEventRecord(use.ev, s)) != hipSuccess) return err;
+    use.last = s;
+    use.used = true;
+    return hipSuccess;
 }
 
 hipError_t launch_gemm_i8_static(hipStream_t s, const uint32_t* xq, const uint32_t* wq, float ssx, float ssw,

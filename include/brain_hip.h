@@ -111,9 +111,13 @@ int bh_matmul_i8_dyn(void* stream, const uint32_t* xq, const uint32_t* wq, const
  * library holds on each GPU until the process ends (instead of the per-stream
  * workspace bh_matmul_i8_dyn grows). A shape whose slabs exceed 32 MiB
  * returns BH_ERR_INVALID. Every call on one GPU shares that array: calls
- * that overlap on one GPU (two streams) race and must be serialized by the
- * caller. The slabs are fully overwritten before they are read, so nothing
- * needs clearing between calls. */
+ * that overlap on one GPU (two streams) would race, so a call whose shape
+ * uses the array returns BH_ERR_INVALID while the last such call, made on
+ * another stream, has not finished (an event recorded after it); calls on
+ * one stream are ordered by the stream. Calls recorded into a HIP graph are
+ * not checked: launching such graphs concurrently races. The slabs are
+ * fully overwritten before they are read, so nothing needs clearing between
+ * calls. */
 int bh_matmul_i8_dyn_noalloc(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx,
                              const float* sw, const float* bias, void* out, int out_dtype, uint32_t m, uint32_t kg,
                              uint32_t n);

@@ -93,3 +93,31 @@ def test_noalloc_rejects_slabs_beyond_scratch(gpu):
     assert "scratch" in _lib.load().bh_last_error().decode()
     torch.cuda.synchronize()
     assert int(out.abs().sum().item()) == 0  # nothing launched
+
+
+def test_noalloc_refuses_an_overlapping_call_from_another_stream(gpu):
+    """The scratch is one array per GPU: while a call that uses it is still
+    queued on one stream (held behind a short spin kernel), a call on another
+    stream is refused; once the first stream is idle the same call runs and
+    matches bh_matmul_i8_dyn."""
+    lib = _lib.load()
+    m, k, n = 128, 3072, 1024  # splits K: uses the scratch
+    ops = operands(m, k, n, 5, gpu)
+    xq, wq, sx, sw, bias = ops
+    a, b = torch.cuda.Stream(), torch.cuda.Stream()
+    out_a = torch.empty(m, n, dtype=torch.float32, device=gpu)
+    out_b = torch.empty(m, n, dtype=torch.float32, device=gpu)
+    args = lambda st, out: (st.cuda_stream, xq.data_ptr(), wq.data_ptr(), sx.data_ptr(), sw.data_ptr(),
+                            bias.data_ptr(), out.data_ptr(), _lib.BH_OUT_F32, m, k // 4, n)
+    with torch.cuda.stream(a):
+        torch.cuda._sleep(20_000_000)           # ~10 ms of spinning ahead of the call on stream a
+    assert lib.bh_matmul_i8_dyn_noalloc(*args(a, out_a)) == 0
+    rc = lib.bh_matmul_i8_dyn_noalloc(*args(b, out_b))
+    assert rc != 0 and "another stream" in lib.bh_last_error().decode()
+    a.synchronize()
+    assert lib.bh_matmul_i8_dyn_noalloc(*args(b, out_b)) == 0
+    b.synchronize()
+    _, want = call(lib.bh_matmul_i8_dyn, ops, m, k, n, _lib.BH_OUT_F32, torch.float32, gpu)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a.view(torch.int32), want.view(torch.int32))
+    assert torch.equal(out_b.view(torch.int32), want.view(torch.int32))
