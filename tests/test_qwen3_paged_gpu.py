@@ -165,3 +165,28 @@ def test_bad_tables_are_refused(gpu):
     with pytest.raises(BrainHipError, match="multiple of 32"):
         Qwen3Engine(dict(cfg, kv_block_size=16), 2, 96)
     e.close()
+
+
+def test_paged_engine_equals_slab_engine_qwen3_0_6b(gpu):
+    """The bench's paged configuration at full size: Qwen3-0.6B shapes, batch 8,
+    128-token prompt, int8 KV in blocks of 32 scattered over a pool with
+    spare blocks, 4 graph decode steps: bit-identical to the slab engine."""
+    from brain_amd.qwen3 import QWEN3_0_6B
+    cfg = dict(QWEN3_0_6B, kv_int8=1)
+    batch, plen, max_seq = 8, 128, 140
+    prompts = np.random.default_rng(12).integers(0, cfg["vocab"], size=(batch, plen))
+    max_bt = -(-max_seq // BS)
+    nblk = batch * max_bt + 16
+    table = np.random.default_rng(13).permutation(nblk)[:batch * max_bt].reshape(batch, max_bt)
+    out = []
+    for paged in (False, True):
+        c = dict(cfg, kv_block_size=BS if paged else 0, kv_num_blocks=nblk if paged else 0)
+        e = Qwen3Engine(c, batch, max_seq, max_rows=batch * plen)
+        if paged:
+            e.set_block_table(table)
+        e.init_random(5)
+        toks = [e.prefill(prompts)] + [e.decode(1)[0] for _ in range(4)]
+        out.append((np.array(toks), e.logits()))
+        e.close()
+    assert np.array_equal(out[0][0], out[1][0])
+    assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
