@@ -109,10 +109,13 @@ def test_noalloc_refuses_an_overlapping_call_from_another_stream(gpu):
     out_b = torch.empty(m, n, dtype=torch.float32, device=gpu)
     args = lambda st, out: (st.cuda_stream, xq.data_ptr(), wq.data_ptr(), sx.data_ptr(), sw.data_ptr(),
                             bias.data_ptr(), out.data_ptr(), _lib.BH_OUT_F32, m, k // 4, n)
+    assert a.cuda_stream != b.cuda_stream
     with torch.cuda.stream(a):
-        torch.cuda._sleep(20_000_000)           # ~10 ms of spinning ahead of the call on stream a
+        torch.cuda._sleep(200_000_000)          # tens of ms or more of spinning ahead of the call on stream a
     assert lib.bh_matmul_i8_dyn_noalloc(*args(a, out_a)) == 0
     rc = lib.bh_matmul_i8_dyn_noalloc(*args(b, out_b))
+    busy = not a.query()                        # still busy now => was busy when the call checked
+    assert busy, "the spin on stream a ended before the second call; lengthen it"
     assert rc != 0 and "another stream" in lib.bh_last_error().decode()
     a.synchronize()
     assert lib.bh_matmul_i8_dyn_noalloc(*args(b, out_b)) == 0
