@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on CPU-baseline work")
     ap.add_argument("--only", default="", help="profiling aid: 'decode', 'gemv', 'shapes', 'config0', 'prefill', "
-                    "'quant', 'qwen3', 'dit', 'w4a8', 'hbm' or 'copy' only")
+                    "'quant', 'qwen3', 'dit', 'w4a8', 'moe', 'hbm' or 'copy' only")
     ap.add_argument("--no-quant", action="store_true")
     ap.add_argument("--no-qwen3", action="store_true")
     ap.add_argument("--no-dit", action="store_true")
@@ -398,6 +398,62 @@ def hbm_read_probe(torch, lib, dev, seg_bytes=256 << 20, nseg=4):
     torch.cuda.empty_cache()
     best["frac_of_8tbs"] = round(best["gbs"] / HBM_PEAK_GBS, 4)
     return best
+
+
+def bench_moe(reps=10, m=16384):
+    """moe_linear_gated_i8 at a long-prefill size (m tokens, one expert's
+    1024 -> 3072 linear), routed fractions 1/8, 1/4 and 1 (from 8192 rows the
+    routed rows are compacted before the GEMM); next to it the dense
+    bh_matmul_i8_dyn of all m rows. Each a graph of `reps` launches (warm
+    weights)."""
+    import torch
+    from brain_amd._lib import BH_OUT_F32, check
+    import brain_amd
+    lib = brain_amd.load()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    k, n, ne, ei = 1024, 3072, 8, 1
+    xq = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=dev, generator=g).view(torch.int32)
+    wq = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev, generator=g).view(torch.int32)
+    sx = torch.empty(m, device=dev).uniform_(0.001, 0.05, generator=g)
+    sw = torch.empty(n, device=dev).uniform_(0.002, 0.02, generator=g)
+    out = torch.empty(m, n, device=dev)
+
+    def timed(fn):
+        gr = torch.cuda.CUDAGraph()
+        st = torch.cuda.Stream()
+        with torch.cuda.stream(st):
+            fn()  # on the capture stream: its per-stream workspace exists before capture
+        torch.cuda.synchronize()
+        with torch.cuda.graph(gr, stream=st):
+            for _ in range(reps):
+                fn()
+        gr.replay()
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        gr.replay()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / reps
+
+    rows = []
+    for frac in (0.125, 0.25, 1.0):
+        gate = torch.full((m, ne), -1.0, device=dev)
+        routed = torch.rand(m, device=dev, generator=g) < frac
+        gate[:, ei] = torch.where(routed, 1.0, -1.0)
+        us = timed(lambda: check(lib.bh_moe_linear_gated_i8(torch.cuda.current_stream().cuda_stream, xq.data_ptr(),
+                                                            wq.data_ptr(), sx.data_ptr(), sw.data_ptr(),
+                                                            gate.data_ptr(), ne, ei, out.data_ptr(), m, k // 4, n)))
+        mr = int(routed.sum().item())
+        rows.append({"routed_rows": mr, "us": round(us, 1), "tops_routed": round(2.0 * mr * k * n / us / 1e6, 1)})
+    dense = timed(lambda: check(lib.bh_matmul_i8_dyn(torch.cuda.current_stream().cuda_stream, xq.data_ptr(),
+                                                     wq.data_ptr(), sx.data_ptr(), sw.data_ptr(), None,
+                                                     out.data_ptr(), BH_OUT_F32, m, k // 4, n)))
+    return {"workload": f"moe_linear_gated_i8 M={m} K={k} N={n}, f32 out", "gated": rows,
+            "dense_all_rows_us": round(dense, 1)}
 
 
 def bench_w4a8(reps=20):
@@ -809,6 +865,8 @@ def main():
         leg("dit", bench_dit)
     if args.only in ("", "w4a8") and not args.no_w4a8:
         leg("w4a8", bench_w4a8)
+    if args.only in ("", "moe") and not args.no_w4a8:
+        leg("moe", bench_moe)
     if args.only:
         print(json.dumps(res))
         return
@@ -892,6 +950,8 @@ def main():
         line["dit_stack"] = res["dit"]
     if "w4a8" in res:
         line["w4a8"] = res["w4a8"]
+    if "moe" in res:
+        line["moe_gated"] = res["moe"]
     if cpu is not None:
         line["gpu_vs_cpu"] = round(value / cpu["value"], 1)
     print(json.dumps(line))

@@ -87,6 +87,13 @@ struct GemmArgs {
     // a wider output (the column split of launch_gemm_i8) writes row r at
     // out + r * ldo; the split-K slabs stay compact ([S][m][n]).
     int ldo = 0;
+    // Row compaction (moe_linear_gated_i8 at prefill sizes): the A rows are
+    // the routed rows only, *m_dev of them (m is then an upper bound that
+    // sizes the grid; tiles past *m_dev exit), and A row r is output row
+    // row_map[r]. Null: m rows, row r is output row r. DMA kernel, f32/bf16
+    // output, no split-K.
+    const int* m_dev = nullptr;
+    const int* row_map = nullptr;
 };
 
 __host__ __device__ __forceinline__ int64_t out_ld(const GemmArgs& a) { return a.ldo ? a.ldo : a.n; }
@@ -384,8 +391,13 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
     const int tile_id = blockIdx.x / S;
     const int split = blockIdx.x - tile_id * S;
     int tm, tn;
-    tile_of(tile_id, gridDim.x / S, tiles_m, tiles_n, tm, tn);
+    // Row compaction: the tiles that hold rows are the first ones, so they go
+    // to the XCDs round-robin (no run-per-XCD remap, which would put them all
+    // on one or two XCDs).
+    tile_of(tile_id, a.m_dev ? 1 : gridDim.x / S, tiles_m, tiles_n, tm, tn);
     const int row0 = tm * BM, col0 = tn * BN;
+    const int mrows = a.m_dev ? *a.m_dev : m;  // rows that exist (row compaction: the routed rows)
+    if (row0 >= mrows) return;
     if (gated_tile_skipped<BM, BN, WM * WN * 64, SPLITK>(a, row0, col0)) return;
     const int kbytes = a.kg * 4;
     const int nk_all = kbytes / DK;
@@ -404,7 +416,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < C::A_LOADS; ++i) {
         const int q = t + C::NT * i, r = q / C::CPR, p = q % C::CPR;
-        const int gr = min(row0 + r, m - 1);
+        const int gr = min(row0 + r, mrows - 1);
         asrc[i] = reinterpret_cast<const uint8_t*>(a.xq) + (int64_t)gr * kbytes + ((p ^ dswz<DK>(r)) << 4);
     }
 #pragma unroll
@@ -444,8 +456,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) float ep_b[HAS_BIAS && EP_COLS ? BN : 1];
     __shared__ float ep_sx[EP_ROWS ? BM : 1];
     __shared__ int ep_off[EP_ROWS ? BM : 1];
+    __shared__ int ep_map[EP_ROWS ? BM : 1];
     float r_sw = 0.0f, r_b = 0.0f, r_sx = 0.0f;
     bool r_off = false;
+    int r_map = 0;
     if constexpr (EP_COLS) {
         if (t < BN && col0 + t < n) {
             r_sw = a.sw[col0 + t];
@@ -453,9 +467,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
         }
     }
     if constexpr (EP_ROWS) {
-        if (t < BM && row0 + t < m) {
+        if (t < BM && row0 + t < mrows) {
             if constexpr (!STATIC) r_sx = a.sx[row0 + t];
             r_off = gated_off(a, row0 + t);
+            r_map = a.row_map ? a.row_map[row0 + t] : row0 + t;
         }
     }
 
@@ -661,6 +676,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
         if (t < BM) {
             ep_sx[t] = r_sx;
             ep_off[t] = r_off;
+            ep_map[t] = r_map;
         }
     }
     __builtin_amdgcn_s_waitcnt(0);  // every DMA and fragment read has landed
@@ -739,8 +755,11 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
                     const int q = q0 + lane, r = q / EP_CPR, c = q % EP_CPR;
                     const v4i v = *reinterpret_cast<const v4i*>(reg + r * EP_PITCH + c * 16);
                     const int grow = wrow0 + i * 32 + r, gcol = wcol0 + c * (16 / ESZ);
-                    if (grow < m && gcol < n)
-                        *reinterpret_cast<v4i*>(reinterpret_cast<uint8_t*>(a.out) + ((int64_t)grow * out_ld(a) + gcol) * ESZ) = v;
+                    if (grow < mrows && gcol < n) {
+                        int orow = grow;
+                        if constexpr (EP_ROWS) orow = ep_map[grow - row0];
+                        *reinterpret_cast<v4i*>(reinterpret_cast<uint8_t*>(a.out) + ((int64_t)orow * out_ld(a) + gcol) * ESZ) = v;
+                    }
                 }
                 __builtin_amdgcn_s_waitcnt(0xC07F);
                 __builtin_amdgcn_wave_barrier();
@@ -768,7 +787,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < C::FM; ++i) {
                 const int row = rbase + i * 32;
-                if (row >= m || col >= n) continue;
+                if (row >= mrows || col >= n) continue;
                 float sxm = 0.0f;
                 bool off = false;
                 if constexpr (EP_ROWS) {
@@ -788,7 +807,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_dma_kernel(GemmArgs a) {
                         if (off) f[q] = 0.0f;
                     }
                 }
-                const int64_t idx = (int64_t)row * out_ld(a) + col;
+                int orow = row;
+                if constexpr (EP_ROWS) orow = ep_map[row - row0];
+                const int64_t idx = (int64_t)orow * out_ld(a) + col;
                 if (vec_ok && col + 3 < n) {
                     if constexpr (OUT == OUT_I32)
                         *reinterpret_cast<v4i*>(reinterpret_cast<int*>(a.out) + idx) = v4i{v[0], v[1], v[2], v[3]};
@@ -1391,12 +1412,107 @@ hipError_t launch_gemm_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
     }
 }
 
+// ---------------------------------------------------------------- routed-row compaction
+// moe_linear_gated_i8 multiplies only the rows routed to its expert
+// (gate[r, e] <= 0 is false; moe_linear_gated_i8.wgsl:66-69). At prefill
+// sizes the GEMM runs on those rows alone: moe_slot_kernel gives each routed
+// row a slot in a dense copy (slots taken with one atomic add per 64 rows,
+// so their order varies from call to call; every row's result is the same
+// bits wherever it sits) and records rowmap[slot] = r, moe_gather_kernel
+// copies the routed rows' codes there and writes the +0 row of every
+// unrouted row; the GEMM
+// reads the packed rows, skips tiles past *count and stores slot k's row to
+// rowmap[k].
+__global__ void moe_count_clear_kernel(int* count) { *count = 0; }
+
+constexpr int MOE_PACK_ROWS = 64;  // rows per block of the slot assignment: one ballot
+
+__global__ __launch_bounds__(64) void moe_slot_kernel(const float* gate, int stride, int col, const float* sx, int m,
+                                                      float* csx, int* rowmap, int* rowpos, int* count) {
+    const int r = blockIdx.x * MOE_PACK_ROWS + threadIdx.x;
+    const bool routed = r < m && !(gate[(int64_t)r * stride + col] <= 0.0f);
+    const unsigned long long bal = __ballot(routed);
+    int base = 0;
+    if (threadIdx.x == 0 && bal) base = atomicAdd(count, __popcll(bal));
+    base = __shfl(base, 0);
+    const int k = base + __popcll(bal & ((1ull << threadIdx.x) - 1ull));
+    if (r < m) rowpos[r] = routed ? k : -1;
+    if (routed) {
+        rowmap[k] = r;
+        csx[k] = sx[r];
+    }
+}
+
+// One block per row: a routed row's codes to its slot, an unrouted row's
+// output row to +0.
+__global__ __launch_bounds__(256) void moe_gather_kernel(const uint32_t* xq, const int* rowpos, int kg, int n,
+                                                         uint32_t* cxq, float* out) {
+    const int r = blockIdx.x;
+    const int k = rowpos[r];
+    if (k >= 0) {
+        const v4i* src = reinterpret_cast<const v4i*>(xq + (int64_t)r * kg);
+        v4i* dst = reinterpret_cast<v4i*>(cxq + (int64_t)k * kg);
+        for (int j = threadIdx.x; j < kg / 4; j += 256) dst[j] = src[j];
+    } else {
+        float* o = out + (int64_t)r * n;
+        if ((n & 3) == 0) {
+            float4* o4 = reinterpret_cast<float4*>(o);
+            for (int j = threadIdx.x; j < n / 4; j += 256) o4[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        } else {
+            for (int j = threadIdx.x; j < n; j += 256) o[j] = 0.0f;
+        }
+    }
+}
+
+// Rows from which the gated GEMM compacts; fewer take the per-tile skip.
+// The compaction costs a gather of the routed rows and the +0 stores of the
+// others (~23 us at 16384 x 3072 f32) and pays off once the dense GEMM needs
+// several waves of tiles. Measured, K=1024 N=3072, per-tile skip -> compacted:
+// M=16384 76 -> 52 us at 1/8 routed, 76 -> 65 us at 1/4, 79 -> 92 us with
+// every row routed; M=8192 44 -> 34 / 45 -> 33 / 46 -> 56 us; M=4096 and
+// below slower at every fraction (25 -> 33 us at 1/8).
+constexpr int MOE_COMPACT_MIN_ROWS = 8192;
+static int moe_compact_env() {
+    static int v = env_int("BH_MOE_COMPACT", 1);
+    return v;
+}
+
 hipError_t launch_gemm_i8_gated(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                                 const float* sw, const float* gate, int gate_stride, int gate_col, float* out, int m,
                                 int kg, int n) {
     GemmArgs a{xq, wq, sx, sw, nullptr, out, m, kg, n, 0.f, 0.f, 1, nullptr, gate, gate_stride, gate_col};
     const bool al = gemm_aligned(xq, wq, kg);
     const bool dma = al && ((kg * 4) % 128 == 0);
+    if (dma && m >= MOE_COMPACT_MIN_ROWS && moe_compact_env()) {
+        // Workspace (its own slot of the stream's workspaces): packed codes
+        // [m][kg], scales [m], rowmap [m], rowpos [m], count. Under a capture
+        // that finds it too small, the uncompacted path below runs instead.
+        const size_t pad = ((size_t)m + 63) / 64 * 64;
+        const size_t ints = (size_t)m * kg + 3 * pad + 64;
+        hipError_t err = hipSuccess;
+        int* ws = splitk_workspace(s, ints, &err, 3);
+        if (ws) {
+            uint32_t* cxq = reinterpret_cast<uint32_t*>(ws);
+            float* csx = reinterpret_cast<float*>(ws + (size_t)m * kg);
+            int* rowmap = ws + (size_t)m * kg + pad;
+            int* rowpos = rowmap + pad;
+            int* count = rowpos + pad;
+            moe_count_clear_kernel<<<1, 1, 0, s>>>(count);
+            if ((err = hipGetLastError()) != hipSuccess) return err;
+            moe_slot_kernel<<<(m + MOE_PACK_ROWS - 1) / MOE_PACK_ROWS, 64, 0, s>>>(
+                gate, gate_stride, gate_col, sx, m, csx, rowmap, rowpos, count);
+            if ((err = hipGetLastError()) != hipSuccess) return err;
+            moe_gather_kernel<<<m, 256, 0, s>>>(xq, rowpos, kg, n, cxq, out);
+            if ((err = hipGetLastError()) != hipSuccess) return err;
+            GemmArgs c{cxq, wq, csx, sw, nullptr, out, m, kg, n, 0.f, 0.f, 1, nullptr};
+            c.m_dev = count;
+            c.row_map = rowmap;
+            TileChoice tc = choose_tiles(m, kg, n);
+            tc.splits = 1;
+            return go_cfg<OUT_F32, false, false>(s, true, true, tc, c);
+        }
+        (void)hipGetLastError();
+    }
     return run_gemm<OUT_F32, false, false>(s, al, dma, choose_tiles(m, kg, n), a);
 }
 

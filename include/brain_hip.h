@@ -166,7 +166,9 @@ int bh_matmul_q4(void* stream, const uint32_t* xq, const uint32_t* wq4, const fl
  * +0 for rows with gate[row * n_experts + e_idx] <= 0 (moe_linear_gated_i8.wgsl:66-69).
  * The GEMV (m <= 32) or MFMA GEMM skips the weights of a launch (GEMV) or
  * output tile (GEMM) with no routed row, multiplies the rest and zeroes the
- * unrouted rows in the epilogue.
+ * unrouted rows in the epilogue. From m = 8192 (K % 32 == 0, 16-byte
+ * aligned xq/wq) the routed rows are first packed into the stream's
+ * workspace and the GEMM runs over them alone.
  * Step name "moe_linear_gated_i8": bindings [xq, wq, sx, sw, gate, out],
  * params [m, kg, n, n_experts, e_idx]. */
 int bh_moe_linear_gated_i8(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,

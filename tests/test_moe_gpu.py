@@ -92,3 +92,33 @@ def test_moe_unrouted_tiles_skip(gpu, m, k, n, pattern):
     if len(on):
         want[on] = o.epilogue(o.acc_exact(xq[on], wq), sx[on], sw)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,k,n,frac", [(8192, 1024, 768, 0.25), (8200, 2048, 1000, 0.125), (8192, 1024, 512, 0.0),
+                                        (8256, 1024, 256, 1.0), (12000, 1024, 256, 0.5)])
+def test_moe_compacted_rows(gpu, m, k, n, frac):
+    """Long prefills (>= 8192 rows): the routed rows are compacted, multiplied
+    as a dense GEMM and scattered back; every routed row equals the dense
+    result bit for bit and every other row is +0 -- with no routed row at
+    all, every row routed, a width that is not a multiple of 8 (the direct
+    epilogue) and a row count that is not a multiple of 64 (a partial last
+    slot-assignment block)."""
+    rng = np.random.default_rng(m + n)
+    n_experts, e_idx = 4, 2
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    sx = o.max_abs_row(x)
+    xq = o.quant_pack(x, sx)
+    wq, sw = o.synth_weights(n, k, m + 1)
+    gate = rng.standard_normal((m, n_experts)).astype(np.float32)
+    routed = rng.random(m) < frac
+    gate[:, e_idx] = np.where(routed, np.abs(gate[:, e_idx]) + 0.1, -np.abs(gate[:, e_idx]))
+    if frac > 0 and m > 7:
+        gate[7, e_idx] = np.nan              # routed (`<= 0` is false)
+        routed[7] = True
+    got = ops.moe_linear_gated_i8(dev_u32(xq, gpu), dev_u32(wq, gpu), torch.from_numpy(sx).to(gpu),
+                                  torch.from_numpy(sw).to(gpu), torch.from_numpy(gate).to(gpu), e_idx).cpu().numpy()
+    rows = np.nonzero(routed)[0]
+    if rows.size:
+        want = o.epilogue(o.acc_exact(xq, wq, rows, np.arange(n)), sx[rows], sw)
+        assert np.array_equal(got[rows].view(np.uint32), want.view(np.uint32))
+    assert (got[~routed].view(np.uint32) == 0).all()
