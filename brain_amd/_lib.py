@@ -67,6 +67,7 @@ SIGNATURES = {
     "bh_matmul_i8": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
     "bh_matmul_i8_gemv": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
     "bh_matmul_i8_dyn": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
+    "bh_matmul_i8_dyn_quant": (i32, [vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, vp, vp]),
     "bh_matmul_i8_dyn_noalloc": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, u32, u32, u32]),
     "bh_paged_kv_append_i8": (i32, [vp, vp, vp, vp, vp, vp, u64, vp, u64, u32, u32, u32, u32]),
     "bh_paged_decode_scores_i8": (i32, [vp, vp, vp, u64, vp, vp, vp, u64, vp] + [u32] * 8 + [f32]),

@@ -38,6 +38,10 @@ hipError_t launch_gemm_i8_static(hipStream_t s, const uint32_t* xq, const uint32
                                  float* out, int m, int kg, int n);
 
 size_t gemm_workspace_ints(int m, int kg, int n);
+size_t gemm_quant_workspace_ints(int m, int kg, int n);
+hipError_t launch_gemm_i8_quant(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
+                                const float* sw, const float* bias, uint16_t* out, int m, int kg, int n, float* sx_out,
+                                uint32_t* xq_out);
 hipError_t launch_gemm_i8_noalloc(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                                   const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n,
                                   size_t* need_bytes);
@@ -307,6 +311,26 @@ int bh_matmul_i8_dyn(void* stream, const uint32_t* xq, const uint32_t* wq, const
     return hip_status(e, "gemm_i8 launch");
 }
 
+int bh_matmul_i8_dyn_quant(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
+                           const float* bias, uint16_t* out, uint32_t m, uint32_t kg, uint32_t n, float* sx_out,
+                           uint32_t* xq_out) {
+    int rc = check_matmul(xq, wq, sx, sw, out, OUT_BF16, m, kg, n, "bh_matmul_i8_dyn_quant");
+    if (rc) return rc;
+    if (n % 4 != 0) return fail(BH_ERR_INVALID, "bh_matmul_i8_dyn_quant: n=%u is not a multiple of 4", n);
+    if (m == 0) return BH_OK;
+    if (n == 0 || !sx_out || !xq_out) return fail(BH_ERR_INVALID, "bh_matmul_i8_dyn_quant: n=%u or null output", n);
+    const uint64_t tiles = (((uint64_t)m + 127) / 128) * (((uint64_t)n + 127) / 128);
+    if (tiles > I32MAX) return fail(BH_ERR_INVALID, "bh_matmul_i8_dyn_quant: %llu tiles", (unsigned long long)tiles);
+    hipError_t e = launch_gemm_i8_quant((hipStream_t)stream, xq, wq, sx, sw, bias, out, (int)m, (int)kg, (int)n,
+                                        sx_out, xq_out);
+    if (e == hipErrorStreamCaptureUnsupported)
+        return fail(BH_ERR_INVALID,
+                    "bh_matmul_i8_dyn_quant: m=%u kg=%u n=%u needs the split-K workspace, which cannot be allocated "
+                    "while the stream is capturing; call bh_reserve_workspace on this stream first",
+                    m, kg, n);
+    return hip_status(e, "gemm_i8_quant launch");
+}
+
 int bh_matmul_i8_dyn_noalloc(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx,
                              const float* sw, const float* bias, void* out, int out_dtype, uint32_t m, uint32_t kg,
                              uint32_t n) {
@@ -335,8 +359,10 @@ int bh_reserve_workspace(void* stream, uint32_t m, uint32_t kg, uint32_t n) {
     if ((uint64_t)kg * 4 > I32MAX || m > I32MAX || n > I32MAX)
         return fail(BH_ERR_INVALID, "bh_reserve_workspace: m=%u kg=%u n=%u out of range", m, kg, n);
     // Both workspaces a GEMM of this shape may take: the split-K slabs of the
-    // int8 GEMM, and for W4A8 (K = 4*kg) the weights expanded to int8.
-    const size_t need[2] = {gemm_workspace_ints((int)m, (int)kg, (int)n),
+    // int8 GEMM (bh_matmul_i8_dyn or bh_matmul_i8_dyn_quant), and for W4A8
+    // (K = 4*kg) the weights expanded to int8.
+    const size_t need[2] = {std::max(gemm_workspace_ints((int)m, (int)kg, (int)n),
+                                     gemm_quant_workspace_ints((int)m, (int)kg, (int)n)),
                             gemm_q4_workspace_ints((int)m, (int)kg * 4, (int)n)};
     for (int slot = 0; slot < 2; ++slot) {
         if (!need[slot]) continue;

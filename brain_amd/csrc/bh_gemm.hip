@@ -1412,6 +1412,149 @@ hipError_t launch_gemm_q4(hipStream_t s, const uint32_t* xq, const uint32_t* wq,
     }
 }
 
+// ---------------------------------------------------------------- GEMM + row quantization
+// A bf16-output matmul_i8_dyn whose output is then quantized per row for the
+// next linear (quant -> matmul_i8_dyn -> quant, as s3dit's block chains its
+// int8 linears: crates/s3dit/src/block.rs:727-790). When the GEMM splits K
+// over 256x256 tiles (a grid that would leave most CUs idle over a long K,
+// e.g. the DiT down projection), one kernel per output row adds the S i32
+// slabs, applies the epilogue, stores the bf16 row and quantizes it from the
+// bf16 values exactly as quantize_rows_bf16_kernel does (same max, scale and
+// rounding): the reduction pass and the quantization's read of the row
+// become one pass. Otherwise the GEMM and quantize_rows_bf16 run one after
+// the other. Splitting a GEMM only to fuse its quantization does not pay:
+// the DiT out projection (1152x3840x3840) as 3-way split 256x256 tiles took
+// 31 us + 12.7 us for the fused reduction, against 36.7 + 5.7 us for its
+// unsplit 256x128 tiles and the quantization.
+
+static int qfuse_env() {
+    static int v = env_int("BH_GEMM_QUANT_FUSE", 1);
+    return v;
+}
+
+// Splits of the fused form for this shape (0: not fused).
+static int qfuse_splits(int m, int kg, int n, bool dma) {
+    if (!dma || n % 8 != 0 || n / 4 > 256 * 8 || !qfuse_env()) return 0;
+    const TileChoice tc = choose_tiles(m, kg, n);
+    return tc.cfg == TILE_256 && tc.splits > 1 && tc.splits <= 4 && column_split(m, kg, n, tc, dma) == 0 ? tc.splits
+                                                                                                        : 0;
+}
+
+size_t gemm_quant_workspace_ints(int m, int kg, int n) {
+    const int S = qfuse_splits(m, kg, n, (kg * 4) % 128 == 0);
+    return S ? (size_t)S * m * n : gemm_workspace_ints(m, kg, n);
+}
+
+// One block per row: 256 threads, NV groups of 4 columns each (n/4 <= 256*NV).
+template <int SN, int NV, bool HAS_BIAS>
+__global__ __launch_bounds__(256) void splitk_reduce_quant_kernel(GemmArgs a, float* sx_out, uint32_t* xq_out) {
+    const int row = blockIdx.x, n = a.n, n4 = n >> 2;
+    const v4i* ws = reinterpret_cast<const v4i*>(a.ws);
+    const int64_t q4 = ((int64_t)a.m * n) >> 2;
+    const int64_t rq = (int64_t)row * n4;
+    v4i acc[NV];
+    // Every slab load first, at clamped groups (n4 >= 1), then the scales.
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int g = min((int)threadIdx.x + 256 * i, n4 - 1);
+        acc[i] = ws[rq + g];
+    }
+#pragma unroll
+    for (int sp = 1; sp < SN; ++sp)
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int g = min((int)threadIdx.x + 256 * i, n4 - 1);
+            const v4i v = ws[(int64_t)sp * q4 + rq + g];
+            acc[i][0] += v[0]; acc[i][1] += v[1]; acc[i][2] += v[2]; acc[i][3] += v[3];
+        }
+    const float sxm = a.sx[row];  // read before this block writes sx_out[row] (they may alias)
+    uint2 hb[NV];
+    float amax = 0.0f;
+    uint2* orow = reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + (int64_t)row * out_ld(a));
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int g = threadIdx.x + 256 * i;
+        hb[i] = make_uint2(0u, 0u);
+        if (g >= n4) continue;
+        const int col = g * 4;
+        const float4 swv = *reinterpret_cast<const float4*>(a.sw + col);
+        float f[4] = {dequant(acc[i][0], sxm, swv.x), dequant(acc[i][1], sxm, swv.y), dequant(acc[i][2], sxm, swv.z),
+                      dequant(acc[i][3], sxm, swv.w)};
+        if constexpr (HAS_BIAS) {
+            const float4 bv = *reinterpret_cast<const float4*>(a.bias + col);
+            f[0] = f[0] + bv.x; f[1] = f[1] + bv.y; f[2] = f[2] + bv.z; f[3] = f[3] + bv.w;
+        }
+        hb[i] = make_uint2(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]));
+        orow[g] = hb[i];
+        const uint32_t w[2] = {hb[i].x, hb[i].y};
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(w[j] << 16)), fabsf(__uint_as_float(w[j] & 0xffff0000u))));
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    __shared__ float red[4];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float sc = fmaxf(mx, 1e-8f) / 127.0f;
+    if (threadIdx.x == 0) sx_out[row] = sc;
+    const float inv = 1.0f / sc;
+    uint32_t* q = xq_out + (int64_t)row * n4;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int g = threadIdx.x + 256 * i;
+        if (g >= n4) continue;
+        q[g] = quant_word(make_float4(__uint_as_float(hb[i].x << 16), __uint_as_float(hb[i].x & 0xffff0000u),
+                                      __uint_as_float(hb[i].y << 16), __uint_as_float(hb[i].y & 0xffff0000u)),
+                          inv);
+    }
+}
+
+template <int SN, bool HAS_BIAS>
+static void launch_reduce_quant(hipStream_t s, const GemmArgs& a, float* sx_out, uint32_t* xq_out) {
+    const int n4 = a.n / 4;
+    if (n4 <= 256) splitk_reduce_quant_kernel<SN, 1, HAS_BIAS><<<a.m, 256, 0, s>>>(a, sx_out, xq_out);
+    else if (n4 <= 512) splitk_reduce_quant_kernel<SN, 2, HAS_BIAS><<<a.m, 256, 0, s>>>(a, sx_out, xq_out);
+    else if (n4 <= 1024) splitk_reduce_quant_kernel<SN, 4, HAS_BIAS><<<a.m, 256, 0, s>>>(a, sx_out, xq_out);
+    else splitk_reduce_quant_kernel<SN, 8, HAS_BIAS><<<a.m, 256, 0, s>>>(a, sx_out, xq_out);
+}
+
+hipError_t launch_quantize_rows_bf16(hipStream_t s, const uint16_t* x, int m, int k, float* sx, uint32_t* xq);
+
+hipError_t launch_gemm_i8_quant(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
+                                const float* sw, const float* bias, uint16_t* out, int m, int kg, int n, float* sx_out,
+                                uint32_t* xq_out) {
+    const bool al = gemm_aligned(xq, wq, kg);
+    const bool dma = al && ((kg * 4) % 128 == 0);
+    const bool vec_ok = ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(sw) |
+                          reinterpret_cast<uintptr_t>(bias)) & 15u) == 0;
+    const int S = vec_ok ? qfuse_splits(m, kg, n, dma) : 0;
+    if (S >= 2 && S <= 4) {
+        hipError_t err = hipSuccess;
+        GemmArgs a{xq, wq, sx, sw, bias, out, m, kg, n, 0.f, 0.f, S, nullptr};
+        a.ws = splitk_workspace(s, (size_t)S * m * n, &err);
+        if (a.ws) {
+            err = go_dma<256, 256, 2, 4, 4, 64, OUT_I32, false, false, true, false, true>(s, a);
+            if (err != hipSuccess) return err;
+            switch (S * 2 + (bias ? 1 : 0)) {
+                case 4: launch_reduce_quant<2, false>(s, a, sx_out, xq_out); break;
+                case 5: launch_reduce_quant<2, true>(s, a, sx_out, xq_out); break;
+                case 6: launch_reduce_quant<3, false>(s, a, sx_out, xq_out); break;
+                case 7: launch_reduce_quant<3, true>(s, a, sx_out, xq_out); break;
+                case 8: launch_reduce_quant<4, false>(s, a, sx_out, xq_out); break;
+                default: launch_reduce_quant<4, true>(s, a, sx_out, xq_out); break;
+            }
+            return hipGetLastError();
+        }
+        if (err != hipErrorStreamCaptureUnsupported) return err == hipSuccess ? hipErrorOutOfMemory : err;
+        (void)hipGetLastError();  // capturing without the workspace: the unfused pair below
+    }
+    hipError_t err = launch_gemm_i8(s, xq, wq, sx, sw, bias, out, OUT_BF16, m, kg, n);
+    if (err != hipSuccess) return err;
+    return launch_quantize_rows_bf16(s, out, m, n, sx_out, xq_out);
+}
+
 // ---------------------------------------------------------------- routed-row compaction
 // moe_linear_gated_i8 multiplies only the rows routed to its expert
 // (gate[r, e] <= 0 is false; moe_linear_gated_i8.wgsl:66-69). At prefill

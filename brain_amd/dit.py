@@ -25,6 +25,12 @@ U(0.5, 1.5) / (73.3 sqrt(K)), which keeps activations O(1) through 30 layers
 (73.3 is the standard deviation of a uniform int8). All compute goes through
 libbrain_hip.so (bh_quantize_rows_bf16, bh_matmul_i8_dyn). torch only
 allocates and captures the step in a HIP graph.
+
+With fuse=True (the default) a linear whose output is quantized next -- the
+out projection, and the down projection of every layer but the last (its
+output is the next layer's input) -- runs as bh_matmul_i8_dyn_quant, which
+gives the same bits as the linear and the quantization called one after the
+other.
 """
 import torch
 
@@ -41,8 +47,8 @@ def linear_ops(m=DIT_M):
 
 
 class DitInt8Stack:
-    def __init__(self, layers=DIT_LAYERS, m=DIT_M, device="cuda", seed=0):
-        self.m, self.layers = m, layers
+    def __init__(self, layers=DIT_LAYERS, m=DIT_M, device="cuda", seed=0, fuse=True):
+        self.m, self.layers, self.fuse = m, layers, fuse
         g = torch.Generator(device=device)
         g.manual_seed(seed)
         self.w = []
@@ -66,16 +72,28 @@ class DitInt8Stack:
         wq, sw = lw[name]
         ops.matmul_i8(xq, wq, self.sx, sw, None, torch.bfloat16, "dyn", out=out)
 
+    def _mm_quant(self, xq, lw, name, out, xq_out):
+        """out = linear(xq), then sx, xq_out = quant(out)."""
+        if self.fuse:
+            wq, sw = lw[name]
+            ops.matmul_i8_quant(xq, wq, self.sx, sw, None, out=out, sx_out=self.sx, xq_out=xq_out)
+        else:
+            self._mm(xq, lw, name, out)
+            ops.quantize_rows_bf16(out, self.sx, xq_out)
+
     def layer(self, i):
         lw, m = self.w[i], self.m
         xq_d = self.xq.view(-1)[: m * DIT_D // 4].view(m, DIT_D // 4)
-        ops.quantize_rows_bf16(self.x, self.sx, xq_d)
+        if i == 0 or not self.fuse:  # otherwise the previous layer's down projection quantized x
+            ops.quantize_rows_bf16(self.x, self.sx, xq_d)
         self._mm(xq_d, lw, "qkv", self.qkv)
-        self._mm(xq_d, lw, "o", self.o)
-        ops.quantize_rows_bf16(self.o, self.sx, xq_d)
+        self._mm_quant(xq_d, lw, "o", self.o, xq_d)
         self._mm(xq_d, lw, "w1", self.h)
         ops.quantize_rows_bf16(self.h, self.sx, self.xq)
-        self._mm(self.xq, lw, "w2", self.x)
+        if i + 1 < self.layers:
+            self._mm_quant(self.xq, lw, "w2", self.x, xq_d)
+        else:
+            self._mm(self.xq, lw, "w2", self.x)
 
     def step(self):
         for i in range(self.layers):

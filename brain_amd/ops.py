@@ -102,6 +102,33 @@ def matmul_i8(xq, wq, sx, sw, bias=None, out_dtype=torch.float32, variant="auto"
     return out
 
 
+def matmul_i8_quant(xq, wq, sx, sw, bias=None, out=None, sx_out=None, xq_out=None):
+    """bf16 out[m,n] = matmul_i8_dyn(xq, wq, sx, sw, bias), then the per-row
+    quantization of out (quantize_rows_bf16) into sx_out [m], xq_out [m, n/4]
+    for the next linear, in one call (split-K GEMMs reduce and quantize in one
+    pass). sx_out may be sx and xq_out may overlap xq."""
+    m, kg = xq.shape
+    n = wq.shape[0]
+    if n % 4:
+        raise ValueError(f"matmul_i8_quant: n={n} is not a multiple of 4")
+    _dev(xq, wq, sx, sw, bias, out, sx_out, xq_out)
+    _need(xq, torch.int32, m * kg, "xq")
+    _need(wq, torch.int32, n * kg, "wq")
+    _need(sx, torch.float32, m, "sx")
+    _need(sw, torch.float32, n, "sw")
+    if bias is not None:
+        _need(bias, torch.float32, n, "bias")
+    out = torch.empty(m, n, device=xq.device, dtype=torch.bfloat16) if out is None else out
+    sx_out = torch.empty(m, device=xq.device, dtype=torch.float32) if sx_out is None else sx_out
+    xq_out = torch.empty(m, n // 4, device=xq.device, dtype=torch.int32) if xq_out is None else xq_out
+    _need(out, torch.bfloat16, m * n, "out")
+    _need(sx_out, torch.float32, m, "sx_out")
+    _need(xq_out, torch.int32, m * n // 4, "xq_out")
+    check(load().bh_matmul_i8_dyn_quant(_stream(), _ptr(xq), _ptr(wq), _ptr(sx), _ptr(sw), _ptr(bias), _ptr(out),
+                                        m, kg, n, _ptr(sx_out), _ptr(xq_out)))
+    return out, sx_out, xq_out
+
+
 def matmul_i8_static(xq, wq, sx, sw, out=None):
     """matmul_i8.wgsl: out = f32(acc) * (sx*sw) with scalar per-tensor scales."""
     m, kg = xq.shape

@@ -102,6 +102,20 @@ int bh_matmul_i8_gemv(void* stream, const uint32_t* xq, const uint32_t* wq, cons
 int bh_matmul_i8_dyn(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
                      const float* bias, void* out, int out_dtype, uint32_t m, uint32_t kg, uint32_t n);
 
+/* bh_matmul_i8_dyn with bf16 output, then bh_quantize_rows_bf16 of that
+ * output for the next linear (sx_out [m], xq_out [m, n/4]), in one call.
+ * The reference runs the two as consecutive steps of a block's int8 linears
+ * (crates/s3dit/src/block.rs:727-790: matmul_i8_dyn, then the next linear's
+ * per-token activation quant); the results are the same bits as those two
+ * calls. n % 4 == 0. When the GEMM's 256x256 grid leaves most of the GPU
+ * idle, K is split and one pass over the partial sums applies the epilogue,
+ * stores `out` and quantizes it. sx_out may be sx and xq_out may overlap xq
+ * (they are written after the GEMM has read its inputs). Uses the stream's
+ * split-K workspace like bh_matmul_i8_dyn (bh_reserve_workspace sizes it). */
+int bh_matmul_i8_dyn_quant(void* stream, const uint32_t* xq, const uint32_t* wq, const float* sx, const float* sw,
+                           const float* bias, uint16_t* out, uint32_t m, uint32_t kg, uint32_t n, float* sx_out,
+                           uint32_t* xq_out);
+
 /* bh_matmul_i8_dyn that allocates nothing. No counterpart in the reference:
  * it is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). Same

@@ -77,3 +77,43 @@ def test_dit_stack_graph_replays_match_eager(gpu):
         torch.cuda.synchronize()
         assert torch.equal(st.x, eager)
     assert torch.isfinite(st.x.float()).all()
+
+
+@pytest.mark.parametrize("m,k,n,bias", [(1152, 10240, 3840, False), (1152, 16384, 6144, True), (1152, 3840, 3840, False),
+                                        (300, 1024, 2048, True), (200, 2048, 1004, False), (7, 1024, 768, False)])
+def test_matmul_i8_quant_equals_matmul_then_quantize(gpu, m, k, n, bias):
+    """bh_matmul_i8_dyn_quant gives the bits of bh_matmul_i8_dyn (bf16) then
+    bh_quantize_rows_bf16: the fused split-K form (the DiT down projection,
+    3-way; a 2-way split with 1536 column groups per row and a bias) and the
+    unfused pair (unsplit GEMMs, n % 8 != 0)."""
+    g = torch.Generator(device=gpu).manual_seed(m + k + n)
+    xq = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=gpu, generator=g).view(torch.int32)
+    wq = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=gpu, generator=g).view(torch.int32)
+    sx = torch.rand(m, device=gpu, generator=g) * 0.02 + 0.001
+    sw = (torch.rand(n, device=gpu, generator=g) + 0.5) / (73.3 * k ** 0.5)
+    b = torch.randn(n, device=gpu, generator=g) if bias else None
+    want = ops.matmul_i8(xq, wq, sx, sw, b, torch.bfloat16, "dyn")
+    want_sx, want_xq = ops.quantize_rows_bf16(want)
+    got, got_sx, got_xq = ops.matmul_i8_quant(xq, wq, sx, sw, b)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    assert torch.equal(got_sx.view(torch.int32), want_sx.view(torch.int32))
+    assert torch.equal(got_xq, want_xq)
+    # In place, as the DiT stack calls it: sx_out is sx and xq_out is the
+    # head of xq's buffer.
+    if n <= k:
+        xq2, sx2 = xq.clone(), sx.clone()
+        ops.matmul_i8_quant(xq2, wq, sx2, sw, b, sx_out=sx2, xq_out=xq2.view(-1)[: m * n // 4].view(m, n // 4))
+        torch.cuda.synchronize()
+        assert torch.equal(sx2.view(torch.int32), want_sx.view(torch.int32))
+        assert torch.equal(xq2.view(-1)[: m * n // 4], want_xq.view(-1))
+
+
+def test_dit_stack_fused_equals_unfused(gpu):
+    fused = dit.DitInt8Stack(layers=3, device=gpu, seed=5)
+    plain = dit.DitInt8Stack(layers=3, device=gpu, seed=5, fuse=False)
+    fused.step()
+    plain.step()
+    torch.cuda.synchronize()
+    for name in ("x", "qkv", "o", "h", "sx", "xq"):
+        assert torch.equal(getattr(fused, name).view(torch.int16), getattr(plain, name).view(torch.int16)), name
