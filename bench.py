@@ -55,6 +55,7 @@ def parse():
     ap.add_argument("--no-qwen3", action="store_true")
     ap.add_argument("--no-dit", action="store_true")
     ap.add_argument("--no-w4a8", action="store_true")
+    ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--qwen3-batch", type=int, default=0,
                     help="profiling aid: the qwen3 leg at this one batch (f32 KV) only")
     return ap.parse_args()
@@ -865,7 +866,7 @@ def main():
         leg("dit", bench_dit)
     if args.only in ("", "w4a8") and not args.no_w4a8:
         leg("w4a8", bench_w4a8)
-    if args.only in ("", "moe") and not args.no_w4a8:
+    if args.only in ("", "moe") and not args.no_moe:
         leg("moe", bench_moe)
     if args.only:
         print(json.dumps(res))

@@ -1558,44 +1558,55 @@ hipError_t launch_gemm_i8_quant(hipStream_t s, const uint32_t* xq, const uint32_
 // ---------------------------------------------------------------- routed-row compaction
 // moe_linear_gated_i8 multiplies only the rows routed to its expert
 // (gate[r, e] <= 0 is false; moe_linear_gated_i8.wgsl:66-69). At prefill
-// sizes the GEMM runs on those rows alone: moe_slot_kernel gives each routed
-// row a slot in a dense copy (slots taken with one atomic add per 64 rows,
-// so their order varies from call to call; every row's result is the same
-// bits wherever it sits) and records rowmap[slot] = r, moe_gather_kernel
-// copies the routed rows' codes there and writes the +0 row of every
-// unrouted row; the GEMM
-// reads the packed rows, skips tiles past *count and stores slot k's row to
-// rowmap[k].
-__global__ void moe_count_clear_kernel(int* count) { *count = 0; }
+// sizes the GEMM runs on those rows alone, packed in row order:
+// moe_rank_kernel ranks each routed row within its 64-row block (one ballot)
+// and counts the block; moe_gather_kernel, one block per row, adds the counts
+// of the blocks before it to get the row's slot, copies its codes and scale
+// there and records rowmap[slot] = r, or writes the +0 row of an unrouted
+// row (row 0's block also stores the total). The GEMM reads the packed rows,
+// skips tiles past the total and stores slot k's row to rowmap[k]. No
+// counter to clear, no atomics.
+constexpr int MOE_PACK_ROWS = 64;  // rows per rank block: one ballot
 
-constexpr int MOE_PACK_ROWS = 64;  // rows per block of the slot assignment: one ballot
-
-__global__ __launch_bounds__(64) void moe_slot_kernel(const float* gate, int stride, int col, const float* sx, int m,
-                                                      float* csx, int* rowmap, int* rowpos, int* count) {
+__global__ __launch_bounds__(64) void moe_rank_kernel(const float* gate, int stride, int col, int m, int* rowpos,
+                                                      int* cnt) {
     const int r = blockIdx.x * MOE_PACK_ROWS + threadIdx.x;
     const bool routed = r < m && !(gate[(int64_t)r * stride + col] <= 0.0f);
     const unsigned long long bal = __ballot(routed);
-    int base = 0;
-    if (threadIdx.x == 0 && bal) base = atomicAdd(count, __popcll(bal));
-    base = __shfl(base, 0);
-    const int k = base + __popcll(bal & ((1ull << threadIdx.x) - 1ull));
-    if (r < m) rowpos[r] = routed ? k : -1;
-    if (routed) {
-        rowmap[k] = r;
-        csx[k] = sx[r];
-    }
+    if (r < m) rowpos[r] = routed ? __popcll(bal & ((1ull << threadIdx.x) - 1ull)) : -1;
+    if (threadIdx.x == 0) cnt[blockIdx.x] = __popcll(bal);
 }
 
-// One block per row: a routed row's codes to its slot, an unrouted row's
-// output row to +0.
-__global__ __launch_bounds__(256) void moe_gather_kernel(const uint32_t* xq, const int* rowpos, int kg, int n,
-                                                         uint32_t* cxq, float* out) {
+__global__ __launch_bounds__(256) void moe_gather_kernel(const uint32_t* xq, const float* sx, const int* rowpos,
+                                                         const int* cnt, int m, int kg, int n, uint32_t* cxq,
+                                                         float* csx, int* rowmap, int* count, float* out) {
     const int r = blockIdx.x;
-    const int k = rowpos[r];
-    if (k >= 0) {
+    const int local = rowpos[r];  // block-uniform, as is r
+    int base = 0;
+    if (local >= 0 || r == 0) {
+        // Row 0 sums every block's count (the total; its own base is 0),
+        // a routed row those of the blocks before its own.
+        const int lim = r == 0 ? (m + MOE_PACK_ROWS - 1) / MOE_PACK_ROWS : r / MOE_PACK_ROWS;
+        int part = 0;
+        for (int i = threadIdx.x; i < lim; i += 256) part += cnt[i];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
+        __shared__ int red[4];
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = part;
+        __syncthreads();
+        const int sum = red[0] + red[1] + red[2] + red[3];
+        if (r == 0 && threadIdx.x == 0) *count = sum;
+        base = r == 0 ? 0 : sum;
+    }
+    if (local >= 0) {
+        const int k = base + local;
         const v4i* src = reinterpret_cast<const v4i*>(xq + (int64_t)r * kg);
         v4i* dst = reinterpret_cast<v4i*>(cxq + (int64_t)k * kg);
         for (int j = threadIdx.x; j < kg / 4; j += 256) dst[j] = src[j];
+        if (threadIdx.x == 0) {
+            csx[k] = sx[r];
+            rowmap[k] = r;
+        }
     } else {
         float* o = out + (int64_t)r * n;
         if ((n & 3) == 0) {
@@ -1609,11 +1620,11 @@ __global__ __launch_bounds__(256) void moe_gather_kernel(const uint32_t* xq, con
 
 // Rows from which the gated GEMM compacts; fewer take the per-tile skip.
 // The compaction costs a gather of the routed rows and the +0 stores of the
-// others (~23 us at 16384 x 3072 f32) and pays off once the dense GEMM needs
-// several waves of tiles. Measured, K=1024 N=3072, per-tile skip -> compacted:
-// M=16384 76 -> 52 us at 1/8 routed, 76 -> 65 us at 1/4, 79 -> 92 us with
-// every row routed; M=8192 44 -> 34 / 45 -> 33 / 46 -> 56 us; M=4096 and
-// below slower at every fraction (25 -> 33 us at 1/8).
+// others (17-23 us at 16384 x 3072 f32) and pays off once the dense GEMM
+// needs several waves of tiles. Measured, K=1024 N=3072, per-tile skip ->
+// compacted: M=16384 78 -> 49 us at 1/8 routed, 78 -> 61 us at 1/4, 79 -> 96
+// us with every row routed; M=8192 45 -> 32 / 46 -> 31 / 46 -> 61 us; M=4096
+// and below slower at every fraction (25 -> 33 us at 1/8).
 constexpr int MOE_COMPACT_MIN_ROWS = 8192;
 static int moe_compact_env() {
     static int v = env_int("BH_MOE_COMPACT", 1);
@@ -1628,10 +1639,11 @@ hipError_t launch_gemm_i8_gated(hipStream_t s, const uint32_t* xq, const uint32_
     const bool dma = al && ((kg * 4) % 128 == 0);
     if (dma && m >= MOE_COMPACT_MIN_ROWS && moe_compact_env()) {
         // Workspace (its own slot of the stream's workspaces): packed codes
-        // [m][kg], scales [m], rowmap [m], rowpos [m], count. Under a capture
-        // that finds it too small, the uncompacted path below runs instead.
+        // [m][kg], scales [m], rowmap [m], rowpos [m], block counts, total.
+        // Under a capture that finds it too small, the uncompacted path below
+        // runs instead.
         const size_t pad = ((size_t)m + 63) / 64 * 64;
-        const size_t ints = (size_t)m * kg + 3 * pad + 64;
+        const size_t ints = (size_t)m * kg + 3 * pad + pad / MOE_PACK_ROWS + 64;
         hipError_t err = hipSuccess;
         int* ws = splitk_workspace(s, ints, &err, 3);
         if (ws) {
@@ -1639,13 +1651,12 @@ hipError_t launch_gemm_i8_gated(hipStream_t s, const uint32_t* xq, const uint32_
             float* csx = reinterpret_cast<float*>(ws + (size_t)m * kg);
             int* rowmap = ws + (size_t)m * kg + pad;
             int* rowpos = rowmap + pad;
-            int* count = rowpos + pad;
-            moe_count_clear_kernel<<<1, 1, 0, s>>>(count);
+            int* cnt = rowpos + pad;  // (m + 63) / 64 block counts
+            int* count = cnt + pad / MOE_PACK_ROWS;
+            moe_rank_kernel<<<(m + MOE_PACK_ROWS - 1) / MOE_PACK_ROWS, 64, 0, s>>>(gate, gate_stride, gate_col, m,
+                                                                                 rowpos, cnt);
             if ((err = hipGetLastError()) != hipSuccess) return err;
-            moe_slot_kernel<<<(m + MOE_PACK_ROWS - 1) / MOE_PACK_ROWS, 64, 0, s>>>(
-                gate, gate_stride, gate_col, sx, m, csx, rowmap, rowpos, count);
-            if ((err = hipGetLastError()) != hipSuccess) return err;
-            moe_gather_kernel<<<m, 256, 0, s>>>(xq, rowpos, kg, n, cxq, out);
+            moe_gather_kernel<<<m, 256, 0, s>>>(xq, sx, rowpos, cnt, m, kg, n, cxq, csx, rowmap, count, out);
             if ((err = hipGetLastError()) != hipSuccess) return err;
             GemmArgs c{cxq, wq, csx, sw, nullptr, out, m, kg, n, 0.f, 0.f, 1, nullptr};
             c.m_dev = count;
