@@ -145,7 +145,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
                 if (u < my_chunks)
 #pragma unroll
                     for (int c = 0; c < CG; ++c)
-                        wf[u][c] = load_k16<ALIGNED>(wp[c], (ks + KSPLIT * u) * 64 + ksub, kbytes);
+                        wf[u][c] = load_k16_nt<ALIGNED>(wp[c], (ks + KSPLIT * u) * 64 + ksub, kbytes);
         } else {
             // Unconditional, and with no masking (this mode needs K % 64 ==
             // 0): slots past this wave's chunks reload its last one (never
@@ -164,8 +164,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
             for (int u = 0; u < U; ++u)
 #pragma unroll
                 for (int c = 0; c < CG; ++c)
-                    wf[u][c] = *reinterpret_cast<const v4i*>(
-                        wp[c] + min(ks + KSPLIT * min(u, last), nchunks - 1) * 64 + ksub);
+                    wf[u][c] = load_w16_nt(wp[c] + min(ks + KSPLIT * min(u, last), nchunks - 1) * 64 + ksub);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -564,7 +563,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
             if (j0 + u < my_chunks)
 #pragma unroll
                 for (int c = 0; c < CG; ++c)
-                    wf[u][c] = load_k16<ALIGNED>(wp[c], (ks + KSPLIT * (j0 + u)) * 64 + ksub, kbytes);
+                    wf[u][c] = load_k16_nt<ALIGNED>(wp[c], (ks + KSPLIT * (j0 + u)) * 64 + ksub, kbytes);
         batch(j0);
     }
     BH_STAMP(2);
