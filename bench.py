@@ -380,13 +380,14 @@ def mfma_roof(torch, lib, dev):
 
 
 def hbm_read_probe(torch, lib, dev, seg_bytes=256 << 20, nseg=4):
-    """The plain streaming-read ceiling on this box (bh_roof_hbm_read: 16-byte
-    loads, as the GEMV's): one graph reading `nseg` distinct 256 MiB segments
-    in turn (1 GiB, so each read is cold), best over four grid sizes."""
+    """The streaming-read ceiling on this box (bh_roof_hbm_read: 16-byte
+    non-temporal loads, as the decode GEMV's): one graph reading `nseg`
+    distinct 256 MiB segments in turn (1 GiB, so each read is cold), best over
+    five grid sizes."""
     from brain_amd._lib import check
     buf = torch.empty(seg_bytes * nseg // 4, dtype=torch.int32, device=dev).random_(-2**31, 2**31 - 1)
     best = None
-    for blocks in (2048, 4096, 8192, 16384):
+    for blocks in (1024, 2048, 4096, 8192, 16384):
         out = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
         fns = [lambda i=i: check(lib.bh_roof_hbm_read(torch.cuda.current_stream().cuda_stream,
                                                        buf.data_ptr() + i * seg_bytes, seg_bytes, blocks,
