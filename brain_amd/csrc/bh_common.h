@@ -110,28 +110,31 @@ __device__ __forceinline__ v4i load_k16(const uint8_t* rowp, int kb, int kbytes)
     return r;
 }
 
-// Weights streamed once per launch (gemv_i8_kernel): 16 bytes with the
-// non-temporal hint. Measured: a plain streaming read of 256 MiB 6.3-6.6 TB/s
-// against 5.6-5.8 with ordinary loads; the Qwen3-0.6B batch-1 decode step
-// (per-layer GEMVs) 0.876 -> 0.865 ms with the LM head also on these loads,
-// while the LM head's resident streaming kernel alone went 29.3-30.0 -> 34.0
-// us, so that kernel keeps ordinary loads.
-__device__ __forceinline__ v4i load_w16_nt(const uint8_t* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+// Weight loads of gemv_i8_kernel, with or without the non-temporal hint
+// (NT: global_load_dwordx4 ... nt). A plain streaming read of 256 MiB
+// measured 6.3-6.6 TB/s with the hint against 5.6-5.8 without; which GEMV
+// launches take it is set where they are launched, by measurement.
+template <bool NT>
+__device__ __forceinline__ v4i load_w16(const uint8_t* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+    else return *reinterpret_cast<const v4i*>(p);
 }
-template <bool ALIGNED>
-__device__ __forceinline__ v4i load_k16_nt(const uint8_t* rowp, int kb, int kbytes) {
-    v4i r = {0, 0, 0, 0};
-    if constexpr (ALIGNED) {
-        if (kb < kbytes) r = load_w16_nt(rowp + kb);
+template <bool ALIGNED, bool NT>
+__device__ __forceinline__ v4i load_wk16(const uint8_t* rowp, int kb, int kbytes) {
+    if constexpr (!NT) {
+        return load_k16<ALIGNED>(rowp, kb, kbytes);
     } else {
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(rowp + kb);
+        v4i r = {0, 0, 0, 0};
+        if constexpr (ALIGNED) {
+            if (kb < kbytes) r = load_w16<true>(rowp + kb);
+        } else {
+            const uint32_t* p = reinterpret_cast<const uint32_t*>(rowp + kb);
 #pragma unroll
-        for (int d = 0; d < 4; ++d)
-            if (kb + 4 * d < kbytes) r[d] = (int)__builtin_nontemporal_load(p + d);
+            for (int d = 0; d < 4; ++d)
+                if (kb + 4 * d < kbytes) r[d] = (int)__builtin_nontemporal_load(p + d);
+        }
+        return r;
     }
-    return r;
 }
-
 
 }  // namespace bh

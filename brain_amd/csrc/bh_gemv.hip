@@ -80,8 +80,13 @@ struct GemvArgs {
 // PRE (XMODE 3 / 4 with several rows): 8 * R + G fixes the prologue's rows
 // per thread and float4 groups per row at compile time; 0 picks them at run
 // time.
+// NTW: the weights are read with the non-temporal hint. Measured on the
+// Qwen3-0.6B decode step, whose per-layer GEMVs are the fused ones: batch 1
+// 0.876 -> 0.860 ms per step, but batch 4 1.089 -> 1.100 and batch 8 1.208
+// -> 1.231 (and no change on the configs[1] sweep), so only the fused
+// one-row launches take it.
 template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int KSPLIT, int XMODE, int U, int CG, int NW = GV_WAVES,
-          int PRE = 0>
+          int PRE = 0, bool NTW = false>
 __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
     constexpr bool XLDS = XMODE != 0;
     constexpr int SLOTS = NW / KSPLIT;  // wave slots per workgroup, each CG column groups
@@ -145,7 +150,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
                 if (u < my_chunks)
 #pragma unroll
                     for (int c = 0; c < CG; ++c)
-                        wf[u][c] = load_k16_nt<ALIGNED>(wp[c], (ks + KSPLIT * u) * 64 + ksub, kbytes);
+                        wf[u][c] = load_wk16<ALIGNED, NTW>(wp[c], (ks + KSPLIT * u) * 64 + ksub, kbytes);
         } else {
             // Unconditional, and with no masking (this mode needs K % 64 ==
             // 0): slots past this wave's chunks reload its last one (never
@@ -164,7 +169,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
             for (int u = 0; u < U; ++u)
 #pragma unroll
                 for (int c = 0; c < CG; ++c)
-                    wf[u][c] = load_w16_nt(wp[c] + min(ks + KSPLIT * min(u, last), nchunks - 1) * 64 + ksub);
+                    wf[u][c] = load_w16<NTW>(wp[c] + min(ks + KSPLIT * min(u, last), nchunks - 1) * 64 + ksub);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -563,7 +568,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
             if (j0 + u < my_chunks)
 #pragma unroll
                 for (int c = 0; c < CG; ++c)
-                    wf[u][c] = load_k16_nt<ALIGNED>(wp[c], (ks + KSPLIT * (j0 + u)) * 64 + ksub, kbytes);
+                    wf[u][c] = load_wk16<ALIGNED, NTW>(wp[c], (ks + KSPLIT * (j0 + u)) * 64 + ksub, kbytes);
         batch(j0);
     }
     BH_STAMP(2);
@@ -802,14 +807,15 @@ static int gv_cfg() {
     return v;
 }
 
-template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int U, int CG, int KSPLIT = 4, int XMODE = 0, int PRE = 0>
+template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int U, int CG, int KSPLIT = 4, int XMODE = 0, int PRE = 0,
+          bool NTW = false>
 static hipError_t gv_go(hipStream_t s, const GemvArgs& a) {
     constexpr int NW = KSPLIT > GV_WAVES ? KSPLIT : GV_WAVES;  // waves per workgroup
     constexpr int per_wg = (NW / KSPLIT) * CG;
     const int ngroups = (a.n + 15) / 16;
     const int grid = (ngroups + per_wg - 1) / per_wg;
     const size_t lds = XMODE ? (size_t)MT * 16 * (a.kg * 4 + 16) + MT * 16 * 4 : 0;
-    gemv_i8_kernel<MT, OUT, HAS_BIAS, ALIGNED, KSPLIT, XMODE, U, CG, NW, PRE><<<grid, NW * 64, lds, s>>>(a);
+    gemv_i8_kernel<MT, OUT, HAS_BIAS, ALIGNED, KSPLIT, XMODE, U, CG, NW, PRE, NTW><<<grid, NW * 64, lds, s>>>(a);
     return hipGetLastError();
 }
 
@@ -991,12 +997,14 @@ hipError_t launch_gemv_i8_pre(hipStream_t s, int mode, const uint32_t* pre_tok, 
     const int ng = nchunks >= 32 ? 4 : 2;  // row groups of the launch below
     const int rpt = m <= ng ? 1 : m <= 2 * ng ? 2 : 4;
     if (mode == 3 && kbytes == 1024) {
+        if (m == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 8 + 1, true>(s, a);
         if (rpt == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 8 + 1>(s, a);
         if (rpt == 2) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 16 + 1>(s, a);
         return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 32 + 1>(s, a);
     }
     if (mode == 4 && kbytes == 3072) {
         // 48 K-chunks over 16 waves: each wave's 3 chunks in one batch.
+        if (m == 1) return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 8 + 3, true>(s, a);
         if (rpt == 1) return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 8 + 3>(s, a);
         if (rpt == 2) return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 16 + 3>(s, a);
         return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 32 + 3>(s, a);
@@ -1027,6 +1035,7 @@ hipError_t launch_gemv_i8_merge(hipStream_t s, const float* part_o, const float*
     a.nh = nh;
     a.hd = hd;
     a.splits = splits;
+    if (m == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 5, 0, true>(s, a);
     return gv_go<1, OUT_F32, false, true, 4, 1, 8, 5>(s, a);
 }
 
