@@ -381,7 +381,7 @@ def mfma_roof(torch, lib, dev):
 
 def hbm_read_probe(torch, lib, dev, seg_bytes=256 << 20, nseg=4):
     """The streaming-read ceiling on this box (bh_roof_hbm_read: 16-byte
-    non-temporal loads, as the decode GEMV's): one graph reading `nseg`
+    non-temporal loads): one graph reading `nseg`
     distinct 256 MiB segments in turn (1 GiB, so each read is cold), best over
     five grid sizes."""
     from brain_amd._lib import check

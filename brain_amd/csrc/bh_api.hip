@@ -160,9 +160,9 @@ __global__ __launch_bounds__(256) void roof_mfma_i8_kernel(uint32_t iters, int32
 }
 
 // Bandwidth roof (the read side of crates/gpu-core/src/roof.rs:458-490's axpy
-// probe): `words4` 16-byte words read with 16-byte non-temporal vector loads,
-// as the decode GEMV loads its weights (the fastest plain streaming read
-// measured: 6.3-6.6 TB/s against 5.6-5.8 without the hint). Each workgroup
+// probe): `words4` 16-byte words read with 16-byte non-temporal vector loads
+// (the fastest plain streaming read measured: 6.3-6.6 TB/s against 5.6-5.8
+// without the hint). Each workgroup
 // reads contiguous runs of 256 x 8 words (8 loads in flight per thread, 4 KB
 // apart), the runs spread over the grid; the words are XOR-folded so no load
 // is dead, one word per thread written.

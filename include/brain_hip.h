@@ -241,8 +241,7 @@ int bh_roof_mfma_i8(void* stream, uint32_t blocks, uint32_t iters, int32_t* out)
  * `blocks` workgroups of 256 threads read `bytes` (a multiple of 16, 16-byte
  * aligned) from `src` with 16-byte non-temporal vector loads, 8 in flight per
  * thread, and write one folded word per thread to `out` (blocks*256 words).
- * Also a calibration kernel for the FETCH_SIZE counter (its loads are the
- * decode GEMV's). */
+ * Also a calibration kernel for the FETCH_SIZE counter. */
 int bh_roof_hbm_read(void* stream, const void* src, uint64_t bytes, uint32_t blocks, uint32_t* out);
 
 /* ======================================================================
