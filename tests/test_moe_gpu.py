@@ -122,3 +122,34 @@ def test_moe_compacted_rows(gpu, m, k, n, frac):
         want = o.epilogue(o.acc_exact(xq, wq, rows, np.arange(n)), sx[rows], sw)
         assert np.array_equal(got[rows].view(np.uint32), want.view(np.uint32))
     assert (got[~routed].view(np.uint32) == 0).all()
+
+
+def test_moe_compacted_rows_graph_replays(gpu):
+    """The compaction under a HIP graph: captured once (after a warm call on
+    the capture stream, which sizes its workspace), replayed with a different
+    routing written into the gate between replays (eager work and
+    synchronizations in between); every replay equals the eager call on the
+    same gate, bit for bit."""
+    m, k, n, n_experts, e_idx = 8192, 1024, 512, 4, 1
+    g = torch.Generator(device=gpu).manual_seed(11)
+    xq = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=gpu, generator=g).view(torch.int32)
+    wq = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=gpu, generator=g).view(torch.int32)
+    sx = torch.rand(m, device=gpu, generator=g) * 0.02 + 0.001
+    sw = torch.rand(n, device=gpu, generator=g) * 0.02 + 0.002
+    gate = torch.empty(m, n_experts, device=gpu)
+    out = torch.empty(m, n, device=gpu)
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        ops.moe_linear_gated_i8(xq, wq, sx, sw, gate.fill_(1.0), e_idx, out=out)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        ops.moe_linear_gated_i8(xq, wq, sx, sw, gate, e_idx, out=out)
+    for frac in (0.125, 1.0, 0.0, 0.4):
+        gate.copy_(torch.where(torch.rand(m, n_experts, device=gpu, generator=g) < frac, 1.0, -1.0))
+        want = ops.moe_linear_gated_i8(xq, wq, sx, sw, gate, e_idx)
+        torch.cuda.synchronize()
+        out.fill_(7.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), want.view(torch.int32)), frac
