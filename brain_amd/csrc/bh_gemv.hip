@@ -71,6 +71,11 @@ struct GemvArgs {
     const float* part_ml = nullptr;
     const uint32_t* pos = nullptr;
     int nh = 0, hd = 0, splits = 0;
+    // The wide-N streaming kernel reads the weights with ordinary loads in
+    // the MFMA's layout (for a caller that re-reads them every step and
+    // wants them kept in the caches) instead of whole 128-byte lines with
+    // the non-temporal hint.
+    bool keep_cached = false;
 };
 
 // XMODE: 0 = packed activation read from global memory, 1 = staged into
@@ -628,15 +633,24 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
 // memory pipe. Work items are (column group, batch of U = 16 64-byte K
 // chunks); K (= KB bytes) is a compile-time multiple of 1024.
 // Measured on MI355X (LM head, cold): two waves per SIMD (256 VGPRs, fewer
-// parked results) and non-temporal weight loads were both slower than this
-// form (one wave per SIMD, 288 VGPRs with the accumulation registers).
+// parked results) was slower than this form (one wave per SIMD, 288 VGPRs
+// with the accumulation registers).
+// LINES: every weight load covers whole 128-byte lines (8 rows x 128 bytes)
+// with the non-temporal hint, and a row_ror:8 lane exchange puts the values
+// into the MFMA's layout (which alone would read 16 rows x 64 bytes per load,
+// each line split over two loads). On the configs[1] sweep (cold weights):
+// the LM head 29.3-29.5 -> 28.1-28.7 us and the 16-launch average 10.19-10.21
+// -> 9.52 us; the non-temporal hint on the split-line layout was 2-3.5 us
+// slower, whole lines without the hint slower too (30.6-31.0 us). The Qwen3
+// engine's head, re-read every step, keeps the ordinary loads
+// (GemvArgs::keep_cached).
 // Q4: W4A8 weights (matmul_q4_gemv, crates/kernels/wgsl/matmul_q4_gemv.wgsl):
 // rows of KB/2 bytes, 8 int4 per u32 word; per 128-K chunk each lane loads 16
 // bytes of int4 (K 32q..32q+31 of its column, q = lane/16), unpacks them to
 // two int8 fragments and feeds two MFMAs against the activation bytes of the
 // same K (a permutation of K inside the chunk shared by both operands, so the
 // sum is exact; the same pairing as gemv_q4_kernel).
-template <int OUT, bool HAS_BIAS, int KB, bool Q4 = false>
+template <int OUT, bool HAS_BIAS, int KB, bool Q4 = false, bool LINES = false>
 __global__ __launch_bounds__(256) void gemv_i8_stream_kernel(GemvArgs a, int groups_per_wave) {
     constexpr int U = Q4 ? 8 : 16, kbytes = KB, nbatch = KB / 1024;
     constexpr int wbytes = Q4 ? KB / 2 : KB;  // weight bytes per row
@@ -667,9 +681,27 @@ __global__ __launch_bounds__(256) void gemv_i8_stream_kernel(GemvArgs a, int gro
             it.sw = OUT != OUT_I32 ? a.sw[r] : 0.0f;
             it.bias = HAS_BIAS ? a.bias[r] : 0.0f;
         }
-        const uint8_t* rp = reinterpret_cast<const uint8_t*>(a.wq) + (int64_t)r * wbytes + b * U * 64 + ksub;
+        if constexpr (LINES && !Q4) {
+            // Whole 128-byte lines per load: the pair (u, u+1) of k-blocks is
+            // two loads, rows 0-7 then rows 8-15 of the group, lane (c, j)
+            // (c = lane % 16, j = lane / 16) reading 16 bytes of row c % 8 at
+            // chunk j (c < 8) or 4 + j (c >= 8) of the 128 bytes. consume()
+            // moves them into the MFMA layout with a row_ror:8 exchange.
+            const int c = lane & 15;
+            const int off = b * U * 64 + (c < 8 ? ksub : 64 + ksub);
+            const int r0 = min(g * 16 + (c & 7), n - 1), r1 = min(g * 16 + 8 + (c & 7), n - 1);
+            const uint8_t* p0 = reinterpret_cast<const uint8_t*>(a.wq) + (int64_t)r0 * wbytes + off;
+            const uint8_t* p1 = reinterpret_cast<const uint8_t*>(a.wq) + (int64_t)r1 * wbytes + off;
 #pragma unroll
-        for (int u = 0; u < U; ++u) it.w[u] = *reinterpret_cast<const v4i*>(rp + u * 64);
+            for (int u = 0; u < U; u += 2) {
+                it.w[u] = load_w16<true>(p0 + u * 64);
+                it.w[u + 1] = load_w16<true>(p1 + u * 64);
+            }
+        } else {
+            const uint8_t* rp = reinterpret_cast<const uint8_t*>(a.wq) + (int64_t)r * wbytes + b * U * 64 + ksub;
+#pragma unroll
+            for (int u = 0; u < U; ++u) it.w[u] = *reinterpret_cast<const v4i*>(rp + u * 64);
+        }
     };
 
     // Activation image: 16 rows plus a 16-byte pad per row. Rows >= m repeat
@@ -749,6 +781,28 @@ __global__ __launch_bounds__(256) void gemv_i8_stream_kernel(GemvArgs a, int gro
                 acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, b0, acc, 0, 0, 0);
                 acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, b1, acc, 0, 0, 0);
             }
+        } else if constexpr (LINES) {
+            // Lane (c, j) holds row c%8 (first load) or 8 + c%8 (second) of
+            // the group; the MFMA wants row c, chunk j for block u and chunk
+            // 4 + j for block u+1. row_ror:8 swaps the two 8-lane halves of
+            // each 16-lane row.
+            const uint8_t* xp = xrow + b * U * 64;
+            const bool lo = (lane & 15) < 8;
+#pragma unroll
+            for (int u = 0; u < U; u += 2) {
+                v4i r0, r1;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    r0[d] = __builtin_amdgcn_mov_dpp(it.w[u][d], 0x128, 0xF, 0xF, false);
+                    r1[d] = __builtin_amdgcn_mov_dpp(it.w[u + 1][d], 0x128, 0xF, 0xF, false);
+                }
+                const v4i w0 = lo ? it.w[u] : r1;
+                const v4i w1 = lo ? r0 : it.w[u + 1];
+                const v4i x0 = *reinterpret_cast<const v4i*>(xp + u * 64);
+                const v4i x1 = *reinterpret_cast<const v4i*>(xp + (u + 1) * 64);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, w0, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, w1, acc, 0, 0, 0);
+            }
         } else {
             const uint8_t* xp = xrow + b * U * 64;
 #pragma unroll
@@ -821,7 +875,7 @@ static hipError_t gv_go(hipStream_t s, const GemvArgs& a) {
 
 // The streaming wide-N kernel: as many waves as can be resident (so the
 // whole grid is one round), each owning an equal share of the column groups.
-template <int OUT, bool HAS_BIAS, int KB, bool Q4 = false>
+template <int OUT, bool HAS_BIAS, int KB, bool Q4 = false, bool LINES = false>
 static hipError_t gv_stream_kb(hipStream_t s, const GemvArgs& a) {
     // Resident waves (the whole grid is one round).
     static const int slots = [] {
@@ -829,7 +883,7 @@ static hipError_t gv_stream_kb(hipStream_t s, const GemvArgs& a) {
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
             cus = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_i8_stream_kernel<OUT, HAS_BIAS, KB, Q4>, 256,
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_i8_stream_kernel<OUT, HAS_BIAS, KB, Q4, LINES>, 256,
                                                          0) !=
                 hipSuccess || per_cu < 1)
             per_cu = 1;
@@ -838,7 +892,7 @@ static hipError_t gv_stream_kb(hipStream_t s, const GemvArgs& a) {
     const int ngroups = (a.n + 15) / 16;
     const int gpw = (ngroups + slots - 1) / slots;  // groups per wave
     const int waves = (ngroups + gpw - 1) / gpw;    // balanced: every wave gpw or gpw-1 groups
-    gemv_i8_stream_kernel<OUT, HAS_BIAS, KB, Q4><<<(waves + 3) / 4, 256, 0, s>>>(a, gpw);
+    gemv_i8_stream_kernel<OUT, HAS_BIAS, KB, Q4, LINES><<<(waves + 3) / 4, 256, 0, s>>>(a, gpw);
     return hipGetLastError();
 }
 
@@ -846,7 +900,8 @@ static hipError_t gv_stream_kb(hipStream_t s, const GemvArgs& a) {
 // of the 1024-wide decoder), m <= 16.
 template <int OUT, bool HAS_BIAS>
 static hipError_t gv_stream(hipStream_t s, const GemvArgs& a) {
-    return gv_stream_kb<OUT, HAS_BIAS, 1024>(s, a);
+    if (a.keep_cached) return gv_stream_kb<OUT, HAS_BIAS, 1024>(s, a);
+    return gv_stream_kb<OUT, HAS_BIAS, 1024, false, true>(s, a);
 }
 
 // Launch policy (measured on MI355X with rotating >256 MB weight pools):
@@ -934,11 +989,13 @@ hipError_t launch_gemv_q4_stream(hipStream_t s, const uint32_t* xq, const uint32
 
 // Preconditions are checked by the C-ABI layer: 1 <= m <= 32, kg >= 0, n >= 1.
 hipError_t launch_gemv_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
-                          const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n) {
+                          const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n,
+                          bool keep_cached = false) {
     const bool aligned = ((kg * 4) % 16 == 0) && ((reinterpret_cast<uintptr_t>(xq) & 15u) == 0) &&
                          ((reinterpret_cast<uintptr_t>(wq) & 15u) == 0);
     GemvArgs a{xq, wq, sx, sw, bias, out, m, kg, n, nullptr, 0, 0, nullptr, nullptr, nullptr,
                nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0.0f};
+    a.keep_cached = keep_cached;
     if (m <= 16) return gv_out<1>(s, aligned, out_dtype, a);
     return gv_out<2>(s, aligned, out_dtype, a);
 }

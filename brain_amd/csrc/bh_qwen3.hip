@@ -50,7 +50,8 @@ namespace bh {
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, float* sx, uint32_t* xq);
 hipError_t launch_quantize_weight(hipStream_t s, const float* w, int n, int k, uint32_t* packed, float* sw);
 hipError_t launch_gemv_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
-                          const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n);
+                          const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n,
+                          bool keep_cached = false);
 hipError_t gemm_reserve(hipStream_t s, int m, int kg, int n);
 hipError_t launch_gemm_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n);
@@ -1199,10 +1200,12 @@ int reserve_linears(bh_qwen3* e, int rows) {
     return BH_OK;
 }
 
-int launch_linear(bh_qwen3* e, const uint32_t* w, const float* sw, float* out, int m, int k, int n) {
+int launch_linear(bh_qwen3* e, const uint32_t* w, const float* sw, float* out, int m, int k, int n,
+                  bool keep_cached = false) {
     const int tuned = tuned_variant((uint32_t)m, (uint32_t)n, (uint32_t)k);
     const bool gemv = tuned ? tuned == BH_VARIANT_WORKGROUP_PER_OUTPUT : m <= 32;
-    hipError_t err = gemv ? launch_gemv_i8(e->stream, e->xq, w, e->sx, sw, nullptr, out, OUT_F32, m, k / 4, n)
+    hipError_t err = gemv ? launch_gemv_i8(e->stream, e->xq, w, e->sx, sw, nullptr, out, OUT_F32, m, k / 4, n,
+                                           keep_cached)
                              : launch_gemm_i8(e->stream, e->xq, w, e->sx, sw, nullptr, out, OUT_F32, m, k / 4, n);
     BH_HIP(err, "int8 linear launch");
     return BH_OK;
@@ -1420,7 +1423,10 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
     nf.xq = e->xq;
     nf.xq_words = d / 4;
     BH_TRY(launch_norm_quant(e, nf, n_out));
-    BH_TRY(launch_linear(e, e->head, e->shead, e->logits, n_out, d, (int)c.vocab));
+    // The head's weights are re-read every step and fit the Infinity Cache
+    // (measured: batch-1 step 0.861 ms with ordinary loads, 0.863-0.864 with
+    // the streaming form that is faster on cold weights).
+    BH_TRY(launch_linear(e, e->head, e->shead, e->logits, n_out, d, (int)c.vocab, true));
     argmax_part_kernel<<<dim3(AM_CH, n_out), RT, 0, e->stream>>>(e->logits, (int)c.vocab, e->am_v, e->am_i);
     BH_HIP(hipGetLastError(), "argmax_part launch");
     argmax_final_kernel<<<n_out, 64, 0, e->stream>>>(e->am_v, e->am_i, e->tok_dec, e->pos_dec,
