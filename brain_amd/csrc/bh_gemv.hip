@@ -681,8 +681,9 @@ __global__ __launch_bounds__(256) void gemv_i8_stream_kernel(GemvArgs a, int gro
             it.sw = OUT != OUT_I32 ? a.sw[r] : 0.0f;
             it.bias = HAS_BIAS ? a.bias[r] : 0.0f;
         }
-        if constexpr (LINES && !Q4) {
-            // Whole 128-byte lines per load: the pair (u, u+1) of k-blocks is
+        if constexpr (LINES) {
+            // Whole 128-byte lines per load (Q4 too: its 64-byte blocks are
+            // 128 K of int4): the pair (u, u+1) of k-blocks is
             // two loads, rows 0-7 then rows 8-15 of the group, lane (c, j)
             // (c = lane % 16, j = lane / 16) reading 16 bytes of row c % 8 at
             // chunk j (c < 8) or 4 + j (c >= 8) of the 128 bytes. consume()
@@ -772,10 +773,29 @@ __global__ __launch_bounds__(256) void gemv_i8_stream_kernel(GemvArgs a, int gro
         const int i = j / nbatch, b = j - i * nbatch;
         if constexpr (Q4) {
             const uint8_t* xp = xrow + b * U * 128;
+            v4i wq4[U];
+            if constexpr (LINES) {
+                // The same exchange as below, then the int4 unpack.
+                const bool lo = (lane & 15) < 8;
+#pragma unroll
+                for (int u = 0; u < U; u += 2) {
+                    v4i r0, r1;
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        r0[d] = __builtin_amdgcn_mov_dpp(it.w[u][d], 0x128, 0xF, 0xF, false);
+                        r1[d] = __builtin_amdgcn_mov_dpp(it.w[u + 1][d], 0x128, 0xF, 0xF, false);
+                    }
+                    wq4[u] = lo ? it.w[u] : r1;
+                    wq4[u + 1] = lo ? r0 : it.w[u + 1];
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < U; ++u) wq4[u] = it.w[u];
+            }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 v4i b0, b1;
-                unpack_q4x4(it.w[u], b0, b1);
+                unpack_q4x4(wq4[u], b0, b1);
                 const v4i x0 = *reinterpret_cast<const v4i*>(xp + u * 128);
                 const v4i x1 = *reinterpret_cast<const v4i*>(xp + u * 128 + 16);
                 acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, b0, acc, 0, 0, 0);
@@ -981,10 +1001,10 @@ hipError_t launch_gemv_q4_stream(hipStream_t s, const uint32_t* xq, const uint32
         return hipErrorNotSupported;
     GemvArgs a{xq, wq, sx, sw, bias, out, m, k / 4, n, nullptr, 0, 0, nullptr, nullptr, nullptr,
                nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0.0f};
-    if (out_dtype == OUT_I32) return gv_stream_kb<OUT_I32, false, 1024, true>(s, a);
+    if (out_dtype == OUT_I32) return gv_stream_kb<OUT_I32, false, 1024, true, true>(s, a);
     if (out_dtype == OUT_F32)
-        return bias ? gv_stream_kb<OUT_F32, true, 1024, true>(s, a) : gv_stream_kb<OUT_F32, false, 1024, true>(s, a);
-    return bias ? gv_stream_kb<OUT_BF16, true, 1024, true>(s, a) : gv_stream_kb<OUT_BF16, false, 1024, true>(s, a);
+        return bias ? gv_stream_kb<OUT_F32, true, 1024, true, true>(s, a) : gv_stream_kb<OUT_F32, false, 1024, true, true>(s, a);
+    return bias ? gv_stream_kb<OUT_BF16, true, 1024, true, true>(s, a) : gv_stream_kb<OUT_BF16, false, 1024, true, true>(s, a);
 }
 
 // Preconditions are checked by the C-ABI layer: 1 <= m <= 32, kg >= 0, n >= 1.
