@@ -91,3 +91,15 @@ def test_step_api_rejects_null_backend():
     lib = brain_amd.load()
     out = C.c_void_p()
     assert lib.bh_step(None, 0, None, 0, None, 0, 0, C.byref(out)) == _lib.BH_ERR_INVALID
+
+
+def test_matmul_quant_rejects_bad_arguments():
+    # Checked before anything reaches the GPU: n not a multiple of 4, a null
+    # output buffer, and a missing quantized output.
+    lib = brain_amd.load()
+    p = C.c_void_p(16)  # never dereferenced: the checks fail first
+    assert lib.bh_matmul_i8_dyn_quant(None, p, p, p, p, None, p, 8, 4, 6, p, p) == _lib.BH_ERR_INVALID
+    assert b"multiple of 4" in lib.bh_last_error()
+    assert lib.bh_matmul_i8_dyn_quant(None, p, p, p, p, None, None, 8, 4, 8, p, p) == _lib.BH_ERR_INVALID
+    assert lib.bh_matmul_i8_dyn_quant(None, p, p, p, p, None, p, 8, 4, 8, p, None) == _lib.BH_ERR_INVALID
+    assert lib.bh_matmul_i8_dyn_quant(None, p, p, p, p, None, p, 0, 4, 8, None, None) == _lib.BH_OK  # m = 0: nothing to do
