@@ -90,9 +90,15 @@ struct GemvArgs {
 // 0.876 -> 0.860 ms per step, but batch 4 1.089 -> 1.100 and batch 8 1.208
 // -> 1.231 (and no change on the configs[1] sweep), so only the fused
 // one-row launches take it.
+// LINES: the K chunks go to the waves in pairs (wave ks owns pairs ks,
+// ks + KSPLIT, ...; slot u of a batch is chunk 2 * pair + u % 2), and each
+// pair of a column group is two loads of whole 128-byte lines (rows 0-7,
+// then rows 8-15), put into the MFMA's layout by a row_ror:8 exchange, as
+// the streaming kernel does. Needs ALIGNED, K % 128 == 0 and an even U.
 template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int KSPLIT, int XMODE, int U, int CG, int NW = GV_WAVES,
-          int PRE = 0, bool NTW = false>
+          int PRE = 0, bool NTW = false, bool LINES = false>
 __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
+    static_assert(!LINES || (ALIGNED && U % 2 == 0 && XMODE != 4), "whole-line loads: aligned, pairs of chunks");
     constexpr bool XLDS = XMODE != 0;
     constexpr int SLOTS = NW / KSPLIT;  // wave slots per workgroup, each CG column groups
     extern __shared__ __attribute__((aligned(16))) uint8_t xs[];  // [MT*16][kbytes+16] when XLDS
@@ -135,7 +141,31 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
         wr = wr < n ? wr : n - 1;  // clamped rows are loaded but never stored
         wp[c] = reinterpret_cast<const uint8_t*>(a.wq) + (int64_t)wr * kbytes;
     }
-    const int my_chunks = g0 < ngroups ? (nchunks - ks + KSPLIT - 1) / KSPLIT : 0;  // chunks ks + KSPLIT*j
+    v4i wf[U][CG];
+    // Chunks of this wave: ks + KSPLIT*j, or with LINES the pairs ks + KSPLIT*v.
+    const int my_chunks = g0 < ngroups ? (LINES ? 2 * ((nchunks / 2 - ks + KSPLIT - 1) / KSPLIT)
+                                                : (nchunks - ks + KSPLIT - 1) / KSPLIT)
+                                       : 0;
+    auto chunk_of = [&](int j) { return LINES ? 2 * (ks + KSPLIT * (j >> 1)) + (j & 1) : ks + KSPLIT * j; };
+    const uint8_t* wl[LINES ? CG : 1][2];  // LINES: the lane's rows c%8 and 8 + c%8 of each group
+    const int lineoff = ((lane & 15) < 8 ? 0 : 64) + ksub;
+    if constexpr (LINES) {
+#pragma unroll
+        for (int c = 0; c < CG; ++c)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int wr = min((g0 + c) * 16 + 8 * h + (lane & 7), n - 1);
+                wl[c][h] = reinterpret_cast<const uint8_t*>(a.wq) + (int64_t)wr * kbytes + lineoff;
+            }
+    }
+    // Slot u (even) and u + 1 of pair `pr`: two whole-line loads.
+    auto load_pair = [&](int u, int pr) {
+#pragma unroll
+        for (int c = 0; c < CG; ++c) {
+            wf[u][c] = load_w16<NTW>(wl[c][0] + pr * 128);
+            wf[u + 1][c] = load_w16<NTW>(wl[c][1] + pr * 128);
+        }
+    };
 
     // The first batch of weight loads. Most launches issue it here, ahead of
     // the activation or the prologue's inputs. The SwiGLU prologue (XMODE 4)
@@ -147,9 +177,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
     // 5.32 at 1 row; the same order made the norm (5.45 -> 5.64 us) and the
     // merge (7.46 -> 8.15 us) slower, their chains being shorter than the
     // head start the weights lose behind the inputs' load instructions.
-    v4i wf[U][CG];
     auto issue_w = [&]() {
-        if constexpr (XMODE != 4) {
+        if constexpr (XMODE != 4 && LINES) {
+#pragma unroll
+            for (int u = 0; u < U; u += 2)
+                if (u < my_chunks) load_pair(u, ks + KSPLIT * (u >> 1));
+        } else if constexpr (XMODE != 4) {
 #pragma unroll
             for (int u = 0; u < U; ++u)
                 if (u < my_chunks)
@@ -554,7 +587,27 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
         for (int u = 0; u < U; ++u)
 #pragma unroll
             for (int t = 0; t < MT; ++t)
-                xf[u][t] = (j0 + u < my_chunks) ? xfrag(t, (ks + KSPLIT * (j0 + u)) * 64 + ksub) : v4i{0, 0, 0, 0};
+                xf[u][t] = (j0 + u < my_chunks) ? xfrag(t, chunk_of(j0 + u) * 64 + ksub) : v4i{0, 0, 0, 0};
+        if constexpr (LINES) {
+            // Lane (c, j) holds row c%8 (first load) or 8 + c%8 (second);
+            // the MFMA wants row c, chunk j of the pair's first 64 bytes,
+            // then of its second.
+            const bool lo = (lane & 15) < 8;
+#pragma unroll
+            for (int u = 0; u < U; u += 2)
+#pragma unroll
+                for (int c = 0; c < CG; ++c) {
+                    v4i r0, r1;
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        r0[d] = __builtin_amdgcn_mov_dpp(wf[u][c][d], 0x128, 0xF, 0xF, false);
+                        r1[d] = __builtin_amdgcn_mov_dpp(wf[u + 1][c][d], 0x128, 0xF, 0xF, false);
+                    }
+                    const v4i w0 = lo ? wf[u][c] : r1, w1 = lo ? r0 : wf[u + 1][c];
+                    wf[u][c] = w0;
+                    wf[u + 1][c] = w1;
+                }
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u)
             if (j0 + u < my_chunks)
@@ -568,12 +621,18 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
     batch(0);
 #pragma unroll 1
     for (int j0 = U; j0 < my_chunks; j0 += U) {
+        if constexpr (LINES) {
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-            if (j0 + u < my_chunks)
+            for (int u = 0; u < U; u += 2)
+                if (j0 + u < my_chunks) load_pair(u, ks + KSPLIT * ((j0 + u) >> 1));
+        } else {
 #pragma unroll
-                for (int c = 0; c < CG; ++c)
-                    wf[u][c] = load_wk16<ALIGNED, NTW>(wp[c], (ks + KSPLIT * (j0 + u)) * 64 + ksub, kbytes);
+            for (int u = 0; u < U; ++u)
+                if (j0 + u < my_chunks)
+#pragma unroll
+                    for (int c = 0; c < CG; ++c)
+                        wf[u][c] = load_wk16<ALIGNED, NTW>(wp[c], (ks + KSPLIT * (j0 + u)) * 64 + ksub, kbytes);
+        }
         batch(j0);
     }
     BH_STAMP(2);
@@ -882,14 +941,14 @@ static int gv_cfg() {
 }
 
 template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int U, int CG, int KSPLIT = 4, int XMODE = 0, int PRE = 0,
-          bool NTW = false>
+          bool NTW = false, bool LINES = false>
 static hipError_t gv_go(hipStream_t s, const GemvArgs& a) {
     constexpr int NW = KSPLIT > GV_WAVES ? KSPLIT : GV_WAVES;  // waves per workgroup
     constexpr int per_wg = (NW / KSPLIT) * CG;
     const int ngroups = (a.n + 15) / 16;
     const int grid = (ngroups + per_wg - 1) / per_wg;
     const size_t lds = XMODE ? (size_t)MT * 16 * (a.kg * 4 + 16) + MT * 16 * 4 : 0;
-    gemv_i8_kernel<MT, OUT, HAS_BIAS, ALIGNED, KSPLIT, XMODE, U, CG, NW, PRE, NTW><<<grid, NW * 64, lds, s>>>(a);
+    gemv_i8_kernel<MT, OUT, HAS_BIAS, ALIGNED, KSPLIT, XMODE, U, CG, NW, PRE, NTW, LINES><<<grid, NW * 64, lds, s>>>(a);
     return hipGetLastError();
 }
 
@@ -1112,7 +1171,12 @@ hipError_t launch_gemv_i8_merge(hipStream_t s, const float* part_o, const float*
     a.nh = nh;
     a.hd = hd;
     a.splits = splits;
-    if (m == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 5, 0, true>(s, a);
+    // One row: whole-line non-temporal weight loads. Batch-1 decode step
+    // 0.859-0.861 -> 0.850-0.851 ms; the same loads in the one-row norm +
+    // q|k|v and norm + gate|up launches made the step 0.859 ms (no gain),
+    // and on the configs[1] sweep they took the narrow shapes' cold time
+    // 3.65 -> 3.53 us on average without moving the 16-launch graph.
+    if (m == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 5, 0, true, true>(s, a);
     return gv_go<1, OUT_F32, false, true, 4, 1, 8, 5>(s, a);
 }
 
