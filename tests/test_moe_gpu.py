@@ -124,6 +124,33 @@ def test_moe_compacted_rows(gpu, m, k, n, frac):
     assert (got[~routed].view(np.uint32) == 0).all()
 
 
+@pytest.mark.parametrize("m,k,n,frac", [(16384, 1024, 3072, 0.125), (8192, 1024, 3072, 0.25)])
+def test_moe_compacted_rows_big_tiles(gpu, m, k, n, frac):
+    """The compaction on the big-tile GEMMs (256x256 ping-pong tiles at
+    16384 x 3072, 256x128 at 8192 x 3072), whose epilogues also store packed
+    row k to its row of the output: a sample of the routed rows (the first,
+    the last, the NaN-gated one and 256 more) against the oracle bit for bit,
+    every unrouted row +0."""
+    rng = np.random.default_rng(m + n + 1)
+    n_experts, e_idx = 8, 5
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    sx = o.max_abs_row(x)
+    xq = o.quant_pack(x, sx)
+    wq, sw = o.synth_weights(n, k, m + 3)
+    gate = rng.standard_normal((m, n_experts)).astype(np.float32)
+    routed = rng.random(m) < frac
+    gate[:, e_idx] = np.where(routed, np.abs(gate[:, e_idx]) + 0.1, -np.abs(gate[:, e_idx]))
+    gate[11, e_idx] = np.nan
+    routed[11] = True
+    got = ops.moe_linear_gated_i8(dev_u32(xq, gpu), dev_u32(wq, gpu), torch.from_numpy(sx).to(gpu),
+                                  torch.from_numpy(sw).to(gpu), torch.from_numpy(gate).to(gpu), e_idx).cpu().numpy()
+    rows = np.nonzero(routed)[0]
+    pick = np.unique(np.concatenate([rows[:1], rows[-1:], [11], rng.choice(rows, 256, replace=False)]))
+    want = o.epilogue(o.acc_exact(xq, wq, pick, np.arange(n)), sx[pick], sw)
+    assert np.array_equal(got[pick].view(np.uint32), want.view(np.uint32))
+    assert (got[~routed].view(np.uint32) == 0).all()
+
+
 def test_moe_compacted_rows_graph_replays(gpu):
     """The compaction under a HIP graph: captured once (after a warm call on
     the capture stream, which sizes its workspace), replayed with a different
