@@ -1133,14 +1133,20 @@ hipError_t launch_gemv_i8_pre(hipStream_t s, int mode, const uint32_t* pre_tok, 
     const int ng = nchunks >= 32 ? 4 : 2;  // row groups of the launch below
     const int rpt = m <= ng ? 1 : m <= 2 * ng ? 2 : 4;
     if (mode == 3 && kbytes == 1024) {
-        if (m == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 8 + 1, true>(s, a);
+        // One row: K split 4 ways (4 waves of 4 chunks) rather than 8 (8 of 2):
+        // batch-1 step 0.8495 -> 0.842 ms.
+        if (m == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 4, 3, 8 + 1, true>(s, a);
         if (rpt == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 8 + 1>(s, a);
         if (rpt == 2) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 16 + 1>(s, a);
         return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 32 + 1>(s, a);
     }
     if (mode == 4 && kbytes == 3072) {
         // 48 K-chunks over 16 waves: each wave's 3 chunks in one batch.
-        if (m == 1) return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 8 + 3, true>(s, a);
+        // One row: 8 waves of 6 chunks rather than 16 of 3: batch-1 step
+        // 0.8495 -> 0.831 ms, with the one-row norm change above 0.819 (same
+        // box; 12 waves of 4 chunks 0.849, 4 of 12 0.858, two column groups
+        // per wave 0.887).
+        if (m == 1) return gv_go<1, OUT_F32, false, true, 6, 1, 8, 4, 8 + 3, true>(s, a);
         if (rpt == 1) return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 8 + 3>(s, a);
         if (rpt == 2) return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 16 + 3>(s, a);
         return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 32 + 3>(s, a);
