@@ -1016,6 +1016,12 @@ static hipError_t gv_split(hipStream_t s, const GemvArgs& a) {
     // K-chunks (K = 1024) 4 waves of 4 chunks measured 1-2% faster than 8 of 2
     // on every K = 1024 shape of the decode sweep.
     const int nchunks = (a.kg * 4 + 63) / 64;
+    // K = 3072 and 2048: 8 waves of 6 / 4 chunks rather than 16 of 3 / 2
+    // (batch-8 decode step 1.2137 -> 1.208 ms, batch 4 1.085 -> 1.082; the
+    // configs[1] K = 3072 shapes 0.05-0.1 us faster each; 4 waves of 12 / 8
+    // chunks measured 0.02-0.04 us slower than 8 waves on the same shapes).
+    if (nchunks == 48) return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 6, 1, 8>(s, a);
+    if (nchunks == 32) return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 1, 8>(s, a);
     if (nchunks >= 32) return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 1, 16>(s, a);
     if (nchunks > 16) return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 4, 1, 8>(s, a);
     if (wave_chunks > 4) return gv_go<MT, OUT, HAS_BIAS, ALIGNED, 16, 1>(s, a);
