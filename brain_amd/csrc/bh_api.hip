@@ -32,7 +32,8 @@ hipError_t launch_quantize_rows_bf16(hipStream_t s, const uint16_t* x, int m, in
 hipError_t launch_quantize_weight(hipStream_t s, const float* w, int n, int k, uint32_t* packed, float* sw);
 hipError_t launch_gemv_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n,
-                          bool keep_cached = false);
+                          bool keep_cached = false, float* am_v = nullptr, uint32_t* am_i = nullptr,
+                          uint32_t* am_n = nullptr, int am_stride = 0);
 hipError_t launch_gemm_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n);
 hipError_t launch_gemm_i8_static(hipStream_t s, const uint32_t* xq, const uint32_t* wq, float ssx, float ssw,

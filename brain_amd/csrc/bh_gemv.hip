@@ -21,6 +21,7 @@
 //     for a column group before its first MFMA; the first group's loads are
 //     issued before the activation staging so the two overlap;
 //   - fused epilogue: dequant, bias, bf16 RNE.
+#include <cfloat>
 #include <cstdlib>
 #include <type_traits>
 
@@ -76,6 +77,15 @@ struct GemvArgs {
     // wants them kept in the caches) instead of whole 128-byte lines with
     // the non-temporal hint.
     bool keep_cached = false;
+    // Greedy-argmax partials of the wide-N streaming kernel (null: none):
+    // wave w stores, for every row r < m, the first column of its largest
+    // output (strictly above -FLT_MAX; NaN never wins) at am_v/am_i[r *
+    // am_stride + w], (-FLT_MAX, 0xffffffff) when it has none, and wave 0
+    // stores the number of waves to *am_n.
+    float* am_v = nullptr;
+    uint32_t* am_i = nullptr;
+    uint32_t* am_n = nullptr;
+    int am_stride = 0;
 };
 
 // XMODE: 0 = packed activation read from global memory, 1 = staged into
@@ -709,8 +719,15 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
 // two int8 fragments and feeds two MFMAs against the activation bytes of the
 // same K (a permutation of K inside the chunk shared by both operands, so the
 // sum is exact; the same pairing as gemv_q4_kernel).
-template <int OUT, bool HAS_BIAS, int KB, bool Q4 = false, bool LINES = false>
+__device__ __forceinline__ bool argmax_better(float v, uint32_t i, float bv, uint32_t bi) {
+    if (i == 0xffffffffu) return false;
+    if (bi == 0xffffffffu) return true;
+    return v > bv || (v == bv && i < bi);
+}
+
+template <int OUT, bool HAS_BIAS, int KB, bool Q4 = false, bool LINES = false, bool AM = false>
 __global__ __launch_bounds__(256) void gemv_i8_stream_kernel(GemvArgs a, int groups_per_wave) {
+    static_assert(!AM || OUT == OUT_F32, "argmax over f32 outputs");
     constexpr int U = Q4 ? 8 : 16, kbytes = KB, nbatch = KB / 1024;
     constexpr int wbytes = Q4 ? KB / 2 : KB;  // weight bytes per row
     __shared__ __attribute__((aligned(16))) uint8_t xs[16 * (KB + 16)];
@@ -795,7 +812,39 @@ __global__ __launch_bounds__(256) void gemv_i8_stream_kernel(GemvArgs a, int gro
         sxr[i] = (OUT != OUT_I32 && row < m) ? a.sx[row] : 0.0f;
     }
     __syncthreads();
-    if (items == 0) return;
+    // Argmax partials: this lane's best column for each of its 4 rows.
+    float amv[4] = {-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX};
+    uint32_t ami[4] = {0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
+    auto am_store = [&]() {
+        if constexpr (AM) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int off = 8; off >= 1; off >>= 1) {
+                    const float ov = __shfl_xor(amv[q], off, 64);
+                    const uint32_t oi = __shfl_xor(ami[q], off, 64);
+                    if (argmax_better(ov, oi, amv[q], ami[q])) {
+                        amv[q] = ov;
+                        ami[q] = oi;
+                    }
+                }
+            if ((lane & 15) == 0) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int row = 4 * (lane >> 4) + q;
+                    if (row < m) {
+                        a.am_v[(int64_t)row * a.am_stride + gw] = amv[q];
+                        a.am_i[(int64_t)row * a.am_stride + gw] = ami[q];
+                    }
+                }
+            }
+            if (gw == 0 && lane == 0) *a.am_n = (uint32_t)nwaves;
+        }
+    };
+    if (items == 0) {
+        am_store();
+        return;
+    }
 
     const uint8_t* xrow = xs + (lane & 15) * xstride + (Q4 ? 2 * ksub : ksub);
     v4i acc = {0, 0, 0, 0};
@@ -907,6 +956,15 @@ __global__ __launch_bounds__(256) void gemv_i8_stream_kernel(GemvArgs a, int gro
                 float v = dequant(acc[q], sxr[q], it.sw);
                 if constexpr (HAS_BIAS) v = v + it.bias;
                 pend[0][q] = v;
+                if constexpr (AM) {
+                    // Columns arrive in increasing order: a strictly larger
+                    // value keeps the first index of the maximum.
+                    const int col = (gw + i * nwaves) * 16 + (lane & 15);
+                    if (col < n && v > amv[q]) {
+                        amv[q] = v;
+                        ami[q] = (uint32_t)col;
+                    }
+                }
             }
         }
         acc = v4i{0, 0, 0, 0};
@@ -928,6 +986,7 @@ __global__ __launch_bounds__(256) void gemv_i8_stream_kernel(GemvArgs a, int gro
         load_item(ia, j + 2);
         consume(ib, j + 1);
     }
+    am_store();
 }
 
 // ---------------------------------------------------------------- host side
@@ -954,7 +1013,7 @@ static hipError_t gv_go(hipStream_t s, const GemvArgs& a) {
 
 // The streaming wide-N kernel: as many waves as can be resident (so the
 // whole grid is one round), each owning an equal share of the column groups.
-template <int OUT, bool HAS_BIAS, int KB, bool Q4 = false, bool LINES = false>
+template <int OUT, bool HAS_BIAS, int KB, bool Q4 = false, bool LINES = false, bool AM = false>
 static hipError_t gv_stream_kb(hipStream_t s, const GemvArgs& a) {
     // Resident waves (the whole grid is one round).
     static const int slots = [] {
@@ -962,7 +1021,7 @@ static hipError_t gv_stream_kb(hipStream_t s, const GemvArgs& a) {
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
             cus = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_i8_stream_kernel<OUT, HAS_BIAS, KB, Q4, LINES>, 256,
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_i8_stream_kernel<OUT, HAS_BIAS, KB, Q4, LINES, AM>, 256,
                                                          0) !=
                 hipSuccess || per_cu < 1)
             per_cu = 1;
@@ -971,7 +1030,8 @@ static hipError_t gv_stream_kb(hipStream_t s, const GemvArgs& a) {
     const int ngroups = (a.n + 15) / 16;
     const int gpw = (ngroups + slots - 1) / slots;  // groups per wave
     const int waves = (ngroups + gpw - 1) / gpw;    // balanced: every wave gpw or gpw-1 groups
-    gemv_i8_stream_kernel<OUT, HAS_BIAS, KB, Q4, LINES><<<(waves + 3) / 4, 256, 0, s>>>(a, gpw);
+    if (AM && ((waves + 3) / 4) * 4 > a.am_stride) return hipErrorInvalidValue;
+    gemv_i8_stream_kernel<OUT, HAS_BIAS, KB, Q4, LINES, AM><<<(waves + 3) / 4, 256, 0, s>>>(a, gpw);
     return hipGetLastError();
 }
 
@@ -979,6 +1039,10 @@ static hipError_t gv_stream_kb(hipStream_t s, const GemvArgs& a) {
 // of the 1024-wide decoder), m <= 16.
 template <int OUT, bool HAS_BIAS>
 static hipError_t gv_stream(hipStream_t s, const GemvArgs& a) {
+    if constexpr (OUT == OUT_F32 && !HAS_BIAS) {
+        if (a.am_v) return gv_stream_kb<OUT, HAS_BIAS, 1024, false, false, true>(s, a);
+    }
+    if (a.am_v) return hipErrorNotSupported;
     if (a.keep_cached) return gv_stream_kb<OUT, HAS_BIAS, 1024>(s, a);
     return gv_stream_kb<OUT, HAS_BIAS, 1024, false, true>(s, a);
 }
@@ -1075,12 +1139,22 @@ hipError_t launch_gemv_q4_stream(hipStream_t s, const uint32_t* xq, const uint32
 // Preconditions are checked by the C-ABI layer: 1 <= m <= 32, kg >= 0, n >= 1.
 hipError_t launch_gemv_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n,
-                          bool keep_cached = false) {
+                          bool keep_cached = false, float* am_v = nullptr, uint32_t* am_i = nullptr,
+                          uint32_t* am_n = nullptr, int am_stride = 0) {
     const bool aligned = ((kg * 4) % 16 == 0) && ((reinterpret_cast<uintptr_t>(xq) & 15u) == 0) &&
                          ((reinterpret_cast<uintptr_t>(wq) & 15u) == 0);
     GemvArgs a{xq, wq, sx, sw, bias, out, m, kg, n, nullptr, 0, 0, nullptr, nullptr, nullptr,
                nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0.0f};
     a.keep_cached = keep_cached;
+    if (am_v) {
+        // The argmax partials come from the wide-N streaming kernel only.
+        if (!aligned || m > 16 || kg != 256 || (n + 15) / 16 < 1024 || out_dtype != OUT_F32 || bias || gv_cfg() != 0)
+            return hipErrorNotSupported;
+        a.am_v = am_v;
+        a.am_i = am_i;
+        a.am_n = am_n;
+        a.am_stride = am_stride;
+    }
     if (m <= 16) return gv_out<1>(s, aligned, out_dtype, a);
     return gv_out<2>(s, aligned, out_dtype, a);
 }

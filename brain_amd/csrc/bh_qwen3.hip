@@ -51,7 +51,8 @@ hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, flo
 hipError_t launch_quantize_weight(hipStream_t s, const float* w, int n, int k, uint32_t* packed, float* sw);
 hipError_t launch_gemv_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n,
-                          bool keep_cached = false);
+                          bool keep_cached = false, float* am_v = nullptr, uint32_t* am_i = nullptr,
+                          uint32_t* am_n = nullptr, int am_stride = 0);
 hipError_t gemm_reserve(hipStream_t s, int m, int kg, int n);
 hipError_t launch_gemm_i8(hipStream_t s, const uint32_t* xq, const uint32_t* wq, const float* sx,
                           const float* sw, const float* bias, void* out, int out_dtype, int m, int kg, int n);
@@ -68,6 +69,7 @@ namespace {
 
 constexpr int RT = 256;       // threads of the row kernels
 constexpr int AM_CH = 64;     // argmax chunks per row
+constexpr int AM_PARTS = 4096;  // argmax partials per row from the streaming LM head (one per wave)
 constexpr int MAX_GROUP = 8;  // query heads per kv head
 constexpr uint32_t NO_INDEX = 0xffffffffu;
 
@@ -1058,6 +1060,36 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* pv, const
     }
 }
 
+// Stage 2 over the LM head's own partials (one per wave of the streaming
+// kernel, *np of them per row, stride AM_PARTS); otherwise as above.
+__global__ __launch_bounds__(64) void argmax_final_parts_kernel(const float* pv, const uint32_t* pi,
+                                                                const uint32_t* np, uint32_t* tok, uint32_t* pos,
+                                                                uint32_t* hist, const uint32_t* ctl, int batch) {
+    const int b = blockIdx.x, lane = threadIdx.x;
+    const int nparts = (int)*np;
+    float v = -FLT_MAX;
+    uint32_t i = NO_INDEX;
+    for (int w = lane; w < nparts; w += 64) {
+        const float ov = pv[(size_t)b * AM_PARTS + w];
+        const uint32_t oi = pi[(size_t)b * AM_PARTS + w];
+        if (am_better(ov, oi, v, i)) {
+            v = ov;
+            i = oi;
+        }
+    }
+    am_wave(v, i);
+    if (lane == 0) {
+        const uint32_t idx = i == NO_INDEX ? 0u : i;
+        tok[b] = idx;
+        if (hist) {
+            const uint32_t p = pos[b];
+            const uint32_t k = p - ctl[0];
+            if (k < ctl[1]) hist[(size_t)k * batch + b] = idx;
+            pos[b] = p + 1;
+        }
+    }
+}
+
 // Counter-based normal generator for the random init: SplitMix64 of
 // (key + i), two 24-bit uniforms, Box-Muller.
 __device__ __forceinline__ uint64_t splitmix(uint64_t z) {
@@ -1122,7 +1154,7 @@ struct bh_qwen3 {
     uint32_t max_splits = 0;
     const uint32_t* cur_pos = nullptr;
     float *sx = nullptr, *logits = nullptr, *tmpw = nullptr, *am_v = nullptr;
-    uint32_t *xq = nullptr, *am_i = nullptr;  // xq: every producer writes rows of width/4 words
+    uint32_t *xq = nullptr, *am_i = nullptr, *am_n = nullptr;  // xq: every producer writes rows of width/4 words
     uint32_t *tok_rows = nullptr, *pos_rows = nullptr, *seq_rows = nullptr;
     int* row_map = nullptr;
     uint32_t *tok_dec = nullptr, *pos_dec = nullptr, *seq_dec = nullptr, *hist = nullptr, *ctl = nullptr;
@@ -1272,6 +1304,12 @@ int fuse_norm_rows() {
 int fuse_swiglu_rows() {
     static const int v = env_rows("BH_QWEN3_FUSE_SWIGLU_ROWS", 4);
     return v;
+}
+// BH_QWEN3_ARGMAX_SEPARATE=1: the argmax's first stage as its own kernel
+// even where the streaming head could carry it (for measurement).
+static bool am_separate() {
+    static const int v = env_rows("BH_QWEN3_ARGMAX_SEPARATE", 0);
+    return v != 0;
 }
 
 // `splits`: key chunks of KCH covering the longest row of this launch (the
@@ -1426,6 +1464,22 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
     // The head's weights are re-read every step and fit the Infinity Cache
     // (measured: batch-1 step 0.861 ms with ordinary loads, 0.863-0.864 with
     // the streaming form that is faster on cold weights).
+    // The argmax's first stage rides in the streaming head GEMV when that is
+    // the kernel the head runs on (one partial per wave); otherwise its own
+    // kernel over the logits.
+    const int tuned = tuned_variant((uint32_t)n_out, c.vocab, (uint32_t)d);
+    const bool head_gemv = tuned ? tuned == BH_VARIANT_WORKGROUP_PER_OUTPUT : n_out <= 32;
+    hipError_t herr = hipErrorNotSupported;
+    if (head_gemv && !am_separate())
+        herr = launch_gemv_i8(e->stream, e->xq, e->head, e->sx, e->shead, nullptr, e->logits, OUT_F32, n_out, d / 4,
+                              (int)c.vocab, true, e->am_v, e->am_i, e->am_n, AM_PARTS);
+    if (herr == hipSuccess) {
+        argmax_final_parts_kernel<<<n_out, 64, 0, e->stream>>>(e->am_v, e->am_i, e->am_n, e->tok_dec, e->pos_dec,
+                                                               decode ? e->hist : nullptr, e->ctl, n_out);
+        BH_HIP(hipGetLastError(), "argmax_final launch");
+        return BH_OK;
+    }
+    if (herr != hipErrorNotSupported) BH_HIP(herr, "int8 head launch");
     BH_TRY(launch_linear(e, e->head, e->shead, e->logits, n_out, d, (int)c.vocab, true));
     argmax_part_kernel<<<dim3(AM_CH, n_out), RT, 0, e->stream>>>(e->logits, (int)c.vocab, e->am_v, e->am_i);
     BH_HIP(hipGetLastError(), "argmax_part launch");
@@ -1637,7 +1691,8 @@ int bh_qwen3_create(const bh_qwen3_config* cfg, uint32_t max_batch, uint32_t max
         (rc = dalloc(e, &e->part_o, R * c.n_heads * e->max_splits * c.head_dim)) || (rc = dalloc(e, &e->part_ml, R * c.n_heads * e->max_splits * 2)) || (rc = dalloc(e, &e->proj, R * d)) || (rc = dalloc(e, &e->gu, R * 2 * ff)) ||
         (rc = dalloc(e, &e->sx, R)) || (rc = dalloc(e, &e->xq, R * e->xq_words)) ||
         (rc = dalloc(e, &e->logits, (uint64_t)max_batch * c.vocab)) || (rc = dalloc(e, &e->tmpw, e->tmpw_floats)) ||
-        (rc = dalloc(e, &e->am_v, (uint64_t)max_batch * AM_CH)) || (rc = dalloc(e, &e->am_i, (uint64_t)max_batch * AM_CH)) ||
+        (rc = dalloc(e, &e->am_v, (uint64_t)max_batch * AM_PARTS)) || (rc = dalloc(e, &e->am_i, (uint64_t)max_batch * AM_PARTS)) ||
+        (rc = dalloc(e, &e->am_n, 1)) ||
         (rc = dalloc(e, &e->tok_rows, R)) || (rc = dalloc(e, &e->pos_rows, R)) || (rc = dalloc(e, &e->seq_rows, R)) ||
         (rc = dalloc(e, &e->row_map, max_batch)) || (rc = dalloc(e, &e->tok_dec, max_batch)) ||
         (rc = dalloc(e, &e->pos_dec, max_batch)) || (rc = dalloc(e, &e->seq_dec, max_batch)) ||
