@@ -1061,24 +1061,46 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* pv, const
 }
 
 // Stage 2 over the LM head's own partials (one per wave of the streaming
-// kernel, *np of them per row, stride AM_PARTS); otherwise as above.
-__global__ __launch_bounds__(64) void argmax_final_parts_kernel(const float* pv, const uint32_t* pi,
-                                                                const uint32_t* np, uint32_t* tok, uint32_t* pos,
-                                                                uint32_t* hist, const uint32_t* ctl, int batch) {
-    const int b = blockIdx.x, lane = threadIdx.x;
+// kernel, *np of them per row, stride AM_PARTS); otherwise as above. 256
+// threads, every thread's loads issued before the first comparison.
+constexpr int AMF_T = 256, AMF_L = 4;  // threads, loads per thread and round
+__global__ __launch_bounds__(AMF_T) void argmax_final_parts_kernel(const float* pv, const uint32_t* pi,
+                                                                   const uint32_t* np, uint32_t* tok, uint32_t* pos,
+                                                                   uint32_t* hist, const uint32_t* ctl, int batch) {
+    const int b = blockIdx.x, t = threadIdx.x;
     const int nparts = (int)*np;
     float v = -FLT_MAX;
     uint32_t i = NO_INDEX;
-    for (int w = lane; w < nparts; w += 64) {
-        const float ov = pv[(size_t)b * AM_PARTS + w];
-        const uint32_t oi = pi[(size_t)b * AM_PARTS + w];
-        if (am_better(ov, oi, v, i)) {
-            v = ov;
-            i = oi;
+    for (int w0 = 0; w0 < nparts; w0 += AMF_T * AMF_L) {
+        float ov[AMF_L];
+        uint32_t oi[AMF_L];
+#pragma unroll
+        for (int k = 0; k < AMF_L; ++k) {
+            const int w = min(w0 + t + AMF_T * k, nparts - 1);  // clamped repeats never win over themselves
+            ov[k] = pv[(size_t)b * AM_PARTS + w];
+            oi[k] = pi[(size_t)b * AM_PARTS + w];
         }
+#pragma unroll
+        for (int k = 0; k < AMF_L; ++k)
+            if (am_better(ov[k], oi[k], v, i)) {
+                v = ov[k];
+                i = oi[k];
+            }
     }
     am_wave(v, i);
-    if (lane == 0) {
+    __shared__ float rv[AMF_T / 64];
+    __shared__ uint32_t ri[AMF_T / 64];
+    if ((t & 63) == 0) {
+        rv[t >> 6] = v;
+        ri[t >> 6] = i;
+    }
+    __syncthreads();
+    if (t == 0) {
+        for (int w = 1; w < AMF_T / 64; ++w)
+            if (am_better(rv[w], ri[w], v, i)) {
+                v = rv[w];
+                i = ri[w];
+            }
         const uint32_t idx = i == NO_INDEX ? 0u : i;
         tok[b] = idx;
         if (hist) {
@@ -1474,8 +1496,9 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
         herr = launch_gemv_i8(e->stream, e->xq, e->head, e->sx, e->shead, nullptr, e->logits, OUT_F32, n_out, d / 4,
                               (int)c.vocab, true, e->am_v, e->am_i, e->am_n, AM_PARTS);
     if (herr == hipSuccess) {
-        argmax_final_parts_kernel<<<n_out, 64, 0, e->stream>>>(e->am_v, e->am_i, e->am_n, e->tok_dec, e->pos_dec,
-                                                               decode ? e->hist : nullptr, e->ctl, n_out);
+        argmax_final_parts_kernel<<<n_out, AMF_T, 0, e->stream>>>(e->am_v, e->am_i, e->am_n, e->tok_dec,
+                                                                  e->pos_dec, decode ? e->hist : nullptr, e->ctl,
+                                                                  n_out);
         BH_HIP(hipGetLastError(), "argmax_final launch");
         return BH_OK;
     }
