@@ -141,8 +141,13 @@ static hipError_t q4_go(hipStream_t s, const GemvQ4Args& a) {
     // workgroup so enough waves stream the weights, up to 4 chunks per pass.
     if (groups >= 1024 && nchunks <= 16 && a.m <= 4)
         gemv_q4_kernel<MT, OUT, HAS_BIAS, ALIGNED, 4, 8, 4><<<(groups + 3) / 4, 256, 0, s>>>(a);
+    // Narrow N: 8 waves per column group. Measured (cold, per launch) against
+    // 4 waves: K = 3072 4.04 -> 3.45 us at M = 1, 4.96 -> 4.39 at M = 16 (8
+    // waves of 3 chunks; 4 waves of 6: 3.6 / 4.6); K = 1024 2.87 -> 2.67 and
+    // 3.26 -> 3.04 (8 waves of 1 chunk; 4 waves of 2: 2.70 / 3.10).
     else if (nchunks >= 32) gemv_q4_kernel<MT, OUT, HAS_BIAS, ALIGNED, 8, 4><<<groups, 512, 0, s>>>(a);
-    else gemv_q4_kernel<MT, OUT, HAS_BIAS, ALIGNED, 4, 4><<<groups, 256, 0, s>>>(a);
+    else if (nchunks > 16) gemv_q4_kernel<MT, OUT, HAS_BIAS, ALIGNED, 8, 3><<<groups, 512, 0, s>>>(a);
+    else gemv_q4_kernel<MT, OUT, HAS_BIAS, ALIGNED, 8, 1><<<groups, 512, 0, s>>>(a);
     return hipGetLastError();
 }
 
