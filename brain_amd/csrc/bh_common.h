@@ -11,6 +11,57 @@ int fail(int code, const char* fmt, ...);
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
+// Cross-lane exchange on the VALU: the value of lane (lane ^ OFF) of a
+// 64-lane wave, bit for bit what __shfl_xor(v, OFF, 64) returns. __shfl_xor
+// is a ds_bpermute through the LDS unit, ~110 cycles per dependent step on
+// MI355X (a 6-step wave reduction then costs ~0.3 us of a decode kernel's
+// critical path); these are a few cycles each. OFF 1 and 2: DPP quad_perm;
+// 4: DPP row_ror:4 (lane l - 4 within its row of 16) or row_ror:12 (l + 4),
+// picked by bit 2 of the lane; 8: row_ror:8; 16 and 32: gfx950's
+// v_permlane16_swap / v_permlane32_swap of the value with itself, whose two
+// results hold the value unchanged in one and the partner's in the other,
+// lane by lane (the one that differs from the value is the partner's; where
+// neither differs they are equal). Call with the whole wave active.
+template <int OFF>
+__device__ __forceinline__ uint32_t xor_lane_u(uint32_t u) {
+    static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "lane xor offset");
+    const int x = (int)u;
+    if constexpr (OFF == 32 || OFF == 16) {
+        const auto r = OFF == 32 ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
+                                 : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        return r[0] != u ? (uint32_t)r[0] : (uint32_t)r[1];
+    } else if constexpr (OFF == 8) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false);
+    } else if constexpr (OFF == 4) {
+        const int dn = __builtin_amdgcn_mov_dpp(x, 0x124, 0xF, 0xF, false);
+        const int up = __builtin_amdgcn_mov_dpp(x, 0x12C, 0xF, 0xF, false);
+        const uint32_t lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+        return (uint32_t)((lane & 4u) ? dn : up);
+    } else if constexpr (OFF == 2) {
+        return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);
+    } else {
+        return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);
+    }
+}
+template <int OFF>
+__device__ __forceinline__ float xor_lane(float v) {
+    return __builtin_bit_cast(float, xor_lane_u<OFF>(__builtin_bit_cast(uint32_t, v)));
+}
+// The butterfly reductions `for (off = HI; off >= 1; off >>= 1) v = v (+|max) xor(v, off)`,
+// step for step (the same additions in the same order, so the same sum).
+template <int HI>
+__device__ __forceinline__ float xor_sum(float v) {
+    v += xor_lane<HI>(v);
+    if constexpr (HI > 1) v = xor_sum<HI / 2>(v);
+    return v;
+}
+template <int HI>
+__device__ __forceinline__ float xor_max(float v) {
+    v = fmaxf(v, xor_lane<HI>(v));
+    if constexpr (HI > 1) v = xor_max<HI / 2>(v);
+    return v;
+}
+
 // Output element types of the dequant epilogue.
 // OUT_I32 stores the raw accumulator (scales and bias unused): the hook the
 // parity tests use to check the integer sums themselves.

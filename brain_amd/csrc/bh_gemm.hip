@@ -1491,8 +1491,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_quant_kernel(GemmArgs a, fl
         for (int j = 0; j < 2; ++j)
             amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(w[j] << 16)), fabsf(__uint_as_float(w[j] & 0xffff0000u))));
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    amax = xor_max<32>(amax);
     __shared__ float red[4];
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
     __syncthreads();

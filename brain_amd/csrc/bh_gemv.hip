@@ -258,8 +258,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
                 am = fmaxf(am, fmaxf(fmaxf(fabsf(h[gi].x), fabsf(h[gi].y)), fmaxf(fabsf(h[gi].z), fabsf(h[gi].w))));
             }
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+        am = xor_max<32>(am);
         if (lane == 0) pm[wave] = am;
         __syncthreads();
         float rm = pm[0];
@@ -314,37 +313,44 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
 #pragma unroll
                 for (int j = 0; j < RMAX; ++j) rc[j] = min(r0 + grp + NG * j, m - 1);
                 if constexpr (XMODE == 3) {
+                    // Row sources: the token's embedding row (the first
+                    // layer; a dependent load), else pre_a; then pre_b (the
+                    // residual's delta), or the first source again. Both
+                    // loads are unconditional: with a load in each branch
+                    // the compiler waited at the join for every load in
+                    // flight, the weights from HBM included, before issuing
+                    // the next ones (two memory round trips instead of one).
+                    const float* sa[RMAX];
+                    const float* sb[RMAX];
                     if (a.pre_tok) {
-                        int tk[RMAX];
 #pragma unroll
-                        for (int j = 0; j < RMAX; ++j) tk[j] = (int)a.pre_tok[rc[j]];
+                        for (int j = 0; j < RMAX; ++j) {
+                            sa[j] = a.pre_emb + (size_t)a.pre_tok[rc[j]] * d;
+                            sb[j] = sa[j];
+                        }
+                    } else {
 #pragma unroll
-                        for (int j = 0; j < RMAX; ++j)
+                        for (int j = 0; j < RMAX; ++j) {
+                            sa[j] = a.pre_a + (size_t)rc[j] * d;
+                            sb[j] = a.pre_b ? a.pre_b + (size_t)rc[j] * d : sa[j];
+                        }
+                    }
+                    float4 bv[RMAX][G];
 #pragma unroll
-                            for (int g = 0; g < G; ++g)
-                                v[j][g] = reinterpret_cast<const float4*>(a.pre_emb + (size_t)tk[j] * d)[min(gt + 256 * g, d4 - 1)];
-                    } else if (a.pre_b) {
-                        float4 bv[RMAX][G];
+                    for (int j = 0; j < RMAX; ++j)
 #pragma unroll
-                        for (int j = 0; j < RMAX; ++j)
-#pragma unroll
-                            for (int g = 0; g < G; ++g) {
-                                const int ic = min(gt + 256 * g, d4 - 1);
-                                v[j][g] = reinterpret_cast<const float4*>(a.pre_a + (size_t)rc[j] * d)[ic];
-                                bv[j][g] = reinterpret_cast<const float4*>(a.pre_b + (size_t)rc[j] * d)[ic];
-                            }
+                        for (int g = 0; g < G; ++g) {
+                            const int ic = min(gt + 256 * g, d4 - 1);
+                            v[j][g] = reinterpret_cast<const float4*>(sa[j])[ic];
+                            bv[j][g] = reinterpret_cast<const float4*>(sb[j])[ic];
+                        }
+                    if (a.pre_b && !a.pre_tok) {
 #pragma unroll
                         for (int j = 0; j < RMAX; ++j)
 #pragma unroll
                             for (int g = 0; g < G; ++g)
                                 v[j][g] = make_float4(v[j][g].x + bv[j][g].x, v[j][g].y + bv[j][g].y,
                                                       v[j][g].z + bv[j][g].z, v[j][g].w + bv[j][g].w);
-                    } else {
-#pragma unroll
-                        for (int j = 0; j < RMAX; ++j)
-#pragma unroll
-                            for (int g = 0; g < G; ++g)
-                                v[j][g] = reinterpret_cast<const float4*>(a.pre_a + (size_t)rc[j] * d)[min(gt + 256 * g, d4 - 1)];
                     }
                 } else {
                     float4 uv[RMAX][G];
@@ -384,8 +390,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
                             if (first && r < m && gt + 256 * g < d4)
                                 reinterpret_cast<float4*>(a.res_out + (size_t)r * d)[gt + 256 * g] = x;
                         }
-#pragma unroll
-                        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+                        ss = xor_sum<32>(ss);
                         if (lane == 0) gred[j][wave] = ss;
                     }
                     __syncthreads();
@@ -410,8 +415,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
                     for (int g = 0; g < G; ++g)
                         am = fmaxf(am, fmaxf(fmaxf(fabsf(v[j][g].x), fabsf(v[j][g].y)),
                                              fmaxf(fabsf(v[j][g].z), fabsf(v[j][g].w))));
-#pragma unroll
-                    for (int off = 32; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+                    am = xor_max<32>(am);
                     if (lane == 0) gmx[j][wave] = am;
                 }
                 __syncthreads();
@@ -467,8 +471,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
                     const float4 v = xr[c];
                     mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
                 }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+            mx = xor_max<32>(mx);
             if (lane == 0) pmax[wave] = mx;
             __syncthreads();
             if (r < m) {
@@ -526,8 +529,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
                     am = fmaxf(am, fmaxf(fmaxf(fabsf(y[gi].x), fabsf(y[gi].y)), fmaxf(fabsf(y[gi].z), fabsf(y[gi].w))));
                 }
             }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+            am = xor_max<32>(am);
             if (lane == 0) pm[wave] = am;
             __syncthreads();
             float rm = pm[0];
@@ -817,17 +819,21 @@ __global__ __launch_bounds__(256) void gemv_i8_stream_kernel(GemvArgs a, int gro
     uint32_t ami[4] = {0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
     auto am_store = [&]() {
         if constexpr (AM) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int off = 8; off >= 1; off >>= 1) {
-                    const float ov = __shfl_xor(amv[q], off, 64);
-                    const uint32_t oi = __shfl_xor(ami[q], off, 64);
-                    if (argmax_better(ov, oi, amv[q], ami[q])) {
-                        amv[q] = ov;
-                        ami[q] = oi;
-                    }
+            auto step = [&](int q, auto off) {
+                const float ov = xor_lane<decltype(off)::value>(amv[q]);
+                const uint32_t oi = xor_lane_u<decltype(off)::value>(ami[q]);
+                if (argmax_better(ov, oi, amv[q], ami[q])) {
+                    amv[q] = ov;
+                    ami[q] = oi;
                 }
+            };
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                step(q, std::integral_constant<int, 8>{});
+                step(q, std::integral_constant<int, 4>{});
+                step(q, std::integral_constant<int, 2>{});
+                step(q, std::integral_constant<int, 1>{});
+            }
             if ((lane & 15) == 0) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {

@@ -40,8 +40,7 @@ __global__ __launch_bounds__(64) void paged_kv_append_i8_kernel(const float* src
             mx = fmaxf(mx, fabsf(v[j]));
         }
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    mx = xor_max<32>(mx);
     float scale = fminf(mx, clip[head]) / 127.0f;
     if (scale == 0.0f) scale = 1.0f;
     const uint64_t slot = (uint64_t)blocks[b] * bs + offsets[b];

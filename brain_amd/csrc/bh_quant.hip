@@ -31,8 +31,7 @@ __device__ __forceinline__ float row_absmax(const float* __restrict__ row, int k
     } else {
         for (int i = threadIdx.x; i < k; i += QT) a = fmaxf(a, fabsf(row[i]));
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
+    a = xor_max<32>(a);
     __shared__ float red[QT / 64];
     const int wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) red[wave] = a;
@@ -92,8 +91,7 @@ __global__ __launch_bounds__(QT) void quantize_rows_reg_kernel(const float* __re
         v[i] = g < kg ? xr[g] : make_float4(0.f, 0.f, 0.f, 0.f);
         a = fmaxf(a, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
+    a = xor_max<32>(a);
     __shared__ float red[QT / 64];
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = a;
     __syncthreads();
@@ -135,8 +133,7 @@ __global__ __launch_bounds__(QT) void quantize_rows_wave_kernel(const float* __r
 #pragma unroll
     for (int i = 0; i < NV; ++i)
         a = fmaxf(a, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
+    a = xor_max<32>(a);
     const float s = fmaxf(a, 1e-8f) / 127.0f;
     if (lane == 0) sx[row] = s;
     const float inv = 1.0f / s;
@@ -197,8 +194,7 @@ __global__ __launch_bounds__(QT) void quantize_rows_bf16_kernel(const uint16_t* 
 #pragma unroll
         for (int j = 0; j < 4; ++j) a = fmaxf(a, fmaxf(fabsf(bf16_lo(w[j])), fabsf(bf16_hi(w[j]))));
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
+    a = xor_max<32>(a);
     __shared__ float red[QT / 64];
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = a;
     __syncthreads();
@@ -228,8 +224,7 @@ __global__ __launch_bounds__(QT) void quantize_rows_bf16_any_kernel(const uint16
     const uint16_t* xr = x + (int64_t)row * k;
     float a = 0.0f;
     for (int i = threadIdx.x; i < k; i += QT) a = fmaxf(a, fabsf(__uint_as_float((uint32_t)xr[i] << 16)));
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
+    a = xor_max<32>(a);
     __shared__ float red[QT / 64];
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = a;
     __syncthreads();
@@ -279,8 +274,7 @@ __global__ __launch_bounds__(QT) void quantize_weight_wave_kernel(const float* _
 #pragma unroll
     for (int i = 0; i < NV; ++i)
         a = fmaxf(a, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
+    a = xor_max<32>(a);
     const float s = fmaxf(a, 1e-8f) / 127.0f;
     if (lane == 0) sw[row] = s;
     const float inv = 1.0f / s;

@@ -74,13 +74,11 @@ constexpr int MAX_GROUP = 8;  // query heads per kv head
 constexpr uint32_t NO_INDEX = 0xffffffffu;
 
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    v = xor_sum<32>(v);
     return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    v = xor_max<32>(v);
     return v;
 }
 // Block-wide reductions over RT threads; `red` holds RT/64 floats. Safe to
@@ -701,9 +699,9 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
         for (int g = 0; g < MAX_GROUP; ++g) {
             if (g >= G) break;
             float v = acc[g];
-            v += __shfl_xor(v, 4, 64);
-            v += __shfl_xor(v, 2, 64);
-            v += __shfl_xor(v, 1, 64);
+            v += xor_lane<4>(v);
+            v += xor_lane<2>(v);
+            v += xor_lane<1>(v);
             if (KV8 && kk < n) v = v * ksc[kk];
             if (l8 == 0) es[g * KCH + kk] = v * p.scale;
         }
@@ -715,12 +713,10 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
         const bool live = g < G && k < n;
         const float s = live ? es[g * KCH + k] : -INFINITY;
         float m = s;
-#pragma unroll
-        for (int off = KCH / 2; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        m = xor_max<KCH / 2>(m);
         const float e = live ? expf(s - m) : 0.0f;
         float l = e;
-#pragma unroll
-        for (int off = KCH / 2; off >= 1; off >>= 1) l += __shfl_xor(l, off, 64);
+        l = xor_sum<KCH / 2>(l);
         __syncthreads();
         if (g < G) es[g * KCH + k] = e;
         if (g < G && k == 0) {
@@ -880,18 +876,18 @@ __global__ __launch_bounds__(RT) void attn_prefill_kernel(AttnArgs p, int rows_p
             sv[c] = Ps[q][k4 + c];
             mx = fmaxf(mx, sv[c]);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+        mx = fmaxf(mx, xor_lane<1>(mx));
+        mx = fmaxf(mx, xor_lane<2>(mx));
+        mx = fmaxf(mx, xor_lane<4>(mx));
         float sum = 0.0f;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             sv[c] = sv[c] == -INFINITY ? 0.0f : expf(sv[c] - mx);
             sum += sv[c];
         }
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        sum += __shfl_xor(sum, 4, 64);
+        sum += xor_lane<1>(sum);
+        sum += xor_lane<2>(sum);
+        sum += xor_lane<4>(sum);
 #pragma unroll
         for (int c = 0; c < 4; ++c) Ps[q][k4 + c] = sv[c];
         if ((tid & 7) == 0) {
@@ -994,16 +990,22 @@ __device__ __forceinline__ bool am_better(float v, uint32_t i, float bv, uint32_
     if (bi == NO_INDEX) return true;
     return v > bv || (v == bv && i < bi);
 }
-__device__ __forceinline__ void am_wave(float& v, uint32_t& i) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(v, off, 64);
-        const uint32_t oi = __shfl_xor(i, off, 64);
-        if (am_better(ov, oi, v, i)) {
-            v = ov;
-            i = oi;
-        }
+template <int OFF>
+__device__ __forceinline__ void am_step(float& v, uint32_t& i) {
+    const float ov = xor_lane<OFF>(v);
+    const uint32_t oi = xor_lane_u<OFF>(i);
+    if (am_better(ov, oi, v, i)) {
+        v = ov;
+        i = oi;
     }
+}
+__device__ __forceinline__ void am_wave(float& v, uint32_t& i) {
+    am_step<32>(v, i);
+    am_step<16>(v, i);
+    am_step<8>(v, i);
+    am_step<4>(v, i);
+    am_step<2>(v, i);
+    am_step<1>(v, i);
 }
 __global__ __launch_bounds__(RT) void argmax_part_kernel(const float* logits, int vocab, float* pv, uint32_t* pi) {
     __shared__ float rv[RT / 64];
