@@ -94,6 +94,50 @@ __device__ __forceinline__ void attn_load_first4(const float* part_o, const floa
     }
 }
 
+// The context pieces only of attn_load_first4 (HEAD32 merge: the chunk
+// statistics are loaded one per lane).
+__device__ __forceinline__ void attn_load_first4_o(const float* part_o, size_t hs, int splits, int d, int hd,
+                                                   AttnFirst4& b) {
+#pragma unroll
+    for (int j = 0; j < ATTN_SB; ++j)
+        b.ov[j] = j < splits ? *reinterpret_cast<const float4*>(part_o + (hs + j) * hd + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+// attn_combine_first4 for a head held by one 32-lane half of a wave (head_dim
+// 128: 4 context elements per lane) whose chunk statistics sit one per lane:
+// lane q of the half holds (m, l) of chunk q (mlq). Every chunk's weight
+// e^(m_q - M) is evaluated once, on lane q, instead of on all 32 lanes, and
+// read by the others with v_readlane; M is the same maximum, and L and the
+// context sum the same products in the same chunk order, so the result is
+// attn_combine_first4's bit for bit. ns <= ATTN_SB; whole wave active.
+__device__ __forceinline__ float4 attn_combine_head32(float2 mlq, int ns, const AttnFirst4& b) {
+    const uint32_t lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    const int q = (int)(lane & 31u);
+    const float mq = q < ns ? mlq.x : -INFINITY;
+    const float M = xor_max<16>(mq);
+    const float wq = q < ns ? expf(mq - M) : 0.0f;
+    const float lwq = mlq.y * wq;
+    const bool hi = lane >= 32u;
+    float L = 0.0f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < ATTN_SB; ++j) {
+        if (j >= ns) continue;
+        const float wl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wq), j));
+        const float wh = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wq), 32 + j));
+        const float ll = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lwq), j));
+        const float lh = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lwq), 32 + j));
+        const float w = hi ? wh : wl;
+        L += hi ? lh : ll;
+        o = make_float4(o.x + b.ov[j].x * w, o.y + b.ov[j].y * w, o.z + b.ov[j].z * w, o.w + b.ov[j].w * w);
+        // Keeps each chunk's reads next to their use (hoisted, the 64 scalar
+        // results outgrow the scalar registers and spill).
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const float inv = 1.0f / L;
+    return make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+}
+
 // attn_combine4 over ns chunks from a preloaded first batch: the same
 // operations in the same order (the one-batch form when ns <= SB, else the
 // batched form, which reloads).

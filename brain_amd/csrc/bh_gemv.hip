@@ -501,7 +501,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
         // row max exact in any order), so the codes and scales are its own.
         // K <= 2048 (launch_gemv_i8_merge): one group per thread from 8 waves,
         // which keeps a thread's 16 preloaded chunk slots in registers.
+        // PRE == 2 (HEAD32): head_dim 128, K = 2048 and at most ATTN_SB
+        // chunks (512 positions), on 8 waves, so every
+        // lane holds one context group and each head is one half-wave; the
+        // chunk statistics are loaded and the chunk weights evaluated once
+        // per chunk (attn_combine_head32) instead of on every lane of the
+        // head (16 of the exponentials' ~14 instructions each per lane
+        // before). The same results.
         constexpr int NTH = NW * 64, GX = (512 + NTH - 1) / NTH;
+        constexpr bool HEAD32 = PRE == 2;
+        static_assert(!HEAD32 || (NTH == 512 && GX == 1), "one context group per lane");
         __shared__ float pm[NW];
         const int q4 = kbytes >> 2;
         for (int r = 0; r < m; ++r) {
@@ -516,15 +525,23 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
                 const int e = (live[gi] ? i : 0) * 4, h = e / a.hd;
                 dd[gi] = e - h * a.hd;
                 hs[gi] = ((size_t)r * a.nh + h) * a.splits;
-                attn_load_first4(a.part_o, a.part_ml, hs[gi], live[gi] ? a.splits : 0, dd[gi], a.hd, fb[gi]);
+                if constexpr (HEAD32) attn_load_first4_o(a.part_o, hs[gi], a.splits, dd[gi], a.hd, fb[gi]);
+                else attn_load_first4(a.part_o, a.part_ml, hs[gi], live[gi] ? a.splits : 0, dd[gi], a.hd, fb[gi]);
             }
+            // HEAD32: lane q of each half-wave loads chunk q's (m, l).
+            float2 mlq = make_float2(0.f, 0.f);
+            if constexpr (HEAD32)
+                mlq = reinterpret_cast<const float2*>(a.part_ml)[hs[0] + min((int)(lane & 31), a.splits - 1)];
             const int ns = ((int)a.pos[r] + ATTN_KCH) / ATTN_KCH;
             float4 y[GX];
             float am = 0.0f;
 #pragma unroll
             for (int gi = 0; gi < GX; ++gi) {
                 y[gi] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (live[gi]) {
+                if constexpr (HEAD32) {
+                    y[gi] = attn_combine_head32(mlq, ns, fb[gi]);  // splits <= ATTN_SB
+                    am = fmaxf(am, fmaxf(fmaxf(fabsf(y[gi].x), fabsf(y[gi].y)), fmaxf(fabsf(y[gi].z), fabsf(y[gi].w))));
+                } else if (live[gi]) {
                     y[gi] = attn_combine_first4(a.part_o, a.part_ml, hs[gi], ns, dd[gi], a.hd, fb[gi]);
                     am = fmaxf(am, fmaxf(fmaxf(fabsf(y[gi].x), fabsf(y[gi].y)), fmaxf(fabsf(y[gi].z), fabsf(y[gi].w))));
                 }
@@ -1268,6 +1285,8 @@ hipError_t launch_gemv_i8_merge(hipStream_t s, const float* part_o, const float*
     // q|k|v and norm + gate|up launches made the step 0.859 ms (no gain),
     // and on the configs[1] sweep they took the narrow shapes' cold time
     // 3.65 -> 3.53 us on average without moving the 16-launch graph.
+    const bool head32 = hd == 128 && kbytes == 2048 && splits <= ATTN_SB && std::getenv("BH_MERGE_HEAD32") == nullptr;
+    if (m == 1 && head32) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 5, 2, true, true>(s, a);
     if (m == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 5, 0, true, true>(s, a);
     return gv_go<1, OUT_F32, false, true, 4, 1, 8, 5>(s, a);
 }
