@@ -934,7 +934,10 @@ __global__ __launch_bounds__(RT) void attn_prefill_kernel(AttnArgs p, int rows_p
 // Merge the key chunks of every head of row r: M = max m_s,
 // L = sum l_s e^(m_s - M), ctx = sum o_s e^(m_s - M) / L; then quantize the
 // whole context row for the output projection (quant_pack semantics).
-template <int GQ, int NT = RT>
+// H32: head_dim 128, one group per thread (2048 context elements on 512
+// threads) and at most ATTN_SB chunks: attn_combine_head32, the chunk
+// statistics one per lane and each chunk weight evaluated once.
+template <int GQ, int NT = RT, bool H32 = false>
 __global__ __launch_bounds__(NT) void attn_combine_quant_kernel(const float* part_o, const float* part_ml,
                                                                 const uint32_t* pos, int nh, int hd, int hq,
                                                                 int splits, float* sx, uint32_t* xq) {
@@ -955,7 +958,16 @@ __global__ __launch_bounds__(NT) void attn_combine_quant_kernel(const float* par
         hs = ((size_t)r * nh + h) * splits;
         return i < q4;
     };
-    if constexpr (PRE == GQ) {
+    if constexpr (H32) {
+        static_assert(GQ == 1, "one group per thread");
+        size_t hs;
+        int d;
+        (void)group(0, hs, d);
+        attn_load_first4_o(part_o, hs, splits, d, hd, fb[0]);
+        const float2 mlq = reinterpret_cast<const float2*>(part_ml)[hs + min((int)(threadIdx.x & 31), splits - 1)];
+        const int ns = ((int)pos[r] + ATTN_KCH) / ATTN_KCH;
+        y[0] = attn_combine_head32(mlq, ns, fb[0]);
+    } else if constexpr (PRE == GQ) {
         size_t hs[GQ];
         int dd[GQ];
         bool live[GQ];
@@ -1297,6 +1309,8 @@ int launch_combine_quant(bh_qwen3* e, int rows, int splits) {
     const int nh = (int)e->c.n_heads, hd = (int)e->c.head_dim;
     const uint32_t* pos = e->cur_pos;
     if (groups <= 1) attn_combine_quant_kernel<1><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, pos, nh, hd, hq, splits, e->sx, e->xq);
+    else if (groups <= 2 && hd == 128 && hq == 4 * 2 * RT && splits <= ATTN_SB)
+        attn_combine_quant_kernel<1, 2 * RT, true><<<rows, 2 * RT, 0, e->stream>>>(e->part_o, e->part_ml, pos, nh, hd, hq, splits, e->sx, e->xq);
     else if (groups <= 2) attn_combine_quant_kernel<1, 2 * RT><<<rows, 2 * RT, 0, e->stream>>>(e->part_o, e->part_ml, pos, nh, hd, hq, splits, e->sx, e->xq);
     else if (groups <= 4) attn_combine_quant_kernel<4><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, pos, nh, hd, hq, splits, e->sx, e->xq);
     else attn_combine_quant_kernel<8><<<rows, RT, 0, e->stream>>>(e->part_o, e->part_ml, pos, nh, hd, hq, splits, e->sx, e->xq);
