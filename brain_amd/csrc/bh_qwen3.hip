@@ -496,7 +496,10 @@ __device__ __forceinline__ float4 i8x4(uint32_t w) {
 // pos (the new key) also rotates the new key, appends key and value to the
 // cache, and takes them from LDS instead of reading the cache back. Same
 // arithmetic, in the same order, as the separate kernels.
-template <bool KV8, bool ROPE = false>
+// HDT, GT (decode): head_dim and query heads per kv head fixed at compile
+// time (0: read from the arguments), so the per-lane loops cover exactly the
+// head's pieces and the group's heads.
+template <bool KV8, bool ROPE = false, int HDT = 0, int GT = 0>
 __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     __shared__ float es[MAX_GROUP * KCH];
     __shared__ float ml[MAX_GROUP * 2];
@@ -512,20 +515,22 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     // needs no load there; elsewhere its load goes out with the position's.
     const size_t sq = ROPE ? (size_t)r : (size_t)p.seq[r];
     const int j0 = sp * KCH;
-    const int G = p.nh / p.nkv;
+    const int G = GT ? GT : p.nh / p.nkv;
+    const int hd = HDT ? HDT : p.hd;
+    constexpr int MG = GT ? GT : MAX_GROUP;
     float* qs = attn_dyn;
-    float* nk = qs + G * p.hd;
-    float* nv = nk + p.hd;
-    float* vls = nv + p.hd;
+    float* nk = qs + G * hd;
+    float* nv = nk + hd;
+    float* vls = nv + hd;
     const size_t tok0 = p.ro.map.slot(sq, j0);  // cache slot of this chunk's first key
-    const size_t cb = tok0 * p.hkv + (size_t)kh * p.hd;  // element of this chunk's first key, this head
+    const size_t cb = tok0 * p.hkv + (size_t)kh * hd;  // element of this chunk's first key, this head
 
     // Every cache read of the chunk is issued first, so its latency overlaps
     // the query rotation: this lane's K pieces (8 lanes per key, float4
     // along head_dim, at most 8 pieces for head_dim <= 256), the V rows
     // (4 elements per piece) and the KV8 scales, for the first `lim` keys.
     const int kk = tid >> 3, l8 = tid & 7;
-    constexpr int KP = 256 / 32;
+    constexpr int KP = (HDT ? HDT : 256) / 32;
     float4 kv[KP];
     uint32_t k8[KV8 ? KP : 1];
     // V is staged into LDS on the decode path only (prefill launches
@@ -536,8 +541,8 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     // consecutive pieces. Completion is awaited with an explicit vmcnt wait
     // before the barrier that publishes vls.
     constexpr bool VST = ROPE;
-    constexpr int VPT = VST ? KCH * 256 / 4 / RT : 0;
-    const int hd4 = p.hd >> 2;
+    constexpr int VPT = VST ? KCH * (HDT ? HDT : 256) / 4 / RT : 0;
+    const int hd4 = hd >> 2;
     const size_t vbo = cb;
     const uint32_t vls_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)vls;
     float scl = 0.0f;  // KV8: ksc[tid] (tid < KCH) or vsc[tid - KCH]
@@ -551,7 +556,7 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
 #pragma unroll
         for (int u = 0; u < KP; ++u) {
             // Pieces past head_dim repeat its last piece (masked below).
-            const int c = min(l8 * 4 + 32 * u, p.hd - 4);
+            const int c = min(l8 * 4 + 32 * u, hd - 4);
             if constexpr (KV8) k8[u] = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.kc) + kro + c);
             else kv[u] = *reinterpret_cast<const float4*>(static_cast<const float*>(p.kc) + kro + c);
         }
@@ -604,8 +609,8 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
             const uint32_t pos = pos_r;
             const float* row = ro.qkv + (size_t)r * (ro.hq + 2 * ro.hkv);
             const int h = min(wave, G + 1);
-            const float* src = h < G ? row + (size_t)(kh * G + h) * p.hd
-                                     : row + ro.hq + (h == G ? 0 : ro.hkv) + kh * p.hd;
+            const float* src = h < G ? row + (size_t)(kh * G + h) * hd
+                                     : row + ro.hq + (h == G ? 0 : ro.hkv) + kh * hd;
             rope_load(ro, src, h < G ? ro.qn : ro.kn, h <= G, pos, lane, rin);
         }
         load_chunk(min(KCH, p.max_seq - j0));
@@ -626,7 +631,7 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     const int nc = last ? n - 1 : n;        // keys read from the cache
     if constexpr (!ROPE) load_chunk(nc);
     if constexpr (ROPE) {
-        const int wave = tid >> 6, lane = tid & 63, half = p.hd >> 1;
+        const int wave = tid >> 6, lane = tid & 63, half = hd >> 1;
         const RopeArgs& ro = p.ro;
         const uint32_t pos = pos_r;
         const float* row = ro.qkv + (size_t)r * (ro.hq + 2 * ro.hkv);
@@ -636,12 +641,12 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
             float* dst;
             if (h < G) {
                 if (one_head) rope_apply(ro, true, lane, rin, y0, y1);
-                else rope_head(ro, row + (size_t)(kh * G + h) * p.hd, ro.qn, true, pos, lane, y0, y1);
-                dst = qs + h * p.hd;
+                else rope_head(ro, row + (size_t)(kh * G + h) * hd, ro.qn, true, pos, lane, y0, y1);
+                dst = qs + h * hd;
             } else {
                 const bool is_k = h == G;
                 if (one_head) rope_apply(ro, is_k, lane, rin, y0, y1);
-                else rope_head(ro, row + ro.hq + (is_k ? 0 : ro.hkv) + kh * p.hd, ro.kn, is_k, pos, lane, y0, y1);
+                else rope_head(ro, row + ro.hq + (is_k ? 0 : ro.hkv) + kh * hd, ro.kn, is_k, pos, lane, y0, y1);
                 const float sc = kv_append<KV8>(ro, is_k, kh, ro.map.slot(sq, (int)pos), lane, y0, y1);
                 dst = is_k ? nk : nv;
                 if (lane == 0) newsc[is_k ? 0 : 1] = sc;
@@ -655,7 +660,7 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
             }
         }
     } else {
-        for (int i = tid; i < G * p.hd; i += RT) qs[i] = p.q[(size_t)r * p.hq + (size_t)kh * G * p.hd + i];
+        for (int i = tid; i < G * hd; i += RT) qs[i] = p.q[(size_t)r * p.hq + (size_t)kh * G * hd + i];
     }
     // The V staging loads (and every other load of this wave) have landed.
     if constexpr (VST) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -670,33 +675,33 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     for (int u = 0; u < KP; ++u) {
         const int c = l8 * 4 + 32 * u;
         if constexpr (KV8) kv[u] = i8x4(k8[u]);
-        if (kk >= nc || c >= p.hd) kv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (kk >= nc || c >= hd) kv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     if (last && kk == n - 1) {
 #pragma unroll
         for (int u = 0; u < KP; ++u) {
             const int c = l8 * 4 + 32 * u;
-            if (c < p.hd) kv[u] = *reinterpret_cast<const float4*>(nk + c);
+            if (c < hd) kv[u] = *reinterpret_cast<const float4*>(nk + c);
         }
     }
     if constexpr (KV8) __syncthreads();  // ksc, vsc
     {
-        float acc[MAX_GROUP];
+        float acc[MG];
 #pragma unroll
-        for (int g = 0; g < MAX_GROUP; ++g) acc[g] = 0.0f;
+        for (int g = 0; g < MG; ++g) acc[g] = 0.0f;
 #pragma unroll
         for (int u = 0; u < KP; ++u) {
             const int c = l8 * 4 + 32 * u;
-            if (c >= p.hd) break;
+            if (c >= hd) break;
 #pragma unroll
-            for (int g = 0; g < MAX_GROUP; ++g) {
+            for (int g = 0; g < MG; ++g) {
                 if (g >= G) break;
-                const float4 qv = *reinterpret_cast<const float4*>(qs + g * p.hd + c);
+                const float4 qv = *reinterpret_cast<const float4*>(qs + g * hd + c);
                 acc[g] += qv.x * kv[u].x + qv.y * kv[u].y + qv.z * kv[u].z + qv.w * kv[u].w;
             }
         }
 #pragma unroll
-        for (int g = 0; g < MAX_GROUP; ++g) {
+        for (int g = 0; g < MG; ++g) {
             if (g >= G) break;
             float v = acc[g];
             v += xor_lane<4>(v);
@@ -725,11 +730,11 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
         }
     }
     __syncthreads();
-    for (int i = tid; i < G * p.hd; i += RT) {
-        const int g = i / p.hd, d = i - g * p.hd;
+    for (int i = tid; i < G * hd; i += RT) {
+        const int g = i / hd, d = i - g * hd;
         float acc = 0.0f;
         // Cache rows from LDS (VST) or straight from the cache, same order.
-        const size_t vstride = VST ? (size_t)p.hd : (size_t)p.hkv;
+        const size_t vstride = VST ? (size_t)hd : (size_t)p.hkv;
         if constexpr (KV8) {
             const int8_t* vb = VST ? reinterpret_cast<const int8_t*>(vls) : reinterpret_cast<const int8_t*>(p.vc) + vbo;
 #pragma unroll 8
@@ -742,7 +747,7 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
             if (last) acc += es[g * KCH + nc] * nv[d];
         }
         const size_t slot = ((size_t)r * p.nh + kh * G + g) * p.splits + sp;
-        p.part_o[slot * p.hd + d] = acc;
+        p.part_o[slot * hd + d] = acc;
         if (d == 0) {
             p.part_ml[2 * slot] = ml[2 * g];
             p.part_ml[2 * slot + 1] = ml[2 * g + 1];
@@ -1419,7 +1424,10 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
         if (decode && !e->nofuse) {
             // One new token per row, each row its own sequence: the rotation
             // and cache append run inside the attention launch.
-            if (c.kv_int8) attn_split_kernel<true, true><<<agrid, RT, alds, e->stream>>>(aa);
+            const bool fixed = hd == 128 && nh == 2 * nkv;
+            if (c.kv_int8 && fixed) attn_split_kernel<true, true, 128, 2><<<agrid, RT, alds, e->stream>>>(aa);
+            else if (c.kv_int8) attn_split_kernel<true, true><<<agrid, RT, alds, e->stream>>>(aa);
+            else if (fixed) attn_split_kernel<false, true, 128, 2><<<agrid, RT, alds, e->stream>>>(aa);
             else attn_split_kernel<false, true><<<agrid, RT, alds, e->stream>>>(aa);
             BH_HIP(hipGetLastError(), "attention launch");
         } else {
