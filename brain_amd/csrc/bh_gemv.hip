@@ -106,7 +106,7 @@ struct GemvArgs {
 // then rows 8-15), put into the MFMA's layout by a row_ror:8 exchange, as
 // the streaming kernel does. Needs ALIGNED, K % 128 == 0 and an even U.
 template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int KSPLIT, int XMODE, int U, int CG, int NW = GV_WAVES,
-          int PRE = 0, bool NTW = false, bool LINES = false, bool ONE = false, int KBT = 0>
+          int PRE = 0, bool NTW = false, bool LINES = false, int MF = 0, int KBT = 0>
 __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
     static_assert(!LINES || (ALIGNED && U % 2 == 0 && XMODE != 4), "whole-line loads: aligned, pairs of chunks");
     constexpr bool XLDS = XMODE != 0;
@@ -119,10 +119,11 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
     const int wave = threadIdx.x >> 6;
     const int slot = wave / KSPLIT;   // which column group of this workgroup
     const int ks = wave % KSPLIT;     // which K slice
-    // ONE, KBT (the decoder's one-row launches): one row and K = KBT bytes
-    // fixed at compile time, so the row loops and the K batches fold away
-    // and the launch runs (and fetches) only the code of its own shape.
-    const int m = ONE ? 1 : a.m, n = a.n;
+    // MF, KBT (the decoder's and the decode sweep's launches): MF rows and
+    // K = KBT bytes fixed at compile time, so the row loops and the K
+    // batches fold away and the launch runs (and fetches) only the code of
+    // its own shape (0: read from the arguments).
+    const int m = MF ? MF : a.m, n = a.n;
     const int kbytes = KBT ? KBT : a.kg * 4;
     const int nchunks = (kbytes + 63) >> 6;
     const int ngroups = (n + 15) >> 4;
@@ -1026,15 +1027,15 @@ static int gv_cfg() {
 }
 
 template <int MT, int OUT, bool HAS_BIAS, bool ALIGNED, int U, int CG, int KSPLIT = 4, int XMODE = 0, int PRE = 0,
-          bool NTW = false, bool LINES = false, bool ONE = false, int KBT = 0>
+          bool NTW = false, bool LINES = false, int MF = 0, int KBT = 0>
 static hipError_t gv_go(hipStream_t s, const GemvArgs& a) {
     constexpr int NW = KSPLIT > GV_WAVES ? KSPLIT : GV_WAVES;  // waves per workgroup
     constexpr int per_wg = (NW / KSPLIT) * CG;
     const int ngroups = (a.n + 15) / 16;
     const int grid = (ngroups + per_wg - 1) / per_wg;
     const size_t lds = XMODE ? (size_t)MT * 16 * (a.kg * 4 + 16) + MT * 16 * 4 : 0;
-    if ((ONE && a.m != 1) || (KBT && a.kg * 4 != KBT)) return hipErrorInvalidValue;
-    gemv_i8_kernel<MT, OUT, HAS_BIAS, ALIGNED, KSPLIT, XMODE, U, CG, NW, PRE, NTW, LINES, ONE, KBT><<<grid, NW * 64, lds, s>>>(a);
+    if ((MF && a.m != MF) || (KBT && a.kg * 4 != KBT)) return hipErrorInvalidValue;
+    gemv_i8_kernel<MT, OUT, HAS_BIAS, ALIGNED, KSPLIT, XMODE, U, CG, NW, PRE, NTW, LINES, MF, KBT><<<grid, NW * 64, lds, s>>>(a);
     return hipGetLastError();
 }
 
@@ -1242,7 +1243,7 @@ hipError_t launch_gemv_i8_pre(hipStream_t s, int mode, const uint32_t* pre_tok, 
     if (mode == 3 && kbytes == 1024) {
         // One row: K split 4 ways (4 waves of 4 chunks) rather than 8 (8 of 2):
         // batch-1 step 0.8495 -> 0.842 ms.
-        if (m == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 4, 3, 8 + 1, true, false, true, 1024>(s, a);
+        if (m == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 4, 3, 8 + 1, true, false, 1, 1024>(s, a);
         if (rpt == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 8 + 1>(s, a);
         if (rpt == 2) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 16 + 1>(s, a);
         return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 32 + 1>(s, a);
@@ -1253,7 +1254,7 @@ hipError_t launch_gemv_i8_pre(hipStream_t s, int mode, const uint32_t* pre_tok, 
         // 0.8495 -> 0.831 ms, with the one-row norm change above 0.819 (same
         // box; 12 waves of 4 chunks 0.849, 4 of 12 0.858, two column groups
         // per wave 0.887).
-        if (m == 1) return gv_go<1, OUT_F32, false, true, 6, 1, 8, 4, 8 + 3, true, false, true, 3072>(s, a);
+        if (m == 1) return gv_go<1, OUT_F32, false, true, 6, 1, 8, 4, 8 + 3, true, false, 1, 3072>(s, a);
         if (rpt == 1) return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 8 + 3>(s, a);
         if (rpt == 2) return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 16 + 3>(s, a);
         return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 32 + 3>(s, a);
@@ -1290,7 +1291,7 @@ hipError_t launch_gemv_i8_merge(hipStream_t s, const float* part_o, const float*
     // and on the configs[1] sweep they took the narrow shapes' cold time
     // 3.65 -> 3.53 us on average without moving the 16-launch graph.
     const bool head32 = hd == 128 && kbytes == 2048 && splits <= ATTN_SB && std::getenv("BH_MERGE_HEAD32") == nullptr;
-    if (m == 1 && head32) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 5, 2, true, true, true, 2048>(s, a);
+    if (m == 1 && head32) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 5, 2, true, true, 1, 2048>(s, a);
     if (m == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 5, 0, true, true>(s, a);
     return gv_go<1, OUT_F32, false, true, 4, 1, 8, 5>(s, a);
 }
