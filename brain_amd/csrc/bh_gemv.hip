@@ -1244,6 +1244,7 @@ hipError_t launch_gemv_i8_pre(hipStream_t s, int mode, const uint32_t* pre_tok, 
         // One row: K split 4 ways (4 waves of 4 chunks) rather than 8 (8 of 2):
         // batch-1 step 0.8495 -> 0.842 ms.
         if (m == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 4, 3, 8 + 1, true, false, 1, 1024>(s, a);
+        if (m == 4) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 16 + 1, false, false, 4, 1024>(s, a);
         if (rpt == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 8 + 1>(s, a);
         if (rpt == 2) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 16 + 1>(s, a);
         return gv_go<1, OUT_F32, false, true, 4, 1, 8, 3, 32 + 1>(s, a);
@@ -1255,6 +1256,7 @@ hipError_t launch_gemv_i8_pre(hipStream_t s, int mode, const uint32_t* pre_tok, 
         // box; 12 waves of 4 chunks 0.849, 4 of 12 0.858, two column groups
         // per wave 0.887).
         if (m == 1) return gv_go<1, OUT_F32, false, true, 6, 1, 8, 4, 8 + 3, true, false, 1, 3072>(s, a);
+        if (m == 4) return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 8 + 3, false, false, 4, 3072>(s, a);
         if (rpt == 1) return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 8 + 3>(s, a);
         if (rpt == 2) return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 16 + 3>(s, a);
         return gv_go<1, OUT_F32, false, true, 3, 1, 16, 4, 32 + 3>(s, a);

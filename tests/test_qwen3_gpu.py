@@ -344,11 +344,12 @@ def test_fused_decode_is_bit_identical_to_unfused(gpu, batch, kv_int8):
     b.close()
 
 
-@pytest.mark.parametrize("batch", [1, 2, 8])
+@pytest.mark.parametrize("batch", [1, 2, 4, 8])
 def test_qwen3_0_6b_fused_decode_matches_unfused(gpu, batch):
     """The fused decode kernels at the config-3 shapes (head_dim 128, a
     2048-wide merge on 512 threads, 16 waves per GEMV workgroup; batch 1 takes
-    the one-row SwiGLU prologue, batch 8 the separate producers on 1024-thread
+    the one-row prologues and batch 4 the four-row ones, both compiled for
+    their row count and K; batch 8 the separate producers on 1024-thread
     SwiGLU rows) against the separate ones."""
     prompts = np.random.default_rng(5).integers(0, QWEN3_0_6B["vocab"], size=(batch, 40))
     out = []
