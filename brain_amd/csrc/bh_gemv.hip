@@ -191,12 +191,15 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
     // 5.32 at 1 row; the same order made the norm (5.45 -> 5.64 us) and the
     // merge (7.46 -> 8.15 us) slower, their chains being shorter than the
     // head start the weights lose behind the inputs' load instructions.
+    // INFIRST: the prologue's input loads go out first, then the weights
+    // (the SwiGLU launches, and the one-row norm launch).
+    constexpr bool INFIRST = XMODE == 4 || (XMODE == 3 && MF == 1);
     auto issue_w = [&]() {
-        if constexpr (XMODE != 4 && LINES) {
+        if constexpr (!INFIRST && LINES) {
 #pragma unroll
             for (int u = 0; u < U; u += 2)
                 if (u < my_chunks) load_pair(u, ks + KSPLIT * (u >> 1));
-        } else if constexpr (XMODE != 4) {
+        } else if constexpr (!INFIRST) {
 #pragma unroll
             for (int u = 0; u < U; ++u)
                 if (u < my_chunks)
@@ -225,7 +228,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    if constexpr (XMODE != 4) issue_w();
+    if constexpr (!INFIRST) issue_w();
 
     float* sxs = reinterpret_cast<float*>(xs + MT * 16 * xstride);  // XMODE 2-4: row scales
     if constexpr (XMODE == 3 || XMODE == 4) {
@@ -348,6 +351,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
                             v[j][g] = reinterpret_cast<const float4*>(sa[j])[ic];
                             bv[j][g] = reinterpret_cast<const float4*>(sb[j])[ic];
                         }
+                    if constexpr (INFIRST)
+                        if (r0 == 0) issue_w();
                     if (a.pre_b && !a.pre_tok) {
 #pragma unroll
                         for (int j = 0; j < RMAX; ++j)
