@@ -188,11 +188,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
     // while the weights are in flight: vmcnt completes in order, so waiting
     // for inputs issued after the weights waits for the weights too.
     // Measured per launch: SwiGLU + down 8.56 -> 7.39 us at 4 rows, 5.44 ->
-    // 5.32 at 1 row; the same order made the norm (5.45 -> 5.64 us) and the
-    // merge (7.46 -> 8.15 us) slower, their chains being shorter than the
-    // head start the weights lose behind the inputs' load instructions.
-    // INFIRST: the prologue's input loads go out first, then the weights
-    // (the SwiGLU launches, and the one-row norm launch).
+    // 5.32 at 1 row. The one-row norm launch takes the same order (batch-1
+    // step 0.684 -> 0.644 ms, once its row loads had no branch join in front
+    // of them); the four-row norm launch measured slower with it (batch 4
+    // 0.940 -> 0.946 ms) and the one-row merge unchanged (0.6426 ms), so
+    // they keep the weights first.
+    // INFIRST: the prologue's input loads go out first, then the weights.
     constexpr bool INFIRST = XMODE == 4 || (XMODE == 3 && MF == 1);
     auto issue_w = [&]() {
         if constexpr (!INFIRST && LINES) {
