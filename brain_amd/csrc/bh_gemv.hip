@@ -1298,7 +1298,9 @@ hipError_t launch_gemv_i8_merge(hipStream_t s, const float* part_o, const float*
     // q|k|v and norm + gate|up launches made the step 0.859 ms (no gain),
     // and on the configs[1] sweep they took the narrow shapes' cold time
     // 3.65 -> 3.53 us on average without moving the 16-launch graph.
-    const bool head32 = hd == 128 && kbytes == 2048 && splits <= ATTN_SB && std::getenv("BH_MERGE_HEAD32") == nullptr;
+    // BH_MERGE_HEAD32 (any value) keeps the general merge, for measurement.
+    static const bool head32_on = std::getenv("BH_MERGE_HEAD32") == nullptr;
+    const bool head32 = hd == 128 && kbytes == 2048 && splits <= ATTN_SB && head32_on;
     if (m == 1 && head32) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 5, 2, true, true, 1, 2048>(s, a);
     if (m == 1) return gv_go<1, OUT_F32, false, true, 4, 1, 8, 5, 0, true, true>(s, a);
     return gv_go<1, OUT_F32, false, true, 4, 1, 8, 5>(s, a);
