@@ -535,7 +535,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(GemvArgs a) {
                 const int e = (live[gi] ? i : 0) * 4, h = e / a.hd;
                 dd[gi] = e - h * a.hd;
                 hs[gi] = ((size_t)r * a.nh + h) * a.splits;
-                if constexpr (HEAD32) attn_load_first4_o(a.part_o, hs[gi], a.splits, dd[gi], a.hd, fb[gi]);
+                // HEAD32: only the row's live chunks (its position is read
+                // first; a uniform bound).
+                if constexpr (HEAD32) attn_load_first4_o(a.part_o, hs[gi], min(((int)a.pos[r] + ATTN_KCH) / ATTN_KCH, a.splits), dd[gi], a.hd, fb[gi]);
                 else attn_load_first4(a.part_o, a.part_ml, hs[gi], live[gi] ? a.splits : 0, dd[gi], a.hd, fb[gi]);
             }
             // HEAD32: lane q of each half-wave loads chunk q's (m, l).
