@@ -968,9 +968,10 @@ __global__ __launch_bounds__(NT) void attn_combine_quant_kernel(const float* par
         size_t hs;
         int d;
         (void)group(0, hs, d);
-        attn_load_first4_o(part_o, hs, splits, d, hd, fb[0]);
-        const float2 mlq = reinterpret_cast<const float2*>(part_ml)[hs + min((int)(threadIdx.x & 31), splits - 1)];
+        // Only the row's live chunks (its position is read first).
         const int ns = ((int)pos[r] + ATTN_KCH) / ATTN_KCH;
+        attn_load_first4_o(part_o, hs, min(ns, splits), d, hd, fb[0]);
+        const float2 mlq = reinterpret_cast<const float2*>(part_ml)[hs + min((int)(threadIdx.x & 31), splits - 1)];
         y[0] = attn_combine_head32(mlq, ns, fb[0]);
     } else if constexpr (PRE == GQ) {
         size_t hs[GQ];
