@@ -499,7 +499,10 @@ __device__ __forceinline__ float4 i8x4(uint32_t w) {
 // HDT, GT (decode): head_dim and query heads per kv head fixed at compile
 // time (0: read from the arguments), so the per-lane loops cover exactly the
 // head's pieces and the group's heads.
-template <bool KV8, bool ROPE = false, int HDT = 0, int GT = 0>
+// PF (decode at many rows, where the cache reads bound the launch): the
+// row's position is read first, and a workgroup whose chunk lies past the
+// row exits before it reads any of the cache.
+template <bool KV8, bool ROPE = false, int HDT = 0, int GT = 0, bool PF = false>
 __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     __shared__ float es[MAX_GROUP * KCH];
     __shared__ float ml[MAX_GROUP * 2];
@@ -603,6 +606,8 @@ __global__ __launch_bounds__(RT) void attn_split_kernel(AttnArgs p) {
     uint32_t pos_r = 0;
     if constexpr (ROPE) {
         pos_r = p.pos[r];
+        if constexpr (PF)
+            if (j0 >= (int)pos_r + 1) return;
         if (one_head) {
             const int wave = tid >> 6, lane = tid & 63;
             const RopeArgs& ro = p.ro;
@@ -1345,6 +1350,12 @@ int fuse_norm_rows() {
     static const int v = env_rows("BH_QWEN3_FUSE_ROWS", 4);
     return v;
 }
+// Decode rows from which the attention reads the position before the cache
+// (BH_ATTN_POSFIRST_ROWS overrides).
+static int attn_posfirst_rows() {
+    static const int v = env_rows("BH_ATTN_POSFIRST_ROWS", 8);
+    return v;
+}
 int fuse_swiglu_rows() {
     static const int v = env_rows("BH_QWEN3_FUSE_SWIGLU_ROWS", 4);
     return v;
@@ -1426,8 +1437,11 @@ int run_rows(bh_qwen3* e, int rows, const uint32_t* tok, const uint32_t* pos, co
             // One new token per row, each row its own sequence: the rotation
             // and cache append run inside the attention launch.
             const bool fixed = hd == 128 && nh == 2 * nkv;
-            if (c.kv_int8 && fixed) attn_split_kernel<true, true, 128, 2><<<agrid, RT, alds, e->stream>>>(aa);
+            const bool pf = rows >= attn_posfirst_rows();
+            if (c.kv_int8 && fixed && pf) attn_split_kernel<true, true, 128, 2, true><<<agrid, RT, alds, e->stream>>>(aa);
+            else if (c.kv_int8 && fixed) attn_split_kernel<true, true, 128, 2><<<agrid, RT, alds, e->stream>>>(aa);
             else if (c.kv_int8) attn_split_kernel<true, true><<<agrid, RT, alds, e->stream>>>(aa);
+            else if (fixed && pf) attn_split_kernel<false, true, 128, 2, true><<<agrid, RT, alds, e->stream>>>(aa);
             else if (fixed) attn_split_kernel<false, true, 128, 2><<<agrid, RT, alds, e->stream>>>(aa);
             else attn_split_kernel<false, true><<<agrid, RT, alds, e->stream>>>(aa);
             BH_HIP(hipGetLastError(), "attention launch");
