@@ -344,17 +344,18 @@ def test_fused_decode_is_bit_identical_to_unfused(gpu, batch, kv_int8):
     b.close()
 
 
-@pytest.mark.parametrize("batch", [1, 2, 4, 8])
-def test_qwen3_0_6b_fused_decode_matches_unfused(gpu, batch):
+@pytest.mark.parametrize("batch,kv_int8", [(1, 0), (2, 0), (4, 0), (8, 0), (8, 1)])
+def test_qwen3_0_6b_fused_decode_matches_unfused(gpu, batch, kv_int8):
     """The fused decode kernels at the config-3 shapes (head_dim 128, a
     2048-wide merge on 512 threads, 16 waves per GEMV workgroup; batch 1 takes
     the one-row prologues and batch 4 the four-row ones, both compiled for
     their row count and K; batch 8 the separate producers on 1024-thread
-    SwiGLU rows) against the separate ones."""
+    SwiGLU rows; at 8 rows the attention reads the position before the
+    cache, with the f32 and the int8 cache) against the separate ones."""
     prompts = np.random.default_rng(5).integers(0, QWEN3_0_6B["vocab"], size=(batch, 40))
     out = []
     for unfused in (False, True):
-        e = Qwen3Engine(QWEN3_0_6B, batch, 64, max_rows=8 * 64)
+        e = Qwen3Engine(dict(QWEN3_0_6B, kv_int8=kv_int8), batch, 64, max_rows=8 * 64)
         e.init_random(11)
         out.append((e.generate(prompts, 6, eager=unfused, unfused=unfused), e.logits()))
         e.close()
