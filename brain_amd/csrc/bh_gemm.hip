@@ -925,7 +925,8 @@ enum TileCfg {
     TILE_256x128 = 5,  // 256x128, 8 waves of 64x64, 4 stages
     TILE_64_K128 = 6,     // 64x64, 8 stages of 128 K-bytes (what TILE_64_DEEP runs)
     TILE_64x128_K128 = 7,  // 64x128, 4 stages of 128 K-bytes (what TILE_64x128 runs)
-    TILE_256x128_K128 = 8  // 256x128, 3 stages of 128 K-bytes (what TILE_256x128 runs)
+    TILE_256x128_K128 = 8,  // 256x128, 3 stages of 128 K-bytes (what TILE_256x128 runs)
+    TILE_32x64 = 9          // 32x64, 2 waves of 32x32, 8 stages of 128 K-bytes
 };
 
 struct TileChoice {
@@ -945,6 +946,11 @@ static int tile_env() {
 }
 static int splitk_env() {
     static int v = env_int("BH_SPLITK", 0);
+    return v;
+}
+// BH_GEMM_T32=0: no 32x64 tiles (for measurement).
+static int t32x64_env() {
+    static int v = env_int("BH_GEMM_T32", 1);
     return v;
 }
 
@@ -1008,6 +1014,12 @@ static TileChoice choose_tiles(int m, int kg, int n) {
     else if (t128 >= CUS) tc.cfg = TILE_128;
     else if (t128 >= CUS / 2) tc.cfg = TILE_64x128;
     else tc.cfg = (t64 <= CUS && stages >= 32) ? TILE_64_DEEP : TILE_64;
+    // At most half the chip's worth of 64x64 tiles over a long K, where
+    // 32x64 tiles fill more than half of it (e.g. 512x3072x1024: 128 tiles
+    // of 64x64 on 48 K stages, 256 of 32x64), and no split-K.
+    const long t32 = (long)((m + 31) / 32) * ((n + 63) / 64);
+    if (tc.cfg == TILE_64_DEEP && t64 <= CUS / 2 && t32 > CUS / 2 && t32 <= CUS && t32x64_env())
+        tc.cfg = TILE_32x64;
     if (tile_env() >= 0) tc.cfg = tile_env();
     switch (tc.cfg) {
         case TILE_128: tc.splits = choose_splits(t128, 0.25, m, kg, n); break;
@@ -1103,6 +1115,7 @@ static hipError_t go_small(hipStream_t s, int cfg, const GemmArgs& a) {
         case TILE_64_K128: return go_dma<64, 64, 2, 2, 8, 128, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
         case TILE_64x128_K128: return go_dma<64, 128, 2, 2, 4, 128, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
         case TILE_256x128_K128: return go_dma<256, 128, 4, 2, 3, 128, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
+        case TILE_32x64: return go_dma<32, 64, 1, 2, 8, 128, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
         default: return go_dma<128, 128, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
     }
 }
