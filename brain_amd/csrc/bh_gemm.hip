@@ -332,7 +332,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_i8_kernel(GemmArgs a) {
 template <int DK>
 __device__ __forceinline__ int dswz(int r) {
     if constexpr (DK == 64) return (r >> 2) & 3;
-    else return (r >> 1) & 7;
+    else if constexpr (DK == 128) return (r >> 1) & 7;
+    else return r & 15;  // DK = 256: a row is one whole 256-byte bank line
 }
 template <int DK>
 __device__ __forceinline__ int dslot(int r, int c) { return r * DK + ((c ^ dswz<DK>(r)) << 4); }
@@ -926,7 +927,7 @@ enum TileCfg {
     TILE_64_K128 = 6,     // 64x64, 8 stages of 128 K-bytes (what TILE_64_DEEP runs)
     TILE_64x128_K128 = 7,  // 64x128, 4 stages of 128 K-bytes (what TILE_64x128 runs)
     TILE_256x128_K128 = 8,  // 256x128, 3 stages of 128 K-bytes (what TILE_256x128 runs)
-    TILE_32x64 = 9          // 32x64, 2 waves of 32x32, 8 stages of 128 K-bytes
+    TILE_32x64 = 9          // 32x64, 2 waves of 32x32, 4 stages of 256 K-bytes (8 of 128 if K % 256 != 0)
 };
 
 struct TileChoice {
@@ -1115,7 +1116,10 @@ static hipError_t go_small(hipStream_t s, int cfg, const GemmArgs& a) {
         case TILE_64_K128: return go_dma<64, 64, 2, 2, 8, 128, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
         case TILE_64x128_K128: return go_dma<64, 128, 2, 2, 4, 128, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
         case TILE_256x128_K128: return go_dma<256, 128, 4, 2, 3, 128, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
-        case TILE_32x64: return go_dma<32, 64, 1, 2, 8, 128, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
+        case TILE_32x64:
+            // 256-byte K stages (8 k-steps per barrier) where K allows.
+            if ((a.kg * 4) % 256 == 0) return go_dma<32, 64, 1, 2, 4, 256, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
+            return go_dma<32, 64, 1, 2, 8, 128, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
         default: return go_dma<128, 128, 2, 2, 4, 64, OUT, HAS_BIAS, STATIC, SPLITK>(s, a);
     }
 }
