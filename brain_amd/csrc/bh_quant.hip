@@ -337,6 +337,7 @@ hipError_t launch_quantize_rows_bf16(hipStream_t s, const uint16_t* x, int m, in
         if (k8 <= QT) quantize_rows_bf16_kernel<1><<<m, QT, 0, s>>>(x, m, k, sx, xq);
         else if (k8 <= 2 * QT) quantize_rows_bf16_kernel<2><<<m, QT, 0, s>>>(x, m, k, sx, xq);
         else if (k8 <= 4 * QT) quantize_rows_bf16_kernel<4><<<m, QT, 0, s>>>(x, m, k, sx, xq);
+        else if (k8 <= 5 * QT) quantize_rows_bf16_kernel<5><<<m, QT, 0, s>>>(x, m, k, sx, xq);  // K = 10240: no clamped repeats
         else quantize_rows_bf16_kernel<8><<<m, QT, 0, s>>>(x, m, k, sx, xq);
     } else {
         quantize_rows_bf16_any_kernel<<<m, QT, 0, s>>>(x, m, k, sx, xq);
