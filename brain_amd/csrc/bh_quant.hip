@@ -356,6 +356,7 @@ hipError_t launch_quantize_rows(hipStream_t s, const float* x, int m, int k, flo
     } else if (al16(x) && kg <= 4 * QT) {
         if (kg <= QT) quantize_rows_reg_kernel<1><<<m, QT, 0, s>>>(x, m, k, sx, xq);
         else if (kg <= 2 * QT) quantize_rows_reg_kernel<2><<<m, QT, 0, s>>>(x, m, k, sx, xq);
+        else if (kg <= 3 * QT) quantize_rows_reg_kernel<3><<<m, QT, 0, s>>>(x, m, k, sx, xq);  // K = 3072
         else quantize_rows_reg_kernel<4><<<m, QT, 0, s>>>(x, m, k, sx, xq);
     } else if (al16(x)) quantize_rows_kernel<true><<<m, QT, 0, s>>>(x, m, k, sx, xq);
     else quantize_rows_kernel<false><<<m, QT, 0, s>>>(x, m, k, sx, xq);
