@@ -155,6 +155,12 @@ __global__ __launch_bounds__(RT) void norm_quant_kernel(NormQuantArgs p) {
     const float4* src = p.tok ? reinterpret_cast<const float4*>(p.emb + (size_t)p.tok[ir] * p.d)
                               : reinterpret_cast<const float4*>(p.a + (size_t)ir * p.d);
     const float4* add = p.b ? reinterpret_cast<const float4*>(p.b + (size_t)ir * p.d) : nullptr;
+    // The gains go out first (unconditional, clamped), so they are not a
+    // second memory round trip after the sum's barriers.
+    const float4* w4 = reinterpret_cast<const float4*>(p.w);
+    float4 wv[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) wv[g] = w4[min((int)threadIdx.x + g * RT, d4 - 1)];
     float4 x[G];
     float ss = 0.0f;
 #pragma unroll
@@ -178,14 +184,12 @@ __global__ __launch_bounds__(RT) void norm_quant_kernel(NormQuantArgs p) {
     }
     ss = block_sum(ss, red);
     const float inv = 1.0f / sqrtf(ss / (float)p.d + p.eps);
-    const float4* w4 = reinterpret_cast<const float4*>(p.w);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         const int i = threadIdx.x + g * RT;
-        if (i < d4) {
-            const float4 wv = w4[i];
-            x[g] = make_float4(x[g].x * inv * wv.x, x[g].y * inv * wv.y, x[g].z * inv * wv.z, x[g].w * inv * wv.w);
-        }
+        if (i < d4)
+            x[g] = make_float4(x[g].x * inv * wv[g].x, x[g].y * inv * wv[g].y, x[g].z * inv * wv[g].z,
+                               x[g].w * inv * wv[g].w);
     }
     quant_row<G>(x, d4, red, p.sx + r, p.xq + (size_t)r * p.xq_words);
 }
