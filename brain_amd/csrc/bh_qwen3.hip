@@ -93,10 +93,11 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     for (int w = 1; w < RT / 64; ++w) s += red[w];
     return s;
 }
-template <int NT = RT>
+// LEAD = false: red has not been used before in this block (no leading barrier).
+template <int NT = RT, bool LEAD = true>
 __device__ __forceinline__ float block_max(float v, float* red) {
     v = wave_max(v);
-    __syncthreads();
+    if constexpr (LEAD) __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
     float s = red[0];
@@ -112,13 +113,13 @@ __device__ __forceinline__ float absmax4(float4 v) { return fmaxf(fmaxf(fabsf(v.
 // sx = max(max|y|, 1e-8)/127, q = clamp(rne(y * (1/sx))) as quant_pack.
 // NT: threads of the block (the row's max is exact in any order, so the
 // result does not depend on it).
-template <int G, int NT = RT>
+template <int G, int NT = RT, bool LEAD = true>
 __device__ __forceinline__ void quant_row(const float4 (&y)[G], int d4, float* red, float* sx, uint32_t* xq) {
     float am = 0.0f;
 #pragma unroll
     for (int g = 0; g < G; ++g)
         if (threadIdx.x + g * NT < d4) am = fmaxf(am, absmax4(y[g]));
-    am = block_max<NT>(am, red);
+    am = block_max<NT, LEAD>(am, red);
     const float s = fmaxf(am, 1e-8f) / 127.0f;
     const float inv = 1.0f / s;
 #pragma unroll
@@ -191,7 +192,8 @@ __global__ __launch_bounds__(RT) void norm_quant_kernel(NormQuantArgs p) {
             x[g] = make_float4(x[g].x * inv * wv[g].x, x[g].y * inv * wv[g].y, x[g].z * inv * wv[g].z,
                                x[g].w * inv * wv[g].w);
     }
-    quant_row<G>(x, d4, red, p.sx + r, p.xq + (size_t)r * p.xq_words);
+    __shared__ float red2[RT / 64];  // the max's own array: no barrier to retire the sum's
+    quant_row<G, RT, false>(x, d4, red2, p.sx + r, p.xq + (size_t)r * p.xq_words);
 }
 
 // silu_mul.wgsl (h = g / (1 + exp(-g)) * u) over the stacked gate|up output,
@@ -214,7 +216,7 @@ __global__ __launch_bounds__(NT) void swiglu_quant_kernel(const float* gu, int f
                                a.z / (1.0f + expf(-a.z)) * b.z, a.w / (1.0f + expf(-a.w)) * b.w);
         }
     }
-    quant_row<G, NT>(h, d4, red, sx + r, xq + (size_t)r * xq_words);
+    quant_row<G, NT, false>(h, d4, red, sx + r, xq + (size_t)r * xq_words);
 }
 
 // Where position `pos` of sequence `seq` lives in a layer's cache: the token
@@ -1006,7 +1008,7 @@ __global__ __launch_bounds__(NT) void attn_combine_quant_kernel(const float* par
             y[g] = live ? attn_combine_first4(part_o, part_ml, hs, ns, d, hd, fb[0]) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     }
-    quant_row<GQ, NT>(y, q4, red, sx + r, xq + (size_t)r * q4);
+    quant_row<GQ, NT, false>(y, q4, red, sx + r, xq + (size_t)r * q4);
 }
 
 // Greedy argmax, stage 1: chunk c of row b -> (value, index) with the
